@@ -1,0 +1,240 @@
+// The C ABI (include/flashrt_moe.h): argument checks, workspace carving, error strings.
+#include "common.hpp"
+
+#include "../../include/flashrt_moe.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+namespace frt {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+// route.hip
+int router_logits(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
+                  float* logits, float* gate, hipStream_t stream);
+int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xq16, hipStream_t stream);
+int route_topk(hipStream_t stream, const float* logits, int T, int E, int K, int32_t* ids, float* wts, uint32_t* counts,
+               uint32_t* tail_counts, int tail_from);
+// decode.hip
+size_t dec_scratch_bytes(int T, int K, int ff);
+int dec_moe(const float* logits, const float* gate, int T, int E, int K, const uint8_t* arena, size_t stride,
+            const uint8_t* shared_blob, const int8_t* xq, const float* xd, int n, int ff, int32_t* ids, float* wts,
+            uint32_t* counts, const float* resid, float* out, void* scratch, hipStream_t stream);
+int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const int8_t* xq, const float* xd, int n,
+             int ff, void* scratch, float* yh, hipStream_t stream, int T);
+int dec_check(int T, int K, int n, int ff);
+// prefill.hip
+size_t pf_workspace_bytes(int T, int K, int n, int ff, int E, bool shared, bool own_yd);
+int pf_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const float* x, const int32_t* ids, int T, int K,
+           void* yd, void* ws, size_t ws_bytes, hipStream_t stream, int block64, int yd_bf16);
+int pf_moe(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, int n, int ff, const float* x,
+           const int32_t* ids, const float* wts, const float* gate, int T, int K, const float* resid, float* out,
+           void* ws, size_t ws_bytes, hipStream_t stream);
+int pf_dispatch(const int32_t* ids, int T, int K, int E, int32_t* bounds, int32_t* tok_of, int32_t* slot_of, void* ws,
+                size_t ws_bytes, hipStream_t stream);
+size_t pf_dispatch_ws_bytes(int T, int K, int E);
+int pf_check(int T, int K, int n, int ff, int E);
+// gen.hip
+int gen_experts(uint64_t seed, int cfg, int layer, int e0, int count, int tensor_base, int n, int ff, float sd,
+                uint8_t* dst, size_t stride, hipStream_t stream);
+int gen_normal(uint64_t seed, int cfg, int layer, int tensor, float sd, float* dst, size_t count, int round_bf16,
+               hipStream_t stream);
+int gen_correlated(uint64_t seed, int cfg, int layer, int tensor0, int T, int n, float rho, float* dst,
+                   hipStream_t stream);
+void gen_zipf_bias(uint64_t seed, int cfg, int layer, int E, float s, float alpha, float* bias);
+
+constexpr int kDecodeMaxT = 4;
+
+// decode-side scratch for moe_hits: x quantized (T rows) ahead of dec scratch
+static size_t hits_bytes(int K, int ff, int T, int n) {
+    return up256(size_t(T) * n) + up256(size_t(T) * (n / kQ8) * 4) + dec_scratch_bytes(T, K, ff);
+}
+
+struct LayerWs {
+    float* logits;
+    float* gate;
+    int32_t* ids;
+    float* wts;
+    int8_t* xq;
+    float* xd;
+    void* rest;
+    size_t rest_bytes;
+    size_t bytes;
+};
+
+static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t total) {
+    LayerWs w{};
+    uint8_t* p = static_cast<uint8_t*>(base);
+    auto take = [&](size_t b) {
+        uint8_t* r = p;
+        p += up256(b);
+        return r;
+    };
+    const int E = L.n_expert, K = L.top_k, n = L.d_model, ff = L.d_ff;
+    w.logits = reinterpret_cast<float*>(take(size_t(T) * E * 4));
+    w.gate = reinterpret_cast<float*>(take(size_t(T) * 4));
+    w.ids = reinterpret_cast<int32_t*>(take(size_t(T) * K * 4));
+    w.wts = reinterpret_cast<float*>(take(size_t(T) * K * 4));
+    const bool dec = T <= kDecodeMaxT;
+    if (dec) {
+        w.xq = reinterpret_cast<int8_t*>(take(size_t(T) * n));
+        w.xd = reinterpret_cast<float*>(take(size_t(T) * (n / kQ8) * 4));
+        w.rest_bytes = dec_scratch_bytes(T, K, ff);
+    } else {
+        w.rest_bytes = pf_workspace_bytes(T, K, n, ff, E, true, true);
+    }
+    w.rest = take(w.rest_bytes);
+    w.bytes = size_t(p - static_cast<uint8_t*>(base));
+    (void)total;
+    return w;
+}
+
+}  // namespace frt
+
+using namespace frt;
+
+extern "C" {
+
+const char* frt_last_error(void) { return g_err; }
+const char* frt_version(void) { return "flashrt-mi355x 0.1 (gfx950)"; }
+
+size_t frt_q2_mat_bytes(int rows, int cols) { return mat_bytes(rows, cols); }
+size_t frt_q2_expert_bytes(int d_model, int d_ff) { return expert_bytes(d_model, d_ff); }
+
+int frt_arena_alloc(int n_layer, int n_expert, size_t blob_bytes, frt_arena* out) {
+    if (!out) return set_error(kErrNull, "arena_alloc: null out");
+    *out = frt_arena{};
+    if (n_layer < 1 || n_expert < 1 || blob_bytes == 0) return set_error(kErrShape, "arena_alloc: bad shape");
+    const size_t stride = (blob_bytes + 4095) & ~size_t(4095);
+    void* p = nullptr;
+    FRT_HIP(hipMalloc(&p, stride * size_t(n_layer) * size_t(n_expert)));
+    *out = frt_arena{static_cast<uint8_t*>(p), blob_bytes, stride, n_layer, n_expert};
+    return kOk;
+}
+
+int frt_arena_free(frt_arena* a) {
+    if (!a) return set_error(kErrNull, "arena_free: null");
+    if (a->base) FRT_HIP(hipFree(a->base));
+    *a = frt_arena{};
+    return kOk;
+}
+
+uint8_t* frt_arena_blob(const frt_arena* a, int layer, int expert) {
+    return a->base + (size_t(layer) * a->n_expert + expert) * a->stride;
+}
+size_t frt_arena_total_bytes(const frt_arena* a) { return size_t(a->n_layer) * a->n_expert * a->stride; }
+
+int frt_arena_upload(const frt_arena* a, int layer, int expert, const void* host_blob, void* stream) {
+    if (!a || !a->base || !host_blob) return set_error(kErrNull, "arena_upload: null");
+    if (layer < 0 || layer >= a->n_layer || expert < 0 || expert >= a->n_expert) return set_error(kErrShape, "arena_upload: index");
+    FRT_HIP(hipMemcpyAsync(frt_arena_blob(a, layer, expert), host_blob, a->blob_bytes, hipMemcpyHostToDevice,
+                           static_cast<hipStream_t>(stream)));
+    return kOk;
+}
+
+int frt_moe_route_topk(void* stream, const float* logits, int T, int E, int k, int32_t* ids, float* wts,
+                       uint32_t* counts, uint32_t* tail_counts, int tail_from) {
+    return route_topk(static_cast<hipStream_t>(stream), logits, T, E, k, ids, wts, counts, tail_counts, tail_from);
+}
+
+int frt_router_logits(void* stream, const float* x, int T, const float* W, const float* bias, const float* gate_w,
+                      int E, int n, float* logits, float* gate) {
+    return router_logits(x, T, W, bias, gate_w, E, n, logits, gate, static_cast<hipStream_t>(stream));
+}
+
+int frt_quantize_q8(void* stream, const float* x, int rows, int n, int8_t* xq, float* xd) {
+    if (!x || !xq || !xd) return set_error(kErrNull, "quantize_q8: null pointer");
+    return quantize_q8(x, rows, n, xq, xd, nullptr, static_cast<hipStream_t>(stream));
+}
+
+size_t frt_moe_dispatch_workspace_bytes(int T, int K, int E) { return pf_dispatch_ws_bytes(T, K, E); }
+int frt_moe_dispatch(void* stream, const int32_t* ids, int T, int K, int E, int32_t* bounds, int32_t* tok_of,
+                     int32_t* slot_of, void* ws, size_t ws_bytes) {
+    if (!ids || !bounds || !tok_of || !slot_of || !ws) return set_error(kErrNull, "dispatch: null pointer");
+    return pf_dispatch(ids, T, K, E, bounds, tok_of, slot_of, ws, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+size_t frt_moe_q2_workspace_bytes(int T, int K, int n, int ff, int E) {
+    return pf_workspace_bytes(T, K, n, ff, E, false, false);
+}
+int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const float* x, const int32_t* ids,
+                   int T, int K, void* yd, void* ws, size_t ws_bytes, void* stream, int block64, int yd_bf16) {
+    return pf_run(experts, stride, E, n, ff, x, ids, T, K, yd, ws, ws_bytes, static_cast<hipStream_t>(stream), block64,
+                  yd_bf16);
+}
+
+size_t frt_moe_hits_scratch_bytes(int K, int ff, int T, int n) { return hits_bytes(K, ff, T, n); }
+int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const float* x, int n, int ff,
+                 void* scratch, float* yh, void* stream, int T) {
+    if (!hit_ptr || !hit_n || !x || !scratch || !yh) return set_error(kErrNull, "moe_hits: null pointer");
+    if (int rc = dec_check(T, K, n, ff)) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint8_t* p = static_cast<uint8_t*>(scratch);
+    int8_t* xq = reinterpret_cast<int8_t*>(p);
+    p += up256(size_t(T) * n);
+    float* xd = reinterpret_cast<float*>(p);
+    p += up256(size_t(T) * (n / kQ8) * 4);
+    if (int rc = quantize_q8(x, T, n, xq, xd, nullptr, s)) return rc;
+    return dec_hits(hit_ptr, hit_n, K, xq, xd, n, ff, p, yh, s, T);
+}
+
+size_t frt_moe_layer_workspace_bytes(const frt_moe_layer* L, int T) {
+    if (!L || T < 1) return 0;
+    return layer_carve(nullptr, *L, T, 0).bytes + 256;
+}
+
+int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out, int32_t* ids,
+                          float* wts, uint32_t* counts, void* ws, size_t ws_bytes, void* stream) {
+    if (!L || !x || !out || !ws) return set_error(kErrNull, "moe_layer: null pointer");
+    if (!L->experts || !L->shared || !L->router_w || !L->gate_w) return set_error(kErrNull, "moe_layer: layer weights missing");
+    if (T < 1) return set_error(kErrShape, "moe_layer: T=%d", T);
+    const int E = L->n_expert, K = L->top_k, n = L->d_model, ff = L->d_ff;
+    if (E < 1 || E > 1024 || K < 1 || K > 32 || K > E) return set_error(kErrShape, "moe_layer: E=%d K=%d", E, K);
+    if (L->stride < expert_bytes(n, ff)) return set_error(kErrShape, "moe_layer: stride %zu < blob %zu", L->stride, expert_bytes(n, ff));
+    const LayerWs w = layer_carve(ws, *L, T, ws_bytes);
+    if (w.bytes > ws_bytes) return set_error(kErrWorkspace, "moe_layer: workspace %zu < %zu", ws_bytes, w.bytes);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int32_t* ids_o = ids ? ids : w.ids;
+    float* wts_o = wts ? wts : w.wts;
+    if (int rc = router_logits(x, T, L->router_w, L->router_bias, L->gate_w, E, n, w.logits, w.gate, s)) return rc;
+    if (T <= kDecodeMaxT) {
+        if (int rc = dec_check(T, K, n, ff)) return rc;
+        if (int rc = quantize_q8(x, T, n, w.xq, w.xd, nullptr, s)) return rc;
+        return dec_moe(w.logits, w.gate, T, E, K, L->experts, L->stride, L->shared, w.xq, w.xd, n, ff, ids_o, wts_o,
+                       counts, resid, out, w.rest, s);
+    }
+    if (int rc = pf_check(T, K, n, ff, E)) return rc;
+    if (int rc = route_topk(s, w.logits, T, E, K, ids_o, wts_o, counts, nullptr, 1 << 30)) return rc;
+    return pf_moe(L->experts, L->stride, E, L->shared, n, ff, x, ids_o, wts_o, w.gate, T, K, resid, out, w.rest,
+                  w.rest_bytes, s);
+}
+
+int frt_gen_experts(uint64_t seed, int cfg, int layer, int e0, int count, int tensor_base, int n, int ff, float sd,
+                    uint8_t* dst, size_t stride, void* stream) {
+    if (!dst) return set_error(kErrNull, "gen_experts: null");
+    return gen_experts(seed, cfg, layer, e0, count, tensor_base, n, ff, sd, dst, stride, static_cast<hipStream_t>(stream));
+}
+int frt_gen_normal(uint64_t seed, int cfg, int layer, int tensor, float sd, float* dst, size_t count, int round_bf16,
+                   void* stream) {
+    if (!dst) return set_error(kErrNull, "gen_normal: null");
+    return gen_normal(seed, cfg, layer, tensor, sd, dst, count, round_bf16, static_cast<hipStream_t>(stream));
+}
+int frt_gen_correlated(uint64_t seed, int cfg, int layer, int tensor0, int T, int n, float rho, float* dst, void* stream) {
+    if (!dst || T < 1) return set_error(kErrNull, "gen_correlated: null");
+    return gen_correlated(seed, cfg, layer, tensor0, T, n, rho, dst, static_cast<hipStream_t>(stream));
+}
+void frt_gen_zipf_bias(uint64_t seed, int cfg, int layer, int E, float s, float alpha, float* host_bias) {
+    gen_zipf_bias(seed, cfg, layer, E, s, alpha, host_bias);
+}
+
+}  // extern "C"

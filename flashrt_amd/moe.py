@@ -1,0 +1,220 @@
+"""Host-side mirror of the reference's MoE call surface, over the C ABI (include/flashrt_moe.h).
+
+Names, argument order and error behaviour follow the reference's C++ entry points:
+  ExpertArena / arena_alloc / arena_free      core/expert_arena.hpp:14-30
+  moe_route_topk                              arch/qwen4exp/blocks.hpp:130-135
+  moe_q2.workspace_bytes / moe_q2.run         kernels/cuda/moe_q2.h:20-30
+  moe_hits_scratch_bytes / moe_hits           arch/qwen4exp/moe_fast.hpp:134-142
+  MoeLayer.forward (moe_block_fast / moe_block_stream / moe_block on an HBM arena)
+                                              arch/qwen4exp/moe_fast.hpp:144-147, moe_stream.hpp:35,
+                                              blocks.hpp:286
+Device buffers are torch tensors on the GPU (or raw device addresses as ints); a call enqueues on
+the given stream (torch's current stream by default) and raises FrtError where the reference throws
+std::runtime_error.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from types import SimpleNamespace
+
+import torch
+
+from ._lib import FrtArena, FrtError, FrtMoeLayer, check, lib
+
+__all__ = ["FrtError", "ExpertArena", "arena_alloc", "arena_free", "moe_route_topk", "router_logits", "quantize_q8",
+           "moe_dispatch", "moe_q2", "moe_hits_scratch_bytes", "moe_hits", "MoeLayer", "expert_bytes", "gen"]
+
+
+def _p(t) -> int | None:
+    """Device address of a tensor (or an int address, or None)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if not t.is_cuda:
+        raise ValueError("flashrt_amd: expected a device tensor")
+    return t.data_ptr()
+
+
+def _s(stream) -> int | None:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def expert_bytes(d_model: int, d_ff: int) -> int:
+    """q2_0::expert_bytes (quant/q2_0/q2_0.hpp:51): gate | up | down planar Q2_0."""
+    return int(lib().frt_q2_expert_bytes(d_model, d_ff))
+
+
+# ---------------------------------------------------------------- arena
+
+class ExpertArena:
+    """HBM-resident expert arena: blob(l, e) = base + (l * n_expert + e) * stride, stride a
+    multiple of 4 KiB (core/expert_arena.hpp:14-30, on the device instead of host RAM)."""
+
+    def __init__(self, raw: FrtArena):
+        self._raw = raw
+
+    @property
+    def base(self) -> int:
+        return int(self._raw.base)
+
+    @property
+    def stride(self) -> int:
+        return int(self._raw.stride)
+
+    @property
+    def blob_bytes(self) -> int:
+        return int(self._raw.blob_bytes)
+
+    @property
+    def n_layer(self) -> int:
+        return int(self._raw.n_layer)
+
+    @property
+    def n_expert(self) -> int:
+        return int(self._raw.n_expert)
+
+    def blob(self, layer: int, expert: int) -> int:
+        return int(lib().frt_arena_blob(C.byref(self._raw), layer, expert))
+
+    def total_bytes(self) -> int:
+        return int(lib().frt_arena_total_bytes(C.byref(self._raw)))
+
+    def upload(self, layer: int, expert: int, host_blob, stream=None) -> None:
+        """Copies one host blob (bytes-like / numpy uint8) into (layer, expert)."""
+        import numpy as np
+        buf = np.ascontiguousarray(np.frombuffer(host_blob, np.uint8) if not isinstance(host_blob, np.ndarray)
+                                   else host_blob.view(np.uint8))
+        check(lib().frt_arena_upload(C.byref(self._raw), layer, expert, buf.ctypes.data, _s(stream)))
+        torch.cuda.current_stream().synchronize() if stream is None else stream.synchronize()
+
+    def free(self) -> None:
+        if self._raw.base:
+            check(lib().frt_arena_free(C.byref(self._raw)))
+
+
+def arena_alloc(n_layer: int, n_expert: int, blob_bytes: int) -> ExpertArena:
+    raw = FrtArena()
+    check(lib().frt_arena_alloc(n_layer, n_expert, blob_bytes, C.byref(raw)))
+    return ExpertArena(raw)
+
+
+def arena_free(a: ExpertArena) -> None:
+    a.free()
+
+
+# ---------------------------------------------------------------- routing and quantization
+
+def moe_route_topk(stream, logits, T: int, E: int, k: int, ids, wts, counts=None, tail_counts=None,
+                   tail_from: int = 1 << 30) -> None:
+    check(lib().frt_moe_route_topk(_s(stream), _p(logits), T, E, k, _p(ids), _p(wts), _p(counts), _p(tail_counts),
+                                   tail_from))
+
+
+def router_logits(x, T: int, W, E: int, n: int, logits, bias=None, gate_w=None, gate=None, stream=None) -> None:
+    check(lib().frt_router_logits(_s(stream), _p(x), T, _p(W), _p(bias), _p(gate_w), E, n, _p(logits), _p(gate)))
+
+
+def quantize_q8(x, rows: int, n: int, xq, xd, stream=None) -> None:
+    check(lib().frt_quantize_q8(_s(stream), _p(x), rows, n, _p(xq), _p(xd)))
+
+
+def moe_dispatch(ids, T: int, K: int, E: int, bounds, tok_of, slot_of, stream=None):
+    nbytes = int(lib().frt_moe_dispatch_workspace_bytes(T, K, E))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    check(lib().frt_moe_dispatch(_s(stream), _p(ids), T, K, E, _p(bounds), _p(tok_of), _p(slot_of), _p(ws), nbytes))
+    return ws
+
+
+# ---------------------------------------------------------------- prefill grouped GEMM
+
+def _q2_workspace_bytes(T: int, K: int, n: int, ff: int, E: int) -> int:
+    return int(lib().frt_moe_q2_workspace_bytes(T, K, n, ff, E))
+
+
+def _q2_run(experts, stride: int, E: int, n: int, ff: int, x, ids, T: int, K: int, yd, ws, ws_bytes: int,
+            stream=None, block64: bool = False, yd_bf16: bool = False) -> None:
+    check(lib().frt_moe_q2_run(_p(experts), stride, E, n, ff, _p(x), _p(ids), T, K, _p(yd), _p(ws), ws_bytes,
+                               _s(stream), int(block64), int(yd_bf16)))
+
+
+moe_q2 = SimpleNamespace(workspace_bytes=_q2_workspace_bytes, run=_q2_run)
+
+
+# ---------------------------------------------------------------- decode hits
+
+def moe_hits_scratch_bytes(K: int, ff: int, T: int = 1, n: int = 2048) -> int:
+    return int(lib().frt_moe_hits_scratch_bytes(K, ff, T, n))
+
+
+def moe_hits(hit_ptr, hit_n, K: int, x, n: int, ff: int, scratch, yh, stream=None, T: int = 1) -> None:
+    check(lib().frt_moe_hits(_p(hit_ptr), _p(hit_n), K, _p(x), n, ff, _p(scratch), _p(yh), _s(stream), T))
+
+
+# ---------------------------------------------------------------- one layer
+
+class MoeLayer:
+    """One MoE layer on the HBM arena: router -> top-k -> routed experts + shared expert *
+    sigmoid(gate). T <= 4 runs the decode GEMV path, larger T the grouped MFMA path."""
+
+    def __init__(self, experts: int, stride: int, n_expert: int, shared: int, router_w, gate_w, d_model: int,
+                 d_ff: int, top_k: int, router_bias=None):
+        self._keep = (router_w, gate_w, router_bias)
+        self.raw = FrtMoeLayer(experts, stride, n_expert, shared, _p(router_w), _p(router_bias), _p(gate_w),
+                               d_model, d_ff, top_k)
+        self.d_model, self.top_k, self.n_expert = d_model, top_k, n_expert
+        self._ws = None
+
+    def workspace_bytes(self, T: int) -> int:
+        return int(lib().frt_moe_layer_workspace_bytes(C.byref(self.raw), T))
+
+    def workspace(self, T: int) -> torch.Tensor:
+        need = self.workspace_bytes(T)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        return self._ws
+
+    def forward(self, x, out, T: int | None = None, resid=None, ids=None, wts=None, counts=None, ws=None,
+                stream=None) -> None:
+        T = x.shape[0] if T is None else T
+        ws = self.workspace(T) if ws is None else ws
+        check(lib().frt_moe_layer_forward(C.byref(self.raw), _p(x), T, _p(resid), _p(out), _p(ids), _p(wts),
+                                          _p(counts), _p(ws), ws.numel(), _s(stream)))
+
+
+# ---------------------------------------------------------------- synthetic inputs
+
+class _Gen:
+    SEED = 20261201
+    SHARED_TENSOR = 100000
+    ROUTER_TENSOR = 3000000
+    GATE_TENSOR = 3000001
+    X_TENSOR = 4000000
+
+    def experts(self, dst, stride: int, cfg: int, layer: int, e0: int, count: int, n: int, ff: int, sd: float = 0.02,
+                tensor_base: int = -1, seed: int | None = None, stream=None) -> None:
+        check(lib().frt_gen_experts(self.SEED if seed is None else seed, cfg, layer, e0, count, tensor_base, n, ff, sd,
+                                    _p(dst), stride, _s(stream)))
+
+    def normal(self, dst, cfg: int, layer: int, tensor: int, sd: float = 1.0, round_bf16: bool = False,
+               seed: int | None = None, stream=None) -> None:
+        check(lib().frt_gen_normal(self.SEED if seed is None else seed, cfg, layer, tensor, sd, _p(dst), dst.numel(),
+                                   int(round_bf16), _s(stream)))
+
+    def correlated(self, dst, cfg: int, layer: int, tensor0: int, T: int, n: int, rho: float, seed: int | None = None,
+                   stream=None) -> None:
+        check(lib().frt_gen_correlated(self.SEED if seed is None else seed, cfg, layer, tensor0, T, n, rho, _p(dst),
+                                       _s(stream)))
+
+    def zipf_bias(self, cfg: int, layer: int, E: int, s: float, alpha: float = 1.0, seed: int | None = None):
+        import numpy as np
+        out = np.zeros(E, np.float32)
+        lib().frt_gen_zipf_bias(self.SEED if seed is None else seed, cfg, layer, E, s, alpha, out.ctypes.data)
+        return out
+
+
+gen = _Gen()

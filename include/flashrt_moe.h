@@ -1,0 +1,132 @@
+/* flashrt_moe.h — C ABI of the MI355X (gfx950) MoE-layer library, libflashrt_moe.so.
+ *
+ * Each entry point replaces one entry of the reference's C++ MoE call surface; the reference
+ * declaration it stands for is cited beside it (paths into BFinn/flashrt). Conventions kept from
+ * the reference:
+ *   - every device buffer and workspace is allocated by the caller; each kernel family has a
+ *     *_bytes() size query; no call allocates device memory (graph capture stays legal);
+ *   - calls only enqueue work on the given stream (no host synchronisation);
+ *   - layouts: token-major [T][n] fp32 activations, ids/wts [T][K], per-slot outputs [T*K][n],
+ *     expert blobs in the planar Q2_0 layout (quant/q2_0/q2_0.hpp:5-15): gate [ff][n] | up [ff][n] |
+ *     down [n][ff], each as codes [rows][cols/64][16] then fp16 scales [rows][cols/64].
+ * Errors: functions return 0 on success and a negative FRT_ERR_* code otherwise (the reference
+ * throws std::runtime_error in the same places); frt_last_error() gives the message.
+ * All pointers are device pointers unless stated. hipStream_t is passed as void*.
+ */
+#ifndef FLASHRT_MOE_H
+#define FLASHRT_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FRT_OK 0
+#define FRT_ERR_SHAPE -1      /* unsupported shape or argument */
+#define FRT_ERR_WORKSPACE -2  /* workspace or scratch too small */
+#define FRT_ERR_HIP -3        /* a HIP call failed */
+#define FRT_ERR_NULL -4       /* a required pointer is missing */
+
+/* Message of the last failure on this thread (static storage; "" when none). */
+const char* frt_last_error(void);
+/* Library version string. */
+const char* frt_version(void);
+
+/* ---- planar Q2_0 sizes (quant/q2_0/q2_0.hpp:40,51: mat_bytes, expert_bytes) ---- */
+size_t frt_q2_mat_bytes(int rows, int cols);
+size_t frt_q2_expert_bytes(int d_model, int d_ff);
+
+/* ---- HBM expert arena (core/expert_arena.hpp:14-30: ExpertArena, arena_alloc, arena_free).
+ * One device allocation of n_layer * n_expert blobs, each at a 4 KiB-aligned stride; expert e of
+ * layer l is at base + (l * n_expert + e) * stride. The reference's arena lives in host RAM and
+ * is registered for DMA (arch/qwen4exp/moe_fast.hpp:109-112 arena_register); on MI355X all experts
+ * are resident in HBM, so this one allocation at load time replaces both. */
+typedef struct frt_arena {
+    uint8_t* base;      /* device */
+    size_t blob_bytes;  /* useful bytes per expert */
+    size_t stride;      /* blob_bytes rounded up to 4 KiB */
+    int n_layer, n_expert;
+} frt_arena;
+int frt_arena_alloc(int n_layer, int n_expert, size_t blob_bytes, frt_arena* out);
+int frt_arena_free(frt_arena* a);
+uint8_t* frt_arena_blob(const frt_arena* a, int layer, int expert);
+size_t frt_arena_total_bytes(const frt_arena* a);
+/* Copies one repacked blob from host memory into (layer, expert) (the per-expert step of
+ * arch/qwen4exp/experts.cpp:93-116 load_experts, minus the file read). */
+int frt_arena_upload(const frt_arena* a, int layer, int expert, const void* host_blob, void* stream);
+
+/* ---- routing (arch/qwen4exp/blocks.hpp:130-135 moe_route_topk): softmax over E <= 1024 logits,
+ * top-k (k <= 32) ranked by logit, ties to the lower expert id, weights p / max(sum_top p, 2^-14);
+ * counts [E] (optional) += 1 per selection; tail_counts likewise for tokens t >= tail_from. */
+int frt_moe_route_topk(void* stream, const float* logits, int T, int E, int k, int32_t* ids, float* wts,
+                       uint32_t* counts, uint32_t* tail_counts, int tail_from);
+
+/* ---- router logits in the canonical order (the reference computes them with its dense linear(),
+ * arch/qwen4exp/blocks.hpp:85, ffn_gate_inp and ffn_gate_inp_shexp; this build fixes one float
+ * order so CPU and GPU agree bit for bit): logits [T][E] = W x + bias (bias optional), and, when
+ * gate_w is given, gate [T] = gate_w . x. n a multiple of 512 up to 4096. */
+int frt_router_logits(void* stream, const float* x, int T, const float* W, const float* bias, const float* gate_w,
+                      int E, int n, float* logits, float* gate);
+
+/* ---- Q8_0 activation quantization (quant/q2_0/q2_0.hpp:66-70 quantize_q8): per 32 values
+ * d = fp16(amax/127), q = roundf(x * 127/amax). xq [rows][n] int8, xd [rows][n/32] float. */
+int frt_quantize_q8(void* stream, const float* x, int rows, int n, int8_t* xq, float* xd);
+
+/* ---- dispatch permutation (kernels/cuda/moe_q2.cu:83-168): a stable sort of slots s = t*K + k by
+ * ids[s]: bounds [E+1], row r holds slot_of[r] and tok_of[r] = slot_of[r] / K. */
+size_t frt_moe_dispatch_workspace_bytes(int T, int K, int E);
+int frt_moe_dispatch(void* stream, const int32_t* ids, int T, int K, int E, int32_t* bounds, int32_t* tok_of,
+                     int32_t* slot_of, void* ws, size_t ws_bytes);
+
+/* ---- prefill grouped expert GEMM (kernels/cuda/moe_q2.h:20-30 moe_q2::workspace_bytes, run).
+ * yd [T*K][n]: slot t*K + k gets down(silu(gate x_t) * up x_t) of expert ids[t*K + k], expert e's
+ * blob at experts + e * stride. yd_bf16 selects bf16 output. block64 (activations quantized per
+ * 64) is not supported here: it returns FRT_ERR_SHAPE (activations use Q8_0 blocks of 32, the CPU
+ * path's quantization). */
+size_t frt_moe_q2_workspace_bytes(int T, int K, int n, int ff, int E);
+int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const float* x, const int32_t* ids,
+                   int T, int K, void* yd, void* ws, size_t ws_bytes, void* stream, int block64, int yd_bf16);
+
+/* ---- decode expert GEMVs (arch/qwen4exp/moe_fast.hpp:134-142 moe_hits_scratch_bytes, moe_hits).
+ * yh [T][K][n]: entry (t, k) for k < hit_n[t] = down(silu(gate x) * up x) of the blob at
+ * hit_ptr[t*K + k] (device array of device pointers); entries k >= hit_n[t] are not written.
+ * x [T][n] fp32, T <= 4 (each distinct blob read once for the window, moe_fast.cu:195-355).
+ * Activations are quantized to Q8_0 per 32 (the reference quantizes per 64 here). */
+size_t frt_moe_hits_scratch_bytes(int K, int ff, int T, int n);
+int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const float* x, int n, int ff,
+                 void* scratch, float* yh, void* stream, int T);
+
+/* ---- one whole MoE layer on an HBM-resident arena: router logits -> route_topk -> routed experts
+ * + shared expert * sigmoid(gate) (moe_block_fast, arch/qwen4exp/moe_fast.hpp:144-147, for T <= 4;
+ * moe_block_stream, arch/qwen4exp/moe_stream.hpp:35, for prefill chunks; same math as moe_block,
+ * arch/qwen4exp/blocks.hpp:286). out [T][n] = (resid ? resid : 0) + moe(x). ids/wts [T][K]
+ * (optional outputs), counts [E] optional. */
+typedef struct frt_moe_layer {
+    const uint8_t* experts;   /* routed expert 0 of this layer; expert e at experts + e * stride */
+    size_t stride;
+    int n_expert;             /* E <= 1024 */
+    const uint8_t* shared;    /* the shared expert's planar Q2_0 blob (same shape) */
+    const float* router_w;    /* [E][n] fp32 (ffn_gate_inp) */
+    const float* router_bias; /* [E] added to the logits, or NULL */
+    const float* gate_w;      /* [n] fp32 (ffn_gate_inp_shexp) */
+    int d_model, d_ff, top_k;
+} frt_moe_layer;
+size_t frt_moe_layer_workspace_bytes(const frt_moe_layer* L, int T);
+int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out, int32_t* ids,
+                          float* wts, uint32_t* counts, void* ws, size_t ws_bytes, void* stream);
+
+/* ---- seeded synthetic inputs written on the device (no reference counterpart: the reference's
+ * tests draw from std::mt19937; this recipe is documented in flashrt_amd/csrc/gen.hip) ---- */
+int frt_gen_experts(uint64_t seed, int cfg, int layer, int e0, int count, int tensor_base, int n, int ff, float sd,
+                    uint8_t* dst, size_t stride, void* stream);
+int frt_gen_normal(uint64_t seed, int cfg, int layer, int tensor, float sd, float* dst, size_t count, int round_bf16,
+                   void* stream);
+int frt_gen_correlated(uint64_t seed, int cfg, int layer, int tensor0, int T, int n, float rho, float* dst, void* stream);
+void frt_gen_zipf_bias(uint64_t seed, int cfg, int layer, int E, float s, float alpha, float* host_bias);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,306 @@
+"""GPU parity: the HIP library through its C ABI against the CPU oracle on the same seeded inputs.
+
+Bars: ids and the dispatch permutation bit-exact; routing weights <= 1e-6 relative; layer outputs
+<= 2e-3 max relative per token (tests/helpers.py).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests import helpers as H
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def F():
+    import flashrt_amd
+    flashrt_amd.lib()   # raises if the HIP library is not built
+    return flashrt_amd
+
+
+@pytest.fixture(scope="module")
+def w0(F):
+    return H.World(cfg=0)
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return t.cuda() if dtype is None else t.to(dtype).cuda()
+
+
+# ---------------------------------------------------------------- synthetic inputs
+
+def test_generator_matches_oracle(F, w0):
+    for e in (0, 7, 511):
+        assert np.array_equal(w0.blob(e), O.gen_expert(0, 0, e, H.N, H.FF)), e
+    sh = np.zeros(w0.eb, np.uint8)
+    O.lib().orc_gen_expert(O.SEED, 0, 0, O.SHARED_TENSOR, H.N, H.FF, 0.02, sh)
+    assert np.array_equal(w0.shared_h, sh)
+    assert np.array_equal(w0.router_h.reshape(-1), O.gen_normal(0, 0, O.ROUTER_TENSOR, H.E * H.N, 0.02))
+    assert np.array_equal(w0.gate_h, O.gen_normal(0, 0, O.GATE_TENSOR, H.N, 0.02))
+    x = torch.empty(4096, dtype=torch.float32, device="cuda")
+    F.gen.normal(x, 3, 0, O.X_TENSOR, 1.0, round_bf16=True)
+    ref = O.gen_normal(3, 0, O.X_TENSOR, 4096)
+    bits = ref.view(np.uint32).astype(np.uint64)
+    rb = (((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)).view(np.float32)
+    assert np.array_equal(x.cpu().numpy(), rb)
+    xc = torch.empty((3, H.N), dtype=torch.float32, device="cuda")
+    F.gen.correlated(xc, 1, 0, O.X_TENSOR, 3, H.N, 0.8)
+    z0 = O.gen_normal(1, 0, O.X_TENSOR, H.N)
+    a, b = np.sqrt(np.float32(0.8)), np.sqrt(np.float32(0.2))
+    for t in range(3):
+        zt = O.gen_normal(1, 0, O.X_TENSOR + 1 + t, H.N)
+        assert np.array_equal(xc[t].cpu().numpy(), (a * z0 + b * zt).astype(np.float32))
+    assert np.array_equal(F.gen.zipf_bias(2, 5, 512, 1.1), O.gen_zipf_bias(2, 5, 512, 1.1))
+
+
+# ---------------------------------------------------------------- quantization and router
+
+def test_quantize_q8_bit_exact(F):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 2048)).astype(np.float32)
+    x[1, :32] = 0.0                  # an all-zero block: d = 0, codes 0
+    x[2, 32:64] *= 1e4               # large values
+    x[3, 64:96] = np.float32(-7.0)   # a constant block: codes -127
+    x[4, 96:128] = np.arange(32, dtype=np.float32) * 0.5 - 8.0   # exact halves: roundf ties away from zero
+    xq = torch.empty((5, 2048), dtype=torch.int8, device="cuda")
+    xd = torch.empty((5, 64), dtype=torch.float32, device="cuda")
+    F.quantize_q8(dev(x), 5, 2048, xq, xd)
+    torch.cuda.synchronize()
+    qs, d = O.quantize_q8(x)
+    assert np.array_equal(xq.cpu().numpy().reshape(-1), qs)
+    assert np.array_equal(xd.cpu().numpy().reshape(-1), d)
+
+
+@pytest.mark.parametrize("T,n,with_bias", [(1, 2048, False), (3, 2048, True), (17, 2048, True), (5, 2560, False)])
+def test_router_logits_bit_exact(F, T, n, with_bias):
+    E = 512
+    rng = np.random.default_rng(T * 7 + n)
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    W = (rng.standard_normal((E, n)) * 0.02).astype(np.float32)
+    g = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    bias = (rng.standard_normal(E)).astype(np.float32) if with_bias else None
+    lg = torch.empty((T, E), dtype=torch.float32, device="cuda")
+    gt = torch.empty(T, dtype=torch.float32, device="cuda")
+    F.router_logits(dev(x), T, dev(W), E, n, lg, bias=None if bias is None else dev(bias), gate_w=dev(g), gate=gt)
+    torch.cuda.synchronize()
+    ref = O.router_logits(x, W, bias)
+    assert np.array_equal(lg.cpu().numpy(), ref)
+    gref = np.array([O.dot_canon(g, x[t]) for t in range(T)], np.float32)
+    assert np.array_equal(gt.cpu().numpy(), gref)
+
+
+# ---------------------------------------------------------------- routing
+
+def _route_gpu(F, lg, K, tail_from=1 << 30):
+    T, E = lg.shape
+    ids = torch.full((T, K), -1, dtype=torch.int32, device="cuda")
+    w = torch.zeros((T, K), dtype=torch.float32, device="cuda")
+    cnt = torch.zeros(E, dtype=torch.int32, device="cuda")
+    tail = torch.zeros(E, dtype=torch.int32, device="cuda")
+    F.moe_route_topk(None, dev(lg), T, E, K, ids, w, cnt, tail, tail_from)
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), w.cpu().numpy(), cnt.cpu().numpy(), tail.cpu().numpy()
+
+
+def test_route_topk_reference_recipe(F):
+    """tests/test_route_topk.cpp:22-69: T 16384, E 512, K 10, logits round(N(0,2)*4)/4 (many exact
+    ties); ids == stable sort by logit, counts exact, weights vs a double softmax. The normals come
+    from this build's generator (the reference draws std::mt19937 + libstdc++'s normal)."""
+    T, E, K = 16384, 512, 10
+    lg = (np.round(O.gen_normal(9, 0, 1, T * E, 2.0) * 4.0) / 4.0).astype(np.float32).reshape(T, E)
+    ids, w, cnt, tail = _route_gpu(F, lg, K, tail_from=T - 100)
+    oid, ow, ocnt = O.route_topk(lg, K)
+    assert np.array_equal(ids, oid)
+    assert np.array_equal(cnt.astype(np.uint32), ocnt)
+    assert H.w_rel(w, ow) <= H.W_REL
+    # the reference test's own definition: stable sort by logit, double softmax, < 1e-5 abs
+    idx = np.argsort(-lg, axis=1, kind="stable")[:, :K]
+    assert np.array_equal(ids, idx)
+    mx = lg.max(axis=1, keepdims=True).astype(np.float64)
+    p = np.exp(lg.astype(np.float64) - mx)
+    p /= p.sum(axis=1, keepdims=True)
+    ps = np.take_along_axis(p, idx, axis=1)
+    assert np.abs(w - ps / ps.sum(axis=1, keepdims=True)).max() < 1e-5
+    tref = np.bincount(oid[T - 100:].reshape(-1), minlength=E)
+    assert np.array_equal(tail, tref)
+
+
+@pytest.mark.parametrize("T,E,K", [(1, 512, 10), (3, 64, 1), (5, 1000, 32), (7, 1024, 8), (33, 96, 10)])
+def test_route_topk_shapes(F, T, E, K):
+    rng = np.random.default_rng(E + K)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg[0, :8] = 3.0   # exact ties at the top
+    ids, w, cnt, _ = _route_gpu(F, lg, K)
+    oid, ow, ocnt = O.route_topk(lg, K)
+    assert np.array_equal(ids, oid)
+    assert np.array_equal(cnt.astype(np.uint32), ocnt)
+    assert H.w_rel(w, ow) <= H.W_REL
+
+
+def test_route_topk_errors(F):
+    lg = torch.zeros((2, 2048), dtype=torch.float32, device="cuda")
+    ids = torch.zeros((2, 10), dtype=torch.int32, device="cuda")
+    w = torch.zeros((2, 10), dtype=torch.float32, device="cuda")
+    with pytest.raises(F.FrtError) as e:
+        F.moe_route_topk(None, lg, 2, 2048, 10, ids, w)
+    assert e.value.code == -1
+    with pytest.raises(F.FrtError):
+        F.moe_route_topk(None, lg, 2, 512, 33, ids, w)
+    F.moe_route_topk(None, lg, 0, 512, 10, ids, w)   # T = 0: nothing to do
+
+
+# ---------------------------------------------------------------- dispatch
+
+@pytest.mark.parametrize("T,skew", [(1, 0.0), (3, 0.0), (2048, 1.2), (8208, 3.0)])
+def test_dispatch_bit_exact(F, T, skew):
+    E, K = 512, 10
+    rng = np.random.default_rng(T)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    if skew:
+        lg += O.gen_zipf_bias(3, 0, E, skew)[None, :]
+    ids, _, _ = O.route_topk(lg, K)
+    b = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    to = torch.empty(T * K, dtype=torch.int32, device="cuda")
+    so = torch.empty(T * K, dtype=torch.int32, device="cuda")
+    F.moe_dispatch(dev(ids), T, K, E, b, to, so)
+    torch.cuda.synchronize()
+    rb, rt, rs = O.dispatch(ids, E)
+    assert np.array_equal(b.cpu().numpy(), rb)
+    assert np.array_equal(so.cpu().numpy(), rs)
+    assert np.array_equal(to.cpu().numpy(), rt)
+    # a stable sort of (expert, slot), the definition in kernels/cuda/moe_q2.cu:83-168
+    assert np.array_equal(rs, np.argsort(ids.reshape(-1), kind="stable"))
+
+
+# ---------------------------------------------------------------- decode path (T <= 4)
+
+def test_layer_decode_config0(F, w0):
+    x = O.gen_normal(0, 0, O.X_TENSOR, H.N).reshape(1, H.N)
+    out, ids, wts = w0.gpu_forward(x)
+    ref, rid, rw, _ = w0.oracle_forward(x)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    assert H.out_rel(out, ref) <= H.OUT_REL
+
+
+def test_layer_decode_config1_window(F):
+    w1 = H.World(cfg=1)
+    xc = torch.empty((3, H.N), dtype=torch.float32, device="cuda")
+    F.gen.correlated(xc, 1, 0, O.X_TENSOR, 3, H.N, 0.8)
+    x = xc.cpu().numpy()
+    out, ids, wts = w1.gpu_forward(x)
+    ref, rid, rw, _ = w1.oracle_forward(x)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    assert H.out_rel(out, ref) <= H.OUT_REL
+    # overlapping routes: the window reads fewer than 3 * 10 distinct experts
+    assert len(set(ids.reshape(-1).tolist())) < 30
+    # each token alone gives the same outputs as the window (moe_fast.cu:195-355 exactness)
+    for t in range(3):
+        o1, i1, _ = w1.gpu_forward(x[t:t + 1])
+        assert np.array_equal(i1[0], ids[t])
+        assert np.array_equal(o1[0], out[t])
+
+
+def test_layer_decode_resid(F, w0):
+    x = O.gen_normal(0, 0, O.X_TENSOR + 5, 2 * H.N).reshape(2, H.N)
+    r = O.gen_normal(0, 0, O.X_TENSOR + 6, 2 * H.N).reshape(2, H.N)
+    out, _, _ = w0.gpu_forward(x)
+    out_r, _, _ = w0.gpu_forward(x, resid=r)
+    assert np.array_equal(out_r, (r + out).astype(np.float32))
+
+
+def test_moe_hits(F, w0):
+    """tests/test_moe_hits.cpp:42-166: per-slot expert outputs; pad entries (k >= hit_n) untouched."""
+    T, K = 3, 16
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((T, H.N)).astype(np.float32)
+    hit_n = np.array([9, 16, 1], np.int32)
+    experts = rng.choice(512, size=(T, K), replace=True).astype(np.int64)
+    experts[1, :4] = experts[0, :4]   # shared across tokens of the window
+    base = w0.arena.data_ptr()
+    ptr = torch.tensor((base + experts * w0.stride).reshape(-1), dtype=torch.int64, device="cuda")
+    yh = torch.full((T, K, H.N), float("nan"), dtype=torch.float32, device="cuda")
+    scratch = torch.empty(F.moe_hits_scratch_bytes(K, H.FF, T, H.N), dtype=torch.uint8, device="cuda")
+    F.moe_hits(ptr, dev(hit_n), K, dev(x), H.N, H.FF, scratch, yh, T=T)
+    torch.cuda.synchronize()
+    y = yh.cpu().numpy()
+    for t in range(T):
+        for k in range(K):
+            if k >= hit_n[t]:
+                assert np.isnan(y[t, k]).all()
+                continue
+            ref = O.expert_ffn(w0.blob(int(experts[t, k])), H.N, H.FF, x[t])
+            assert H.out_rel(y[t, k][None], ref) <= H.OUT_REL
+    # window == one-token calls, exactly
+    for t in range(T):
+        y1 = torch.full((1, K, H.N), float("nan"), dtype=torch.float32, device="cuda")
+        F.moe_hits(ptr[t * K:(t + 1) * K], dev(hit_n[t:t + 1]), K, dev(x[t:t + 1]), H.N, H.FF, scratch, y1, T=1)
+        torch.cuda.synchronize()
+        a = y1.cpu().numpy()[0, :hit_n[t]]
+        assert np.array_equal(a, y[t, :hit_n[t]])
+
+
+# ---------------------------------------------------------------- prefill path
+
+@pytest.mark.parametrize("yd_bf16", [False, True])
+def test_moe_q2_run(F, w0, yd_bf16):
+    """tests/test_moe_q2.cpp:97-153 shape: T = 96 tokens over 24 experts; per-slot outputs vs the
+    oracle's expert_ffn (bf16 output: within bf16 rounding, 2^-8 relative)."""
+    T, K, E = 96, 10, 24
+    rng = np.random.default_rng(96)
+    x = rng.standard_normal((T, H.N)).astype(np.float32)
+    ids = np.stack([rng.choice(E, size=K, replace=False) for _ in range(T)]).astype(np.int32)
+    nb = F.moe_q2.workspace_bytes(T, K, H.N, H.FF, E)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    yd = torch.full((T * K, H.N), float("nan"), dtype=torch.bfloat16 if yd_bf16 else torch.float32, device="cuda")
+    F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, nb, None, False, yd_bf16)
+    torch.cuda.synchronize()
+    y = yd.float().cpu().numpy().reshape(T, K, H.N)
+    tol = 2 ** -8 if yd_bf16 else H.OUT_REL
+    for t in range(0, T, 5):
+        for k in range(K):
+            ref = O.expert_ffn(w0.blob(int(ids[t, k])), H.N, H.FF, x[t])
+            assert H.out_rel(y[t, k][None], ref) <= tol, (t, k)
+    with pytest.raises(F.FrtError) as e:
+        F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, nb - 1024)
+    assert e.value.code == -2
+    with pytest.raises(F.FrtError):
+        F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, nb, None, True)
+
+
+def test_layer_prefill_config3(F):
+    """Config 3: 2048 bf16 tokens, Zipf(1.2) routing prior. Every token's ids are bit-exact; the
+    outputs of 48 sampled tokens are checked against the oracle (a token's output depends only on
+    that token)."""
+    T = 2048
+    bias = O.gen_zipf_bias(3, 0, H.E, H.ZIPF_S_PREFILL, H.PREFILL_ALPHA)
+    w3 = H.World(cfg=3, bias=bias)
+    xt = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    F.gen.normal(xt, 3, 0, O.X_TENSOR, 1.0, round_bf16=True)
+    x = xt.cpu().numpy()
+    out, ids, wts = w3.gpu_forward(x)
+    lg = O.router_logits(x, w3.router_h, bias)
+    rid, rw, cnt = O.route_topk(lg, H.K)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    assert cnt.max() > 100 and (cnt == 0).sum() > 0   # ragged groups, some empty
+    sel = np.random.default_rng(0).choice(T, size=48, replace=False)
+    ref, sid, _, _ = w3.oracle_forward(x[sel])
+    assert np.array_equal(sid, ids[sel])
+    assert H.out_rel(out[sel], ref) <= H.OUT_REL
+    assert np.isfinite(out).all()
+
+
+def test_layer_errors(F, w0):
+    x = torch.zeros((1, H.N), dtype=torch.float32, device="cuda")
+    out = torch.zeros((1, H.N), dtype=torch.float32, device="cuda")
+    ws = w0.layer_obj.workspace(1)
+    with pytest.raises(F.FrtError) as e:
+        w0.layer_obj.forward(x, out, T=1, ws=ws[:16])
+    assert e.value.code == -2
