@@ -1,0 +1,396 @@
+#!/usr/bin/env python3
+"""bench.py — flashrt's MoE-layer hot path on one MI355X.
+
+Headline: a 48-layer stack of the Q2_0 512-expert top-10 MoE layer
+(hidden 2048, expert ff 512, shared expert ff 512), all experts resident in HBM, decode at bs=1.
+A step is one token through the 48 layers (x_{l+1} = x_l + moe_l(rms_norm(x_l)), the pre-MoE
+RMS norm without weight keeping the chained residual stream bounded); each step's input is a
+fresh N(0,1) vector; router logits carry a per-layer Zipf(s=1.1) prior over a random permutation of
+the experts. The 48 layers of one step are captured once as a HIP graph and replayed per step.
+
+Also measured in the same run:
+  - per-kernel durations (hipEvents on the launch stream, eager run) and the roofline of the
+    dominant kernel: algorithmic expert bytes per launch / its average duration vs 8 TB/s;
+  - one layer, 2048-token prefill (bf16 inputs, Zipf(1.2) prior): tokens/s and the
+    grouped GEMM kernels' MFMA utilisation against the 2.5 PFLOP/s dense fp16 peak;
+  - cpu_baseline: the reference's own CPU MoE (moe_cpu over its CpuPool, AVX-512 VNNI; built from
+    its sources into oracle/_ref) on a bounded sample of the same workload on this host.
+
+Prints ONE JSON line. `--gpus N` with N > 1 exits: this build runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-stack tokens/s (decode bs1, prefill 2K); achieved HBM TB/s & MFMA % of peak"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+N, FF, E, K, LAYERS = 2048, 512, 512, 10, 48
+ZIPF_STACK, ZIPF_PREFILL, PREFILL_ALPHA = 1.1, 1.2, 0.4
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def kernel_times(F, fn):
+    """Runs fn() with the library's per-kernel hipEvent timing on; returns {kernel: (ms, launches)}."""
+    import ctypes as C
+    L = F.lib()
+    L.frt_timing_begin()
+    fn()
+    names = C.create_string_buffer(64 * 32)
+    ms = (C.c_double * 32)()
+    cnt = (C.c_int * 32)()
+    n = L.frt_timing_end(names, 32, ms, cnt, 32)
+    out = {}
+    for i in range(n):
+        nm = names.raw[i * 32:(i + 1) * 32].split(b"\0")[0].decode()
+        out[nm] = (float(ms[i]), int(cnt[i]))
+    return out
+
+
+# ---------------------------------------------------------------- config 2: decode stack
+
+def build_stack(F, torch, layers):
+    eb = F.expert_bytes(N, FF)
+    arena = F.arena_alloc(layers, E, eb)
+    g = F.gen
+    for l in range(layers):
+        g.experts(arena.blob(l, 0), arena.stride, 2, l, 0, E, N, FF)
+    shared = torch.empty((layers, arena.stride), dtype=torch.uint8, device="cuda")
+    router = torch.empty((layers, E, N), dtype=torch.float32, device="cuda")
+    gate = torch.empty((layers, N), dtype=torch.float32, device="cuda")
+    bias = torch.empty((layers, E), dtype=torch.float32, device="cuda")
+    for l in range(layers):
+        g.experts(shared[l], arena.stride, 2, l, 0, 1, N, FF, tensor_base=g.SHARED_TENSOR)
+        g.normal(router[l], 2, l, g.ROUTER_TENSOR, 0.02)
+        g.normal(gate[l], 2, l, g.GATE_TENSOR, 0.02)
+        bias[l] = torch.from_numpy(g.zipf_bias(2, l, E, ZIPF_STACK))
+    mls = [F.MoeLayer(arena.blob(l, 0), arena.stride, E, shared[l].data_ptr(), router[l], gate[l], N, FF, K,
+                      router_bias=bias[l], norm_input=True) for l in range(layers)]
+    torch.cuda.synchronize()
+    return arena, shared, router, gate, bias, mls
+
+
+def run_stack(args, F, torch):
+    layers = args.layers
+    arena, shared, router, gate, bias, mls = build_stack(F, torch, layers)
+    total_steps = args.warmup + args.steps
+    xs = torch.empty((total_steps, N), dtype=torch.float32, device="cuda")
+    F.gen.normal(xs, 2, 0, F.gen.X_TENSOR, 1.0)
+    ws = torch.empty(mls[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
+    xin = torch.empty((1, N), dtype=torch.float32, device="cuda")
+    buf = [torch.empty((1, N), dtype=torch.float32, device="cuda") for _ in range(2)]
+    ids = torch.empty((layers, K), dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+
+    def step_body():
+        cur = xin
+        for l, ml in enumerate(mls):
+            nxt = buf[l % 2]
+            ml.forward(cur, nxt, T=1, resid=cur, ids=ids[l], ws=ws)
+            cur = nxt
+
+    with torch.cuda.stream(stream):
+        xin.copy_(xs[0:1])
+        step_body()                      # eager once (sets up everything outside capture)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step_body()
+    with torch.cuda.stream(stream):
+        for s in range(args.warmup):
+            xin.copy_(xs[s:s + 1])
+            graph.replay()
+    stream.synchronize()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for s in range(args.warmup, total_steps):
+            xin.copy_(xs[s:s + 1])
+            graph.replay()
+        e1.record(stream)
+    stream.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = e0.elapsed_time(e1)
+    ms_per_step = gpu_ms / args.steps
+    log(f"stack: {args.steps} steps x {layers} layers: {gpu_ms:.2f} ms on the stream ({wall * 1e3:.2f} ms wall), "
+        f"{ms_per_step * 1e3:.1f} us/token")
+
+    # per-kernel durations, eager launches on the same stream
+    def eager():
+        with torch.cuda.stream(stream):
+            for s in range(min(32, total_steps)):
+                xin.copy_(xs[s:s + 1])
+                step_body()
+    eager()
+    stream.synchronize()
+    kt = kernel_times(F, eager)
+    del graph
+    res = dict(ms_per_step=ms_per_step, wall_s=wall, kernels=kt)
+    res["_keep"] = (arena, shared, router, gate, bias, mls, xs, ws)
+    return res
+
+
+# ---------------------------------------------------------------- config 3: 2K prefill
+
+def run_prefill(args, F, torch):
+    from types import SimpleNamespace
+    T = 2048
+    eb = F.expert_bytes(N, FF)
+    stride = (eb + 4095) // 4096 * 4096
+    g = F.gen
+    arena = torch.empty(E * stride, dtype=torch.uint8, device="cuda")
+    g.experts(arena, stride, 3, 0, 0, E, N, FF)
+    shared = torch.empty(eb, dtype=torch.uint8, device="cuda")
+    g.experts(shared, eb, 3, 0, 0, 1, N, FF, tensor_base=g.SHARED_TENSOR)
+    router = torch.empty((E, N), dtype=torch.float32, device="cuda")
+    g.normal(router, 3, 0, g.ROUTER_TENSOR, 0.02)
+    gate = torch.empty(N, dtype=torch.float32, device="cuda")
+    g.normal(gate, 3, 0, g.GATE_TENSOR, 0.02)
+    bias = torch.from_numpy(g.zipf_bias(3, 0, E, ZIPF_PREFILL, PREFILL_ALPHA)).cuda()
+    ml = F.MoeLayer(arena.data_ptr(), stride, E, shared.data_ptr(), router, gate, N, FF, K, router_bias=bias)
+    x = torch.empty((T, N), dtype=torch.float32, device="cuda")
+    g.normal(x, 3, 0, g.X_TENSOR, 1.0, round_bf16=True)
+    out = torch.empty((T, N), dtype=torch.float32, device="cuda")
+    ws = ml.workspace(T)
+    stream = torch.cuda.Stream()
+    reps = args.prefill_reps
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            ml.forward(x, out, T=T, ws=ws)
+    stream.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(reps):
+            ml.forward(x, out, T=T, ws=ws)
+        e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+
+    def eager():
+        with torch.cuda.stream(stream):
+            for _ in range(reps):
+                ml.forward(x, out, T=T, ws=ws)
+    kt = kernel_times(F, eager)
+    S = T * K + T
+    gu_flops = 2.0 * S * 2 * N * FF
+    dn_flops = 2.0 * S * N * FF
+    util = {}
+    for name, fl in (("pf_gateup", gu_flops), ("pf_down", dn_flops)):
+        if name in kt:
+            avg_ms = kt[name][0] / kt[name][1]
+            util[name] = dict(avg_us=avg_ms * 1e3, tflops=fl / (avg_ms * 1e-3) / 1e12,
+                              mfma_frac=fl / (avg_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS)
+    flops = gu_flops + dn_flops
+    log(f"prefill 2K: {ms:.3f} ms/layer, {T / ms * 1e3:.0f} tok/s, experts {flops / 1e9:.1f} GFLOP")
+    return SimpleNamespace(ms=ms, tokens_per_s=T / ms * 1e3, kernels=kt, util=util, flops=flops)
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(args, F, torch, stack):
+    """The reference's moe_cpu (oracle/_ref, AVX-512 VNNI on its CpuPool) or, when that was not
+    built, the oracle's restatement, on a sample of config 2: the first `cpu_layers` layers' experts
+    copied to host RAM, tokens chained through them with routing done on the host (numpy fp32 router
+    GEMV + top-10 + softmax); the per-layer time is scaled to 48 layers."""
+    from oracle import oracle as O
+    arena, shared, router, gate, bias, mls, _, _ = stack["_keep"]
+    nl = args.cpu_layers
+    host = torch.empty((nl, E, arena.stride), dtype=torch.uint8)
+    import ctypes as C
+    for l in range(nl):
+        t = torch.empty(E * arena.stride, dtype=torch.uint8, device="cuda")
+        _copy_arena_layer(arena, l, t)
+        host[l] = t.view(E, arena.stride).cpu()
+        del t
+    torch.cuda.synchronize()
+    sh_h = shared[:nl].cpu().numpy()
+    rw = router[:nl].cpu().numpy()
+    gw = gate[:nl].cpu().numpy()
+    bh = bias[:nl].cpu().numpy()
+    host_np = host.numpy()
+    n_aff = len(os.sched_getaffinity(0))
+    workers = max(1, min(n_aff, int(os.environ.get("OMP_NUM_THREADS", "16")), 16))
+    kind = "reference" if O.have_ref() else "port"
+    R = O.ref() if O.have_ref() else None
+    pool = R.ref_pool_create(workers, 0) if R else None
+    rng_x = O.gen_normal(2, 0, O.X_TENSOR, 64 * N).reshape(64, N)
+    blobs = (C.c_void_p * 11)()
+    route_times, moe_times = [], []
+    t_end = time.perf_counter() + args.cpu_seconds
+    steps = 0
+    try:
+        from threadpoolctl import threadpool_limits
+        limiter = threadpool_limits(1)
+    except Exception:
+        limiter = None
+    while time.perf_counter() < t_end and steps < 64:
+        x = rng_x[steps].copy()
+        for l in range(nl):
+            t0 = time.perf_counter()
+            u = (x / np.sqrt(np.float32((x.astype(np.float64) ** 2).mean()) + np.float32(1e-6))).astype(np.float32)
+            lg = rw[l] @ u + bh[l]
+            top = np.argsort(-lg, kind="stable")[:K]
+            p = np.exp((lg - lg.max()).astype(np.float64))
+            p /= p.sum()
+            w = (p[top] / p[top].sum()).astype(np.float32)
+            gl = float(gw[l] @ u)
+            order = np.argsort(top)
+            for i, k in enumerate(order):
+                blobs[i] = host_np[l, top[k]].ctypes.data
+            blobs[10] = sh_h[l].ctypes.data
+            ntok = np.ones(11, np.int32)
+            tok = np.zeros(44, np.int32)
+            wv = np.zeros(44, np.float32)
+            wv[0:40:4] = w[order]
+            wv[40] = 1.0 / (1.0 + np.exp(-np.clip(gl, -80.0, 80.0)))
+            out = np.zeros(N, np.float32)
+            t1 = time.perf_counter()
+            if R:
+                prep = R.ref_moe_prepare(pool, N, FF, C.cast(blobs, C.c_void_p), ntok, tok, wv, 11, u, 1)
+                R.ref_moe_run(pool, prep, out, N)
+                R.ref_moe_free(prep)
+            else:
+                qs, d = O.quantize_q8(u)
+                O.lib().orc_moe_cpu(N, FF, C.cast(blobs, C.c_void_p), ntok, tok, wv, 11, qs, d, 1, out, N, workers, 1)
+            t2 = time.perf_counter()
+            route_times.append(t1 - t0)
+            moe_times.append(t2 - t1)
+            x = x + out
+        steps += 1
+    if limiter is not None:
+        limiter.unregister() if hasattr(limiter, "unregister") else None
+    if pool:
+        R.ref_pool_destroy(pool)
+    layer_times = [a + b for a, b in zip(route_times, moe_times)]
+    t_layer = float(np.median(layer_times))
+    return dict(value=1.0 / (LAYERS * t_layer), unit="tokens/s", cores=workers, kind=kind,
+                sample=(f"{steps} tokens x {nl} of {LAYERS} layers of configs[2] on the host CPU ({n_aff} CPUs in "
+                        f"this process's affinity mask): RMS norm + numpy fp32 router + top-10 on one thread "
+                        f"(median {np.median(route_times) * 1e6:.0f} us), then the "
+                        f"{'reference moe_cpu (AVX-512 VNNI) on its CpuPool' if R else 'oracle moe_cpu port'} with "
+                        f"{workers} workers over the 10 routed + shared experts (median "
+                        f"{np.median(moe_times) * 1e6:.0f} us); median {t_layer * 1e6:.0f} us/layer x {LAYERS} layers"),
+                moe_cpu_us=round(float(np.median(moe_times)) * 1e6, 1),
+                moe_cpu_GBps=round(11 * F.expert_bytes(N, FF) / float(np.median(moe_times)) / 1e9, 2))
+
+
+def _copy_arena_layer(arena, l, dst):
+    """Device-to-device hipMemcpy of layer l's E blobs (one contiguous range of the arena) into dst."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    rc = hip.hipMemcpy(C.c_void_p(dst.data_ptr()), C.c_void_p(arena.blob(l, 0)), E * arena.stride, 3)
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy failed: {rc}")
+
+
+# ---------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=384)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        sys.exit("bench.py: this build measures one MI355X; multi-GPU (expert-parallel) runs are not part of it "
+                 "(see DESIGN.md, 'How the path would shard')")
+    import torch
+    import flashrt_amd as F
+    F.lib()
+    torch.cuda.set_device(0)
+
+    st = run_stack(args, F, torch)
+    ms = st["ms_per_step"]
+    tok_s = 1e3 / ms
+    expert_bytes_tok = args.layers * (K + 1) * F.expert_bytes(N, FF)
+    router_bytes_tok = args.layers * (E * N * 4 + N * 4)
+    stack_tbs = expert_bytes_tok / (ms * 1e-3) / 1e12
+
+    # roofline of the dominant decode kernel
+    kt = st["kernels"]
+    per_launch_bytes = {
+        "dec_gateup": (K + 1) * 2 * F.lib().frt_q2_mat_bytes(FF, N),
+        "dec_down": (K + 1) * F.lib().frt_q2_mat_bytes(N, FF),
+        "router": E * N * 4 + N * 4,
+    }
+    dom = max(kt, key=lambda k: kt[k][0])
+    dom_avg_ms = kt[dom][0] / kt[dom][1]
+    dom_bytes = per_launch_bytes.get(dom)
+    achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9 if dom_bytes else None
+    kernels = {k: dict(avg_us=round(v[0] / v[1] * 1e3, 2), launches=v[1],
+                       share=round(v[0] / sum(x[0] for x in kt.values()), 3)) for k, v in kt.items()}
+    for k, b in per_launch_bytes.items():
+        if k in kt:
+            kernels[k]["algo_bytes"] = int(b)
+            kernels[k]["GBps"] = round(b / (kt[k][0] / kt[k][1] * 1e-3) / 1e9, 1)
+
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get(dom)
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded device generator: uniform 2-bit codes, fp16 |N(0,1)|*0.02 scales, fp32 N(0,0.02) "
+                "router, N(0,1) inputs, per-layer Zipf(1.1) logit prior)",
+        "config": {"workload": f"configs[2]: {args.layers}-layer Q2_0 MoE stack, decode bs=1, {args.steps} steps",
+                   "hidden": N, "experts": E, "top_k": K, "expert_ff": FF, "shared_ff": FF, "layers": args.layers,
+                   "global_batch": 1, "seq_len": 1, "parallelism": "none (one GPU)"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1) if achieved else None,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None, "traffic": traffic},
+        "stack": {"expert_bytes_per_token": expert_bytes_tok, "router_bytes_per_token": router_bytes_tok,
+                  "expert_TBps": round(stack_tbs, 3), "expert_hbm_frac": round(stack_tbs * 1e3 / HBM_PEAK_GBS, 4),
+                  "expert_plus_router_hbm_frac": round((expert_bytes_tok + router_bytes_tok) / (ms * 1e-3) / 1e9
+                                                       / HBM_PEAK_GBS, 4),
+                  "kernels": kernels},
+    }
+    if not args.no_prefill:
+        pf = run_prefill(args, F, torch)
+        line["prefill_2k"] = {"tokens_per_s": round(pf.tokens_per_s, 1), "ms_per_layer": round(pf.ms, 4),
+                              "expert_gflop": round(pf.flops / 1e9, 2),
+                              "mfma_frac_layer": round(pf.flops / (pf.ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                              "kernels": {k: dict(avg_us=round(v[0] / v[1] * 1e3, 2), launches=v[1])
+                                          for k, v in pf.kernels.items()},
+                              "mfma": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in pf.util.items()}}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args, F, torch, st)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

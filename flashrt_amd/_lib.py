@@ -18,6 +18,8 @@ _vp, _i, _sz, _u64, _f = C.c_void_p, C.c_int, C.c_size_t, C.c_uint64, C.c_float
 SIGNATURES = {
     "frt_last_error": (C.c_char_p, []),
     "frt_version": (C.c_char_p, []),
+    "frt_timing_begin": (None, []),
+    "frt_timing_end": (_i, [_vp, _i, _vp, _vp, _i]),
     "frt_q2_mat_bytes": (_sz, [_i, _i]),
     "frt_q2_expert_bytes": (_sz, [_i, _i]),
     "frt_arena_alloc": (_i, [_i, _i, _sz, _vp]),
@@ -43,6 +45,9 @@ SIGNATURES = {
 }
 
 
+LAYER_NORM_INPUT = 1
+
+
 class FrtError(RuntimeError):
     """A C-ABI call returned a nonzero status (the reference throws std::runtime_error)."""
 
@@ -59,7 +64,7 @@ class FrtArena(C.Structure):
 class FrtMoeLayer(C.Structure):
     _fields_ = [("experts", C.c_void_p), ("stride", C.c_size_t), ("n_expert", C.c_int), ("shared", C.c_void_p),
                 ("router_w", C.c_void_p), ("router_bias", C.c_void_p), ("gate_w", C.c_void_p),
-                ("d_model", C.c_int), ("d_ff", C.c_int), ("top_k", C.c_int)]
+                ("d_model", C.c_int), ("d_ff", C.c_int), ("top_k", C.c_int), ("flags", C.c_int)]
 
 
 _lib = None

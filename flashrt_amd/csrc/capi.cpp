@@ -6,6 +6,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <string>
+#include <utility>
+#include <vector>
 
 namespace frt {
 
@@ -19,9 +23,33 @@ int set_error(int code, const char* fmt, ...) {
     return code;
 }
 
+// ---- per-kernel timing
+namespace {
+struct Timing {
+    bool on = false;
+    std::vector<hipEvent_t> pool;
+    std::vector<std::pair<std::string, hipEvent_t>> marks;
+};
+Timing g_timing;
+}  // namespace
+
+void timing_mark(hipStream_t stream, const char* kernel) {
+    Timing& t = g_timing;
+    if (!t.on) return;
+    if (t.marks.size() == t.pool.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return;
+        t.pool.push_back(e);
+    }
+    hipEvent_t e = t.pool[t.marks.size()];
+    if (hipEventRecord(e, stream) != hipSuccess) return;
+    t.marks.emplace_back(kernel, e);
+}
+
 // route.hip
 int router_logits(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
-                  float* logits, float* gate, hipStream_t stream);
+                  float* logits, float* gate, hipStream_t stream, int norm, int8_t* xq, float* xd);
+int rmsnorm(const float* x, int T, int n, float* u, hipStream_t stream);
 int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xq16, hipStream_t stream);
 int route_topk(hipStream_t stream, const float* logits, int T, int E, int K, int32_t* ids, float* wts, uint32_t* counts,
                uint32_t* tail_counts, int tail_from);
@@ -63,6 +91,7 @@ static size_t hits_bytes(int K, int ff, int T, int n) {
 struct LayerWs {
     float* logits;
     float* gate;
+    float* u;   // normalised input (prefill with FRT_LAYER_NORM_INPUT)
     int32_t* ids;
     float* wts;
     int8_t* xq;
@@ -85,12 +114,13 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
     w.gate = reinterpret_cast<float*>(take(size_t(T) * 4));
     w.ids = reinterpret_cast<int32_t*>(take(size_t(T) * K * 4));
     w.wts = reinterpret_cast<float*>(take(size_t(T) * K * 4));
-    const bool dec = T <= kDecodeMaxT;
+    const bool dec = T <= kDecodeMaxT && T * K <= 63;
     if (dec) {
         w.xq = reinterpret_cast<int8_t*>(take(size_t(T) * n));
         w.xd = reinterpret_cast<float*>(take(size_t(T) * (n / kQ8) * 4));
         w.rest_bytes = dec_scratch_bytes(T, K, ff);
     } else {
+        if (L.flags & FRT_LAYER_NORM_INPUT) w.u = reinterpret_cast<float*>(take(size_t(T) * n * 4));
         w.rest_bytes = pf_workspace_bytes(T, K, n, ff, E, true, true);
     }
     w.rest = take(w.rest_bytes);
@@ -106,6 +136,40 @@ using namespace frt;
 extern "C" {
 
 const char* frt_last_error(void) { return g_err; }
+
+void frt_timing_begin(void) {
+    g_timing.on = true;
+    g_timing.marks.clear();
+}
+
+// Durations between consecutive marks of one stream's launches, summed per kernel name (a mark
+// named "begin" opens each call). Writes up to max entries; returns the number of kernel names.
+int frt_timing_end(char* names, int name_len, double* total_ms, int* launches, int max) {
+    Timing& t = g_timing;
+    t.on = false;
+    if (!t.marks.empty()) FRT_HIP(hipEventSynchronize(t.marks.back().second));
+    std::map<std::string, std::pair<double, int>> acc;
+    std::vector<std::string> order;
+    for (size_t i = 1; i < t.marks.size(); ++i) {
+        const std::string& k = t.marks[i].first;
+        if (k == "begin") continue;
+        float ms = 0.0f;
+        FRT_HIP(hipEventElapsedTime(&ms, t.marks[i - 1].second, t.marks[i].second));
+        if (!acc.count(k)) order.push_back(k);
+        acc[k].first += ms;
+        acc[k].second += 1;
+    }
+    int n = 0;
+    for (const auto& k : order) {
+        if (n >= max) break;
+        std::snprintf(names + size_t(n) * name_len, size_t(name_len), "%s", k.c_str());
+        total_ms[n] = acc[k].first;
+        launches[n] = acc[k].second;
+        ++n;
+    }
+    t.marks.clear();
+    return n;
+}
 const char* frt_version(void) { return "flashrt-mi355x 0.1 (gfx950)"; }
 
 size_t frt_q2_mat_bytes(int rows, int cols) { return mat_bytes(rows, cols); }
@@ -149,7 +213,7 @@ int frt_moe_route_topk(void* stream, const float* logits, int T, int E, int k, i
 
 int frt_router_logits(void* stream, const float* x, int T, const float* W, const float* bias, const float* gate_w,
                       int E, int n, float* logits, float* gate) {
-    return router_logits(x, T, W, bias, gate_w, E, n, logits, gate, static_cast<hipStream_t>(stream));
+    return router_logits(x, T, W, bias, gate_w, E, n, logits, gate, static_cast<hipStream_t>(stream), 0, nullptr, nullptr);
 }
 
 int frt_quantize_q8(void* stream, const float* x, int rows, int n, int8_t* xq, float* xd) {
@@ -206,16 +270,32 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     hipStream_t s = static_cast<hipStream_t>(stream);
     int32_t* ids_o = ids ? ids : w.ids;
     float* wts_o = wts ? wts : w.wts;
-    if (int rc = router_logits(x, T, L->router_w, L->router_bias, L->gate_w, E, n, w.logits, w.gate, s)) return rc;
-    if (T <= kDecodeMaxT) {
+    const int norm = (L->flags & FRT_LAYER_NORM_INPUT) ? 1 : 0;
+    timing_mark(s, "begin");
+    if (T <= kDecodeMaxT && T * K <= 63) {
         if (int rc = dec_check(T, K, n, ff)) return rc;
-        if (int rc = quantize_q8(x, T, n, w.xq, w.xd, nullptr, s)) return rc;
+        // router logits, the shared gate, the RMS scale and Q8_0 of the input in one launch
+        if (int rc = router_logits(x, T, L->router_w, L->router_bias, L->gate_w, E, n, w.logits, w.gate, s, norm, w.xq,
+                                   w.xd))
+            return rc;
+        timing_mark(s, "router_quant");
         return dec_moe(w.logits, w.gate, T, E, K, L->experts, L->stride, L->shared, w.xq, w.xd, n, ff, ids_o, wts_o,
                        counts, resid, out, w.rest, s);
     }
     if (int rc = pf_check(T, K, n, ff, E)) return rc;
+    const float* xin = x;
+    if (norm) {
+        if (int rc = rmsnorm(x, T, n, w.u, s)) return rc;
+        xin = w.u;
+        timing_mark(s, "rmsnorm");
+    }
+    if (int rc = router_logits(xin, T, L->router_w, L->router_bias, L->gate_w, E, n, w.logits, w.gate, s, 0, nullptr,
+                               nullptr))
+        return rc;
+    timing_mark(s, "router");
     if (int rc = route_topk(s, w.logits, T, E, K, ids_o, wts_o, counts, nullptr, 1 << 30)) return rc;
-    return pf_moe(L->experts, L->stride, E, L->shared, n, ff, x, ids_o, wts_o, w.gate, T, K, resid, out, w.rest,
+    timing_mark(s, "route_topk");
+    return pf_moe(L->experts, L->stride, E, L->shared, n, ff, xin, ids_o, wts_o, w.gate, T, K, resid, out, w.rest,
                   w.rest_bytes, s);
 }
 

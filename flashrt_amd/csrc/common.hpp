@@ -46,11 +46,16 @@ int set_error(int code, const char* fmt, ...);
                                                       hipGetErrorString(e_));                      \
     } while (0)
 
+// Per-kernel timing (off by default): between launches the library records a hipEvent on the
+// launch stream; frt_timing_end() turns consecutive events into per-kernel durations. Not for use
+// under graph capture.
+void timing_mark(hipStream_t stream, const char* kernel);
+
 inline size_t up256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // ---- device helpers
 
-__device__ inline float h2f(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
+__device__ __forceinline__ float h2f(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 
 // fp32 -> fp16 bits, round to nearest even with subnormals, overflow to inf, NaN kept quiet
 // (core/fp16.hpp:32-50 semantics), in integer operations: the compiler cannot fuse the rounding
@@ -77,20 +82,64 @@ __host__ __device__ inline uint16_t f32_to_f16_bits(float f) {
 }
 
 // fp16 round trip of a float (round to nearest even)
-__device__ inline float f16_round(float x) { return h2f(f32_to_f16_bits(x)); }
+__device__ __forceinline__ float f16_round(float x) { return h2f(f32_to_f16_bits(x)); }
 
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+// ---- cross-lane steps on DPP (no LDS round trip). After k pairwise steps every block of 2^k
+// lanes holds one value, so the mirror permutations pair whole blocks exactly like an xor would.
+#define FRT_DPP(v, ctrl) __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, true))
+#define FRT_DPP_ROWS(old, v, ctrl, rows)                                                                    \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, (old)), __builtin_bit_cast(int, (v)), \
+                                                          (ctrl), (rows), 0xF, false))
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;   // lane i <-> 7-i within 8
+constexpr int kDppMirror = 0x140;       // lane i <-> 15-i within 16
+constexpr int kDppBcast15 = 0x142;      // lane 15 of row r to row r+1
+constexpr int kDppBcast31 = 0x143;      // lane 31 to rows 2 and 3
+
+// Sum over the wave as the adjacent pairwise tree ((v0+v1)+(v2+v3))+... of the 64 lane values
+// (the canonical order of the router logits and the RMS norm); every lane gets the total.
+__device__ __forceinline__ float wave_sum_tree(float v) {
+    v = v + FRT_DPP(v, kDppXor1);
+    v = v + FRT_DPP(v, kDppXor2);
+    v = v + FRT_DPP(v, kDppHalfMirror);
+    v = v + FRT_DPP(v, kDppMirror);
+    v = v + FRT_DPP_ROWS(-0.0f, v, kDppBcast15, 0xA);   // rows 1, 3 += rows 0, 2 (x + -0 == x)
+    v = v + FRT_DPP_ROWS(-0.0f, v, kDppBcast31, 0xC);   // rows 2, 3 += row 1
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+// Sum of the lane values within aligned groups of G lanes (G = 2, 4, 8, 16 or 32), the same
+// pairwise tree; the group total is in the group's last lane (and, for G <= 16, in every lane).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    v = v + FRT_DPP(v, kDppXor1);
+    if (G >= 4) v = v + FRT_DPP(v, kDppXor2);
+    if (G >= 8) v = v + FRT_DPP(v, kDppHalfMirror);
+    if (G >= 16) v = v + FRT_DPP(v, kDppMirror);
+    if (G >= 32) v = v + FRT_DPP_ROWS(-0.0f, v, kDppBcast15, 0xA);
     return v;
 }
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, FRT_DPP(v, kDppXor1));
+    v = fmaxf(v, FRT_DPP(v, kDppXor2));
+    v = fmaxf(v, FRT_DPP(v, kDppHalfMirror));
+    v = fmaxf(v, FRT_DPP(v, kDppMirror));
+    v = fmaxf(v, FRT_DPP_ROWS(-INFINITY, v, kDppBcast15, 0xA));
+    v = fmaxf(v, FRT_DPP_ROWS(-INFINITY, v, kDppBcast31, 0xC));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
-__device__ inline int wave_sum_i(int v) {
-#pragma unroll
+// max within aligned groups of 32 lanes (lanes 0-31 and 32-63), in every lane of the group
+__device__ __forceinline__ float half_max(float v) {
+    v = fmaxf(v, FRT_DPP(v, kDppXor1));
+    v = fmaxf(v, FRT_DPP(v, kDppXor2));
+    v = fmaxf(v, FRT_DPP(v, kDppHalfMirror));
+    v = fmaxf(v, FRT_DPP(v, kDppMirror));
+    v = fmaxf(v, FRT_DPP_ROWS(-INFINITY, v, kDppBcast15, 0xA));   // rows 1, 3 hold the half maxima
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    return (threadIdx.x & 32) ? b : a;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
     return v;
 }
@@ -99,11 +148,11 @@ __device__ inline int wave_sum_i(int v) {
 // d = amax/127 (stored fp16-rounded), id = 1/d from the unrounded d, q = roundf(x * id).
 // Division and the products are single correctly rounded IEEE operations (hipcc's default
 // correctly rounded fp32 divide), so the codes equal the CPU's bit for bit.
-__device__ inline int q8_code(float x, float id) { return int(roundf(x * id)); }
-__device__ inline float q8_scale(float amax) { return amax / 127.0f; }
-__device__ inline float q8_inv(float d) { return d != 0.0f ? 1.0f / d : 0.0f; }
+__device__ __forceinline__ int q8_code(float x, float id) { return int(roundf(x * id)); }
+__device__ __forceinline__ float q8_scale(float amax) { return amax / 127.0f; }
+__device__ __forceinline__ float q8_inv(float d) { return d != 0.0f ? 1.0f / d : 0.0f; }
 
 // 4 x int8 dot with int32 accumulate (v_dot4_i32_i8)
-__device__ inline int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 }  // namespace frt

@@ -4,9 +4,12 @@
 // every token that selected it, arch/qwen4exp/moe_fast.cu:195-355), in ascending expert id, the
 // shared expert last. Entry c-slots (entry u, token j) are numbered compactly (base[u] + j).
 //
-//   k_dec_route   routing of the window (topk_wave), the entry list, sigmoid of the shared gate
-//   k_dec_gateup  per (32 ff rows, entry): gate and up rows of every token of the entry, SwiGLU,
-//                 and Q8_0 of that 32-row block of h (quant/q2_0/moe_cpu.cpp:43-61 phase A)
+//   k_dec_route_gateup  per (32 ff rows, entry): every workgroup routes the window itself (top-k
+//                 of each token, topk.hpp) and builds the entry list in LDS, so routing costs no
+//                 launch; then gate and up rows of every token of its entry, SwiGLU, and Q8_0 of
+//                 that 32-row block of h (quant/q2_0/moe_cpu.cpp:43-61 phase A). Workgroup (0, 0)
+//                 publishes ids, weights and the entry list.
+//   k_dec_gateup  the same body for moe_hits, entries from k_hits_group
 //   k_dec_down    per 8 output rows: down rows of every entry, then the weighted sum per token in
 //                 expert order plus shared * sigmoid(gate) (moe_cpu.cpp:63-80 phase B and
 //                 moe_ref.cu:90-97); or, for moe_hits, the per-slot outputs yh.
@@ -15,6 +18,7 @@
 // & 0x03030303 lines up with activation dword 4s + w (the planar layout), so 16 v_dot4_i32_i8
 // give sum(q * a) for both 32-halves exactly; the -1 offset uses the halves' code sums.
 #include "common.hpp"
+#include "topk.hpp"
 
 namespace frt {
 
@@ -32,153 +36,119 @@ constexpr int kDecMaxT = 4;
 
 namespace {
 
-__device__ inline float sigmoidf_(float g) { return 1.0f / (1.0f + expf(-g)); }
+__device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + expf(-g)); }
 
-// routing keys: orderable logit bits << 32 | (0xffffffff - id); the maximum is the largest logit,
-// lowest id on ties (the selection of route.hip, repeated here so one launch routes the window)
-__device__ inline uint64_t dkey(float l, int e) {
-    uint32_t b = __builtin_bit_cast(uint32_t, l);
-    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return (uint64_t(b) << 32) | uint64_t(0xffffffffu - uint32_t(e));
-}
+// ---- the window's routing and its entry list, built in LDS by one 256-thread workgroup: wave t
+// routes token t (topk_wave); then wave 0, one lane per selection, orders the distinct experts
+// ascending (first occurrences ranked by id), the shared expert last, and numbers the compact slots.
+// Needs T * K <= 63. Returns the number of entries (every thread).
+struct WinLds {
+    DecEntry ent[64];
+    int32_t ids[kDecMaxT][32];
+    float w[kDecMaxT][32];
+    float cand_v[kDecMaxT][64];
+    int32_t cand_id[kDecMaxT][64];
+    int32_t n_ent;
+};
 
 template <int V>
-__global__ void __launch_bounds__(256) k_dec_route(const float* __restrict__ logits, const float* __restrict__ gate,
-                                                   int T, int E, int K, const uint8_t* __restrict__ arena, size_t stride,
-                                                   const uint8_t* __restrict__ shared_blob, int32_t* __restrict__ ids,
-                                                   float* __restrict__ wts, DecEntry* __restrict__ ent,
-                                                   int32_t* __restrict__ n_ent, uint32_t* counts) {
-    __shared__ int32_t s_ids[kDecMaxT][32];
-    __shared__ float s_w[kDecMaxT][32];
-    __shared__ __align__(16) uint8_t s_mask[1024];
-    __shared__ int32_t s_pos[1024];
-    __shared__ int32_t s_wsum[16];
+__device__ __forceinline__ int window_entries(const float* __restrict__ logits, const float* __restrict__ gate, int T,
+                                              int E, int K, const uint8_t* __restrict__ arena, size_t stride,
+                                              const uint8_t* __restrict__ shared_blob, WinLds& L) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave < T) {
-        const float* l = logits + size_t(wave) * E;
-        float v[V];
-        uint64_t key[V];
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-            const int e = 64 * i + lane;
-            v[i] = e < E ? l[e] : -INFINITY;
-            key[i] = e < E ? dkey(v[i], e) : 0;
-        }
-        int my_id = -1;
-        float my_l = 0.0f;
-        for (int k = 0; k < K; ++k) {
-            uint64_t best = 0;
-#pragma unroll
-            for (int i = 0; i < V; ++i) best = key[i] > best ? key[i] : best;
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const uint32_t lo = __shfl_xor(uint32_t(best), o, 64), hi = __shfl_xor(uint32_t(best >> 32), o, 64);
-                const uint64_t w = (uint64_t(hi) << 32) | lo;
-                best = w > best ? w : best;
+    if (T == 1) {   // one token: the entries are its K experts by ascending id, then the shared expert
+        if (wave == 0) {
+            const float g = gate[0];
+            int sel_id;
+            float sel_l, mx, se;
+            topk_select<V>(logits, E, K, L.cand_v[0], L.cand_id[0], sel_id, sel_l, mx, se);
+            const float w = topk_weight(sel_l, mx, wave_sum_tree(se), K);
+            int rank = 0;
+            for (int j = 0; j < K; ++j) rank += __builtin_amdgcn_readlane(sel_id, j) < sel_id ? 1 : 0;
+            if (lane < K) {
+                L.ids[0][lane] = sel_id;
+                L.w[0][lane] = w;
+                DecEntry& d = L.ent[rank];
+                d.blob = arena + size_t(sel_id) * stride;
+                d.ntok = 1;
+                d.base = rank;
+                d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
+                d.slot[0] = lane;
+                d.slot[1] = d.slot[2] = d.slot[3] = -1;
+                d.w[0] = w;
+                d.w[1] = d.w[2] = d.w[3] = 0.0f;
+            } else if (lane == K) {
+                DecEntry& d = L.ent[K];
+                d.blob = shared_blob;
+                d.ntok = 1;
+                d.base = K;
+                d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
+                d.slot[0] = d.slot[1] = d.slot[2] = d.slot[3] = -1;
+                d.w[0] = sigmoidf_(g);
+                d.w[1] = d.w[2] = d.w[3] = 0.0f;
+                L.n_ent = K + 1;
             }
-            const int id = int(0xffffffffu - uint32_t(best));
-#pragma unroll
-            for (int i = 0; i < V; ++i)
-                if (key[i] == best) key[i] = 0;
-            if (lane == k) {
-                my_id = id;
-                my_l = l[id];
+        }
+        __syncthreads();
+        return K + 1;
+    }
+    if (wave < T) topk_wave<V>(logits + size_t(wave) * E, E, K, L.ids[wave], L.w[wave], L.cand_v[wave], L.cand_id[wave]);
+    __syncthreads();
+    if (wave == 0) {
+        const int S = T * K;
+        const int e = lane < S ? L.ids[lane / K][lane % K] : 0x7fffffff;
+        bool first = lane < S;
+        for (int j = 0; j < S; ++j) {
+            const int ej = __builtin_amdgcn_readlane(e, j);
+            if (j < lane && ej == e) first = false;
+        }
+        const uint64_t fm = __ballot(first);
+        int rank = 0;
+        for (int j = 0; j < S; ++j) {
+            const int ej = __builtin_amdgcn_readlane(e, j);
+            if (((fm >> j) & 1ull) && ej < e) ++rank;
+        }
+        const int U = __popcll(fm);
+        if (first) {
+            DecEntry& d = L.ent[rank];
+            d.blob = arena + size_t(e) * stride;
+            int nt = 0;
+            for (int j = 0; j < S; ++j) {
+                const int ej = __builtin_amdgcn_readlane(e, j);
+                if (ej == e) {
+                    d.tok[nt] = j / K;
+                    d.slot[nt] = j % K;
+                    d.w[nt] = L.w[j / K][j % K];
+                    ++nt;
+                }
+            }
+            d.ntok = nt;
+            for (int q = nt; q < 4; ++q) {
+                d.tok[q] = 0;
+                d.slot[q] = -1;
+                d.w[q] = 0.0f;
             }
         }
-        const float mx = __shfl(my_l, 0, 64);
-        double s = 0.0;
-#pragma unroll
-        for (int i = 0; i < V; ++i)
-            if (64 * i + lane < E) s += double(expf(v[i] - mx));
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-        float p = 0.0f;
-        if (lane < K) p = float(double(expf(my_l - mx)) / s);
-        float ws = 0.0f;
-        for (int k = 0; k < K; ++k) ws += __shfl(p, k, 64);
-        ws = fmaxf(ws, 6.103515625e-5f);
-        if (lane < K) {
-            const float w = p / ws;
-            ids[wave * K + lane] = my_id;
-            wts[wave * K + lane] = w;
-            s_ids[wave][lane] = my_id;
-            s_w[wave][lane] = w;
-            if (counts) atomicAdd(counts + my_id, 1u);
-        }
-    }
-    for (int e = threadIdx.x; e < E; e += blockDim.x) s_mask[e] = 0;
-    __syncthreads();
-    if (threadIdx.x < T * K) {
-        const int t = threadIdx.x / K, k = threadIdx.x % K;
-        atomicOr(reinterpret_cast<unsigned int*>(s_mask) + s_ids[t][k] / 4, 1u << (8 * (s_ids[t][k] % 4) + t));
-    }
-    __syncthreads();
-    // exclusive scan of "expert used" over E (<= 1024) with 256 threads: 4 experts per thread
-    int c = 0;
-    for (int i = 0; i < 4; ++i) {
-        const int e = threadIdx.x * 4 + i;
-        c += (e < E && s_mask[e]) ? 1 : 0;
-    }
-    int incl = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-    }
-    if (lane == 63) s_wsum[wave] = incl;
-    __syncthreads();
-    int before = 0;
-    for (int w = 0; w < wave; ++w) before += s_wsum[w];
-    int pos = before + incl - c;
-    for (int i = 0; i < 4; ++i) {
-        const int e = threadIdx.x * 4 + i;
-        if (e < E && s_mask[e]) s_pos[e] = pos++;
-    }
-    const int U = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
-    __syncthreads();
-    // entry per used expert: tokens ascending; compact bases follow entry order
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        const uint32_t m = s_mask[e];
-        if (!m) continue;
-        DecEntry d{};
-        d.blob = arena + size_t(e) * stride;
-        int j = 0;
-        for (int t = 0; t < T; ++t)
-            if (m & (1u << t)) {
-                d.tok[j] = t;
-                int k = 0;
-                while (s_ids[t][k] != e) ++k;
-                d.slot[j] = k;
-                d.w[j] = s_w[t][k];
-                ++j;
+        if (lane < 4) {   // the shared expert, every token, weight sigmoid(gate)
+            DecEntry& d = L.ent[U];
+            if (lane == 0) {
+                d.blob = shared_blob;
+                d.ntok = T;
             }
-        d.ntok = j;
-        for (; j < 4; ++j) {
-            d.tok[j] = 0;
-            d.slot[j] = -1;
-            d.w[j] = 0.0f;
+            d.tok[lane] = lane < T ? lane : 0;
+            d.slot[lane] = -1;
+            d.w[lane] = lane < T ? sigmoidf_(gate[lane]) : 0.0f;
         }
-        d.base = 0;
-        ent[s_pos[e]] = d;
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+        const int nt = lane <= U ? L.ent[lane].ntok : 0;
+        int tot;
+        const int base = wave_excl_scan(nt, &tot);
+        if (lane <= U) L.ent[lane].base = base;
+        if (lane == 0) L.n_ent = U + 1;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        DecEntry d{};
-        d.blob = shared_blob;
-        d.ntok = T;
-        for (int t = 0; t < 4; ++t) {
-            d.tok[t] = t < T ? t : 0;
-            d.slot[t] = -1;
-            d.w[t] = t < T ? sigmoidf_(gate[t]) : 0.0f;
-        }
-        ent[U] = d;
-        int b = 0;
-        for (int u = 0; u <= U; ++u) {
-            ent[u].base = b;
-            b += ent[u].ntok;
-        }
-        *n_ent = U + 1;
-    }
+    return L.n_ent;
 }
 
 // ---- moe_hits grouping (moe_fast.cu:195-232): distinct blob pointers across the window's hit
@@ -221,19 +191,35 @@ __global__ void k_hits_group(const uint8_t* const* __restrict__ hit_ptr, const i
 // ---- gate + up for 32 ff rows of one entry. NB = n / 64 blocks per row. 256 threads.
 // RPW rows per wave pass (64 / NB when NB divides 64, else 1 with NB <= 64 lanes live).
 template <int NB>
-__global__ void __launch_bounds__(256) k_dec_gateup(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
-                                                    const int8_t* __restrict__ xq, const float* __restrict__ xd, int n,
-                                                    int ff, int8_t* __restrict__ hq, float* __restrict__ hd) {
+__device__ __forceinline__ void gateup_body(const DecEntry& e, const int8_t* __restrict__ xq, const float* __restrict__ xd, int n,
+                            int ff, int8_t* __restrict__ hq, float* __restrict__ hd, float (*hrow)[32]) {
     constexpr int RPW = (64 % NB == 0) ? 64 / NB : 1;
     constexpr int PASSES = 8 / RPW;   // 8 rows per wave, 4 waves = 32 rows
-    const int u = blockIdx.y;
-    if (u >= *n_ent) return;
-    __shared__ float hrow[kDecMaxT][32];
-    const DecEntry e = ent[u];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rsub = lane / NB, b = lane % NB;
     const bool live = rsub < RPW;
     const int nb = NB;
+    const size_t mb = mat_bytes(ff, n);
+    const uint8_t* gcodes = e.blob;
+    const uint16_t* gscal = reinterpret_cast<const uint16_t*>(e.blob + size_t(ff) * nb * 16);
+    const uint8_t* ucodes = e.blob + mb;
+    const uint16_t* uscal = reinterpret_cast<const uint16_t*>(e.blob + mb + size_t(ff) * nb * 16);
+    // issue every pass's loads first
+    uint4 cg[PASSES], cu[PASSES];
+    uint16_t sg[PASSES], su[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int r = blockIdx.x * 32 + wave * 8 + p * RPW + rsub;
+        if (live) {
+            cg[p] = *reinterpret_cast<const uint4*>(gcodes + (size_t(r) * nb + b) * 16);
+            cu[p] = *reinterpret_cast<const uint4*>(ucodes + (size_t(r) * nb + b) * 16);
+            sg[p] = gscal[size_t(r) * nb + b];
+            su[p] = uscal[size_t(r) * nb + b];
+        } else {
+            cg[p] = cu[p] = make_uint4(0, 0, 0, 0);
+            sg[p] = su[p] = 0;
+        }
+    }
     // this lane's activation block for each token: 16 dwords, scales, and the halves' code sums
     int xa[kDecMaxT][16];
     float xd0[kDecMaxT], xd1[kDecMaxT];
@@ -266,27 +252,6 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const DecEntry* __restrict__
             xs0[j] = xs1[j] = 0;
         }
     }
-    const size_t mb = mat_bytes(ff, n);
-    const uint8_t* gcodes = e.blob;
-    const uint16_t* gscal = reinterpret_cast<const uint16_t*>(e.blob + size_t(ff) * nb * 16);
-    const uint8_t* ucodes = e.blob + mb;
-    const uint16_t* uscal = reinterpret_cast<const uint16_t*>(e.blob + mb + size_t(ff) * nb * 16);
-    // issue every pass's loads first
-    uint4 cg[PASSES], cu[PASSES];
-    uint16_t sg[PASSES], su[PASSES];
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-        const int r = blockIdx.x * 32 + wave * 8 + p * RPW + rsub;
-        if (live) {
-            cg[p] = *reinterpret_cast<const uint4*>(gcodes + (size_t(r) * nb + b) * 16);
-            cu[p] = *reinterpret_cast<const uint4*>(ucodes + (size_t(r) * nb + b) * 16);
-            sg[p] = gscal[size_t(r) * nb + b];
-            su[p] = uscal[size_t(r) * nb + b];
-        } else {
-            cg[p] = cu[p] = make_uint4(0, 0, 0, 0);
-            sg[p] = su[p] = 0;
-        }
-    }
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const uint32_t wg[4] = {cg[p].x, cg[p].y, cg[p].z, cg[p].w};
@@ -316,63 +281,103 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const DecEntry* __restrict__
             ag[j] = fg * dg;
             au[j] = fu * du;
         }
-        // sum over the row's NB lanes
+        // sum over the row's NB lanes (DPP pairwise tree); the total lands in the group's last lane
 #pragma unroll
         for (int j = 0; j < kDecMaxT; ++j) {
             if (j >= e.ntok) continue;
             float a = ag[j], c = au[j];
+            bool writer;
             if (RPW > 1) {
-#pragma unroll
-                for (int o = NB / 2; o > 0; o >>= 1) {
-                    a += __shfl_xor(a, o, 64);
-                    c += __shfl_xor(c, o, 64);
-                }
+                a = group_sum<NB>(a);
+                c = group_sum<NB>(c);
+                writer = live && b == NB - 1;
             } else {
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) {
-                    a += __shfl_xor(a, o, 64);
-                    c += __shfl_xor(c, o, 64);
-                }
+                a = wave_sum_tree(a);
+                c = wave_sum_tree(c);
+                writer = lane == 0;
             }
-            if (live && b == 0) hrow[j][wave * 8 + p * RPW + rsub] = a / (1.0f + expf(-a)) * c;
+            if (writer) hrow[j][wave * 8 + p * RPW + rsub] = a / (1.0f + expf(-a)) * c;
         }
     }
     __syncthreads();
     // Q8_0 of the 32-row block of h for each token: wave w < ntok, lanes 0..31
-    if (wave < e.ntok && lane < 32) {
-        const float v = hrow[wave][lane];
-        float am = fabsf(v);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    if (wave < e.ntok) {   // the whole wave takes part in the DPP max; lanes 0..31 hold the block
+        const float v = lane < 32 ? hrow[wave][lane] : 0.0f;
+        const float am = half_max(fabsf(v));
         const float d = q8_scale(am);
         const float id = q8_inv(d);
         const int c = e.base + wave;
-        hq[size_t(c) * ff + blockIdx.x * 32 + lane] = int8_t(q8_code(v, id));
+        if (lane < 32) hq[size_t(c) * ff + blockIdx.x * 32 + lane] = int8_t(q8_code(v, id));
         if (lane == 0) hd[size_t(c) * (ff / kQ8) + blockIdx.x] = f16_round(d);
     }
+}
+
+template <int NB>
+__global__ void __launch_bounds__(256) k_dec_gateup(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
+                                                    const int8_t* __restrict__ xq, const float* __restrict__ xd, int n,
+                                                    int ff, int8_t* __restrict__ hq, float* __restrict__ hd) {
+    __shared__ float hrow[kDecMaxT][32];
+    if (int(blockIdx.y) >= *n_ent) return;
+    const DecEntry e = ent[blockIdx.y];
+    gateup_body<NB>(e, xq, xd, n, ff, hq, hd, hrow);
+}
+
+template <int NB, int V>
+__global__ void __launch_bounds__(256) k_dec_route_gateup(const float* __restrict__ logits,
+                                                          const float* __restrict__ gate, int T, int E, int K,
+                                                          const uint8_t* __restrict__ arena, size_t stride,
+                                                          const uint8_t* __restrict__ shared_blob,
+                                                          const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                          int n, int ff, int8_t* __restrict__ hq,
+                                                          float* __restrict__ hd, DecEntry* __restrict__ ent_out,
+                                                          int32_t* __restrict__ n_ent_out, int32_t* __restrict__ ids,
+                                                          float* __restrict__ wts, uint32_t* counts) {
+    __shared__ WinLds L;
+    __shared__ float hrow[kDecMaxT][32];
+    const int U1 = window_entries<V>(logits, gate, T, E, K, arena, stride, shared_blob, L);
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+        for (int i = threadIdx.x; i < U1 * int(sizeof(DecEntry) / 4); i += blockDim.x)
+            reinterpret_cast<int32_t*>(ent_out)[i] = reinterpret_cast<const int32_t*>(L.ent)[i];
+        if (threadIdx.x < T * K) {
+            const int t = threadIdx.x / K, k = threadIdx.x % K;
+            ids[t * K + k] = L.ids[t][k];
+            wts[t * K + k] = L.w[t][k];
+            if (counts) atomicAdd(counts + L.ids[t][k], 1u);
+        }
+        if (threadIdx.x == 0) *n_ent_out = U1;
+    }
+    if (int(blockIdx.y) >= U1) return;
+    const DecEntry e = L.ent[blockIdx.y];
+    gateup_body<NB>(e, xq, xd, n, ff, hq, hd, hrow);
 }
 
 // ---- down for 8 output rows x every entry, then the combine. NBF = ff / 64 (8 lanes per row
 // when ff = 512). 256 threads; wave w takes entries w, w + 4, ...
 template <int NBF>
-__global__ void __launch_bounds__(256) k_dec_down(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
+__global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent, const int32_t* __restrict__ n_ent,
                                                   const int8_t* __restrict__ hq, const float* __restrict__ hd, int n,
                                                   int ff, int T, int K, const float* __restrict__ resid,
-                                                  float* __restrict__ out, float* __restrict__ yh) {
+                                                  float* __restrict__ out, float* __restrict__ yh, int U_max,
+                                                  int S_max) {
     constexpr int RPP = 64 / NBF;   // rows per wave pass
     constexpr int RD = 8;           // rows per workgroup
     constexpr int PASSES = (RD + RPP - 1) / RPP;
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ DecEntry s_ent[64];
+    // the entry list, its length and the quantized hidden vectors are independent loads: issue them
+    // together (hq/hd for the largest possible slot count S_max), then one barrier
     const int U = *n_ent;
-    if (U == 0) return;
-    const int S = ent[U - 1].base + ent[U - 1].ntok;   // compact slots
-    int8_t* sh_q = reinterpret_cast<int8_t*>(smem);                       // [S][ff]
-    float* sh_d = reinterpret_cast<float*>(smem + size_t(S) * ff);        // [S][ff/32]
-    float* sh_y = sh_d + size_t(S) * (ff / kQ8);                           // [S][RD]
-    for (int i = threadIdx.x; i < S * ff / 16; i += blockDim.x)
+    for (int i = threadIdx.x; i < U_max * int(sizeof(DecEntry) / 4); i += blockDim.x)
+        reinterpret_cast<int32_t*>(s_ent)[i] = reinterpret_cast<const int32_t*>(ent)[i];
+    int8_t* sh_q = reinterpret_cast<int8_t*>(smem);                        // [S_max][ff]
+    float* sh_d = reinterpret_cast<float*>(smem + size_t(S_max) * ff);    // [S_max][ff/32]
+    float* sh_y = sh_d + size_t(S_max) * (ff / kQ8);                       // [S_max][RD]
+    for (int i = threadIdx.x; i < S_max * ff / 16; i += blockDim.x)
         reinterpret_cast<int4*>(sh_q)[i] = reinterpret_cast<const int4*>(hq)[i];
-    for (int i = threadIdx.x; i < S * (ff / kQ8); i += blockDim.x) sh_d[i] = hd[i];
+    for (int i = threadIdx.x; i < S_max * (ff / kQ8); i += blockDim.x) sh_d[i] = hd[i];
     __syncthreads();
+    if (U == 0) return;
+    ent = s_ent;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rsub = lane / NBF, b = lane % NBF;
     const bool live = rsub < RPP;
@@ -440,9 +445,8 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* __restrict__ e
                                         float(q1 - s1) * sh_d[size_t(c) * (ff / kQ8) + 2 * b + 1];
                         part = f * dw;
                     }
-                    if ((NBF & (NBF - 1)) == 0) {
-#pragma unroll
-                        for (int o = NBF / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+                    if ((NBF & (NBF - 1)) == 0 && NBF <= 16) {
+                        part = group_sum<(NBF <= 16 ? NBF : 16)>(part);
                     } else {
                         // segments of NBF lanes: gather the row's partials from its first lane
                         float acc = 0.0f;
@@ -456,6 +460,7 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* __restrict__ e
     }
     __syncthreads();
     if (yh) {   // moe_hits: per-slot outputs
+        const int S = ent[U - 1].base + ent[U - 1].ntok;
         for (int i = threadIdx.x; i < S * RD; i += blockDim.x) {
             const int c = i / RD, rl = i % RD;
             int u = 0;
@@ -514,35 +519,30 @@ static DecScratch dec_carve(void* base, int T, int K, int ff) {
     return s;
 }
 
-static int dec_gateup_down(const DecScratch& s, int max_ent, const int8_t* xq, const float* xd, int n, int ff, int T,
-                           int K, const float* resid, float* out, float* yh, hipStream_t stream) {
-    const int nb = n / kBlock, nbf = ff / kBlock;
-    dim3 g1(ff / 32, max_ent);
-#define FRT_GU(NBV) \
-    case NBV: k_dec_gateup<NBV><<<g1, 256, 0, stream>>>(s.ent, s.n_ent, xq, xd, n, ff, s.hq, s.hd); break;
-    switch (nb) {
-        FRT_GU(16) FRT_GU(32) FRT_GU(40) FRT_GU(48) FRT_GU(64)
-        default: return set_error(kErrShape, "decode: n=%d unsupported (n/64 in {16,32,40,48,64})", n);
-    }
-#undef FRT_GU
-    const int S = T * (K + 1);
+static int dec_down(const DecScratch& s, int n, int ff, int T, int K, const float* resid, float* out, float* yh,
+                    hipStream_t stream) {
+    const int nbf = ff / kBlock;
+    const int S = T * (K + 1);                         // compact slots at most (the shared expert's included)
+    const int U_max = T * K + 1 < 64 ? T * K + 1 : 64;   // entries at most
     const size_t smem = size_t(S) * ff + size_t(S) * (ff / kQ8) * 4 + size_t(S) * 8 * 4;
 #define FRT_DN(NBFV)                                                                                           \
     case NBFV:                                                                                                 \
-        k_dec_down<NBFV><<<n / 8, 256, smem, stream>>>(s.ent, s.n_ent, s.hq, s.hd, n, ff, T, K, resid, out, yh); \
+        k_dec_down<NBFV><<<n / 8, 256, smem, stream>>>(s.ent, s.n_ent, s.hq, s.hd, n, ff, T, K, resid, out, yh,  \
+                                                       U_max, S);                                               \
         break;
     switch (nbf) {
         FRT_DN(4) FRT_DN(8) FRT_DN(10) FRT_DN(16)
         default: return set_error(kErrShape, "decode: ff=%d unsupported (ff/64 in {4,8,10,16})", ff);
     }
 #undef FRT_DN
-    FRT_LAUNCHED("decode experts");
+    timing_mark(stream, "dec_down");
+    FRT_LAUNCHED("decode down");
     return kOk;
 }
 
 int dec_check(int T, int K, int n, int ff) {
     if (T < 1 || T > kDecMaxT) return set_error(kErrShape, "decode: T=%d (1..4)", T);
-    if (K < 1 || K > 32) return set_error(kErrShape, "decode: K=%d", K);
+    if (K < 1 || K > 32 || T * K > 63) return set_error(kErrShape, "decode: K=%d with T=%d (T*K <= 63)", K, T);
     if (n % 64 || ff % 64 || n % 8 || ff % 32) return set_error(kErrShape, "decode: n=%d ff=%d", n, ff);
     return kOk;
 }
@@ -554,11 +554,24 @@ int dec_moe(const float* logits, const float* gate, int T, int E, int K, const u
     if (int rc = dec_check(T, K, n, ff)) return rc;
     if (E > 1024) return set_error(kErrShape, "decode: E=%d", E);
     const DecScratch s = dec_carve(scratch, T, K, ff);
-    if (E <= 512)
-        k_dec_route<8><<<1, 256, 0, stream>>>(logits, gate, T, E, K, arena, stride, shared_blob, ids, wts, s.ent, s.n_ent, counts);
-    else
-        k_dec_route<16><<<1, 256, 0, stream>>>(logits, gate, T, E, K, arena, stride, shared_blob, ids, wts, s.ent, s.n_ent, counts);
-    return dec_gateup_down(s, T * K + 1, xq, xd, n, ff, T, K, resid, out, nullptr, stream);
+    const int nb = n / kBlock;
+    dim3 g1(ff / 32, T * K + 1);
+#define FRT_RG(NBV, VV)                                                                                         \
+    k_dec_route_gateup<NBV, VV><<<g1, 256, 0, stream>>>(logits, gate, T, E, K, arena, stride, shared_blob, xq, xd, \
+                                                        n, ff, s.hq, s.hd, s.ent, s.n_ent, ids, wts, counts)
+#define FRT_RGN(NBV)                       \
+    case NBV:                              \
+        if (E <= 512) FRT_RG(NBV, 8);      \
+        else FRT_RG(NBV, 16);              \
+        break;
+    switch (nb) {
+        FRT_RGN(16) FRT_RGN(32) FRT_RGN(40) FRT_RGN(48) FRT_RGN(64)
+        default: return set_error(kErrShape, "decode: n=%d unsupported (n/64 in {16,32,40,48,64})", n);
+    }
+#undef FRT_RGN
+#undef FRT_RG
+    timing_mark(stream, "dec_route_gateup");
+    return dec_down(s, n, ff, T, K, resid, out, nullptr, stream);
 }
 
 // moe_hits (arch/qwen4exp/moe_fast.hpp:134-142): per-slot expert outputs for the window's hit lists.
@@ -567,7 +580,18 @@ int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const i
     if (int rc = dec_check(T, K, n, ff)) return rc;
     const DecScratch s = dec_carve(scratch, T, K, ff);
     k_hits_group<<<1, 64, 0, stream>>>(hit_ptr, hit_n, K, T, s.ent, s.n_ent);
-    return dec_gateup_down(s, T * K, xq, xd, n, ff, T, K, nullptr, nullptr, yh, stream);
+    timing_mark(stream, "hits_group");
+    const int nb = n / kBlock;
+    dim3 g1(ff / 32, T * K);
+#define FRT_GU(NBV) \
+    case NBV: k_dec_gateup<NBV><<<g1, 256, 0, stream>>>(s.ent, s.n_ent, xq, xd, n, ff, s.hq, s.hd); break;
+    switch (nb) {
+        FRT_GU(16) FRT_GU(32) FRT_GU(40) FRT_GU(48) FRT_GU(64)
+        default: return set_error(kErrShape, "decode: n=%d unsupported (n/64 in {16,32,40,48,64})", n);
+    }
+#undef FRT_GU
+    timing_mark(stream, "dec_gateup");
+    return dec_down(s, n, ff, T, K, nullptr, nullptr, yh, stream);
 }
 
 }  // namespace frt

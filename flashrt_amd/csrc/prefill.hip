@@ -50,7 +50,7 @@ __global__ void __launch_bounds__(256) k_pf_hist(const int32_t* __restrict__ ids
     for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[size_t(blockIdx.x) * E + e] = h[e];
 }
 
-__device__ int block_excl_scan(int v, int* total, int* ws) {
+__device__ __forceinline__ int block_excl_scan(int v, int* total, int* ws) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     int incl = v;
 #pragma unroll
@@ -158,7 +158,7 @@ __global__ void k_pf_place_shared(int T, int K, int32_t* __restrict__ tok_of, in
 // ---------------------------------------------------------------- GEMM pieces
 
 // A operand (8 fp16) of half h for one weight row's code dword g (see perm64 above), scaled by d.
-__device__ inline half8 dequant8(uint32_t cw, int h, _Float16 d) {
+__device__ __forceinline__ half8 dequant8(uint32_t cw, int h, _Float16 d) {
     const half2v one025 = {_Float16(1025.0f), _Float16(1025.0f)};
     const half2v dd = {d, d};
     half8 r;
@@ -174,19 +174,19 @@ __device__ inline half8 dequant8(uint32_t cw, int h, _Float16 d) {
     return r;
 }
 
-__device__ inline floatx4 mfma16(half8 a, half8 b) {
+__device__ __forceinline__ floatx4 mfma16(half8 a, half8 b) {
     const floatx4 z = {0.0f, 0.0f, 0.0f, 0.0f};
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, z, 0, 0, 0);
 }
 
 // position of element e (0..63) of a 64-block in the perm64 order
-__device__ inline int perm64_pos(int e) {
+__device__ __forceinline__ int perm64_pos(int e) {
     const int s = e >> 4, g = (e >> 2) & 3, c = e & 3;
     const int ci = c == 0 ? 0 : c == 1 ? 2 : c == 2 ? 1 : 3;
     return (s >> 1) * 32 + g * 8 + (s & 1) * 4 + ci;
 }
 
-__device__ inline float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 // ---------------------------------------------------------------- gate + up
 
@@ -290,9 +290,7 @@ __global__ void __launch_bounds__(256) k_pf_gateup(const uint8_t* __restrict__ a
         const int j = p >> 1, qb = p & 1;
         if (j >= cnt) continue;
         const float v = hbuf[j * 64 + qb * 32 + hl];
-        float am = fabsf(v);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 32));
+        const float am = half_max(fabsf(v));
         const float d = q8_scale(am);
         const float id = q8_inv(d);
         const size_t row = size_t(row0 + j);
@@ -489,13 +487,16 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
     int id_bits = 1;
     while ((1 << id_bits) < E) ++id_bits;
     if (int rc = quantize_q8(x, T, n, w.xq, w.xd, w.xq16, stream)) return rc;
+    timing_mark(stream, "pf_quant_x");
     k_pf_hist<<<nchunk, 256, size_t(E) * 4, stream>>>(ids, T * K, E, w.cnt);
     k_pf_scan<<<1, 1024, 0, stream>>>(w.cnt, nchunk, E, T, K, shared ? 1 : 0, w.bounds, w.tiles, w.n_tiles);
     k_pf_place<<<nchunk, 64, size_t(E) * 4, stream>>>(ids, T * K, K, E, id_bits, w.cnt, w.tok_of, w.slot_of);
     if (shared) k_pf_place_shared<<<(T + 255) / 256, 256, 0, stream>>>(T, K, w.tok_of, w.slot_of);
+    timing_mark(stream, "pf_dispatch");
     const int mt = pf_max_tiles(S, G);
     k_pf_gateup<<<dim3(ff / 64, mt), 256, 0, stream>>>(arena, stride, E, shared_blob, n, ff, w.xq16, w.xd, w.tok_of,
                                                        w.bounds, w.tiles, w.n_tiles, w.hq16, w.hd);
+    timing_mark(stream, "pf_gateup");
     const int nbf = ff / kBlock;
     const size_t smem = size_t(kTN) * (ff + 8) * 2 + size_t(kTN) * (ff / kQ8) * 4 + size_t(64) * nbf * 16 + size_t(64) * nbf * 2;
     if (yd_kind == 1) {
@@ -511,6 +512,7 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
                                                                   w.slot_of, w.bounds, w.tiles, w.n_tiles,
                                                                   static_cast<float*>(yd));
     }
+    timing_mark(stream, "pf_down");
     FRT_LAUNCHED("prefill experts");
     return kOk;
 }
@@ -535,6 +537,7 @@ int pf_moe(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blo
     if (w.bytes > ws_bytes) return set_error(kErrWorkspace, "prefill: workspace %zu < %zu", ws_bytes, w.bytes);
     if (int rc = pf_experts(arena, stride, E, shared_blob, n, ff, x, ids, T, K, w.yd, 0, w, stream)) return rc;
     k_pf_combine<float><<<dim3((n + 255) / 256, T), 256, 0, stream>>>(w.yd, ids, wts, gate, T, K, n, 1, resid, out);
+    timing_mark(stream, "pf_combine");
     FRT_LAUNCHED("prefill combine");
     return kOk;
 }

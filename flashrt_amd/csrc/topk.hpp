@@ -1,0 +1,258 @@
+// Top-k routing of one token by one wave64, and the canonical RMS scale, shared by the decode
+// and prefill kernels.
+//
+// Selection (arch/qwen4exp/moe_ref.cu:21-77 semantics; tests/test_route_topk.cpp:52-55 defines the
+// order): rank by logit descending, ties to the lower expert id (topk_select below).
+// Weights (moe_ref.cu:146-164): p = exp(l - max) / sum_e exp(l_e - max), w_k = p_k / max(sum of the
+// selected p in rank order, 2^-14). The sum over all experts is taken in float (pairwise tree); the
+// reference's double sum enters the weights only through the rounding of p (the common factor
+// cancels in w), which stays within the 1e-6 relative bound.
+#pragma once
+
+#include "common.hpp"
+
+namespace frt {
+
+template <int V>
+__device__ __forceinline__ void cas_desc(float (&v)[V], int (&id)[V], int i, int j) {
+    const bool sw = v[j] > v[i] || (v[j] == v[i] && id[j] < id[i]);
+    const float tv = sw ? v[j] : v[i], uv = sw ? v[i] : v[j];
+    const int ti = sw ? id[j] : id[i], ui = sw ? id[i] : id[j];
+    v[i] = tv;
+    v[j] = uv;
+    id[i] = ti;
+    id[j] = ui;
+}
+
+// odd-even transposition rounds (V rounds of disjoint compare-exchanges) sort V values
+template <int V>
+__device__ __forceinline__ void sort_desc(float (&v)[V], int (&id)[V]) {
+#pragma unroll
+    for (int r = 0; r < V; ++r)
+#pragma unroll
+        for (int i = r & 1; i + 1 < V; i += 2) cas_desc<V>(v, id, i, i + 1);
+}
+
+// Value of lane (lane ^ j) for j in {1, 2, 4, 8, 16, 32}: DPP quad_perm, ds_swizzle (xor within
+// 32 lanes) and the gfx950 permlane swaps; no LDS traffic.
+template <int J>
+__device__ __forceinline__ int lane_xor(int v) {
+    if constexpr (J == 1) return __builtin_amdgcn_mov_dpp(v, kDppXor1, 0xF, 0xF, true);
+    else if constexpr (J == 2) return __builtin_amdgcn_mov_dpp(v, kDppXor2, 0xF, 0xF, true);
+    else if constexpr (J == 4 || J == 8) return __builtin_amdgcn_ds_swizzle(v, 0x1F | (J << 10));
+    else if constexpr (J == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (threadIdx.x & 16) ? int(r[0]) : int(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (threadIdx.x & 32) ? int(r[0]) : int(r[1]);
+    }
+}
+
+// one compare-exchange stage of a bitonic network over the 64 lanes, order: logit descending,
+// expert id ascending on equal logits
+template <int K2, int J>
+__device__ __forceinline__ void bitonic_stage(float& v, int& id) {
+    const int lane = threadIdx.x & 63;
+    const float pv = __builtin_bit_cast(float, lane_xor<J>(__builtin_bit_cast(int, v)));
+    const int pid = lane_xor<J>(id);
+    const bool pbetter = pv > v || (pv == v && pid < id);
+    const bool lower = (lane & J) == 0, desc = (lane & K2) == 0;
+    const bool take = (lower == desc) ? pbetter : !pbetter;
+    v = take ? pv : v;
+    id = take ? pid : id;
+}
+
+// sorts one (logit, id) pair per lane across the wave: lane 0 gets the best
+__device__ __forceinline__ void bitonic64(float& v, int& id) {
+    bitonic_stage<2, 1>(v, id);
+    bitonic_stage<4, 2>(v, id);
+    bitonic_stage<4, 1>(v, id);
+    bitonic_stage<8, 4>(v, id);
+    bitonic_stage<8, 2>(v, id);
+    bitonic_stage<8, 1>(v, id);
+    bitonic_stage<16, 8>(v, id);
+    bitonic_stage<16, 4>(v, id);
+    bitonic_stage<16, 2>(v, id);
+    bitonic_stage<16, 1>(v, id);
+    bitonic_stage<32, 16>(v, id);
+    bitonic_stage<32, 8>(v, id);
+    bitonic_stage<32, 4>(v, id);
+    bitonic_stage<32, 2>(v, id);
+    bitonic_stage<32, 1>(v, id);
+    bitonic_stage<64, 32>(v, id);
+    bitonic_stage<64, 16>(v, id);
+    bitonic_stage<64, 8>(v, id);
+    bitonic_stage<64, 4>(v, id);
+    bitonic_stage<64, 2>(v, id);
+    bitonic_stage<64, 1>(v, id);
+}
+
+// exclusive prefix sum of an int over the 64 lanes (and the total): DPP row shifts within each row
+// of 16, then row broadcasts across rows
+__device__ __forceinline__ int wave_excl_scan(int c, int* total) {
+    int x = c;
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, kDppBcast15, 0xA, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0, x, kDppBcast31, 0xC, 0xF, false);
+    *total = __builtin_amdgcn_readlane(x, 63);
+    return x - c;
+}
+
+// Top-K (K <= 64) of one token's E <= 64 V logits by one wave. cand: 64 floats + 64 ints of LDS
+// scratch for this wave. On return lane k < K holds the k-th selection (sel_id, sel_l) in rank
+// order; mx is the largest logit and se this lane's share of sum_e exp(l_e - mx).
+// Method: lane l holds experts V l .. V l + V - 1. The K best lane maxima (bitonic sort of the 64
+// lane maxima) are K distinct logits, so every member of the top K ranks at or above the K-th of
+// them; the (few) logits that do are compacted and sorted. Should more than 64 tie there (coarse,
+// heavily tied logits), K rounds of wave maxima over the lanes' sorted lists do the selection.
+template <int V>
+__device__ __forceinline__ void topk_select(const float* __restrict__ l, int E, int K, float* cand_v, int* cand_id,
+                                           int& sel_id, float& sel_l, float& mx, float& se) {
+    const int lane = threadIdx.x & 63;
+    float v[V];
+    if (E == 64 * V) {
+        const float4* l4 = reinterpret_cast<const float4*>(l + V * lane);
+#pragma unroll
+        for (int i = 0; i < V / 4; ++i) {
+            const float4 q = l4[i];
+            v[4 * i] = q.x;
+            v[4 * i + 1] = q.y;
+            v[4 * i + 2] = q.z;
+            v[4 * i + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = V * lane + i < E ? l[V * lane + i] : -INFINITY;
+    }
+    // lane maximum (first index on ties: the lowest expert id of the lane)
+    float lm = v[0];
+    int li = V * lane;
+#pragma unroll
+    for (int i = 1; i < V; ++i)
+        if (v[i] > lm) {
+            lm = v[i];
+            li = V * lane + i;
+        }
+    float sv = lm;
+    int sid = li;
+    bitonic64(sv, sid);
+    mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), 0));
+    const float tv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), K - 1));
+    const int tid = __builtin_amdgcn_readlane(sid, K - 1);
+    se = 0.0f;
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int e = V * lane + i;
+        if (e < E) se += expf(v[i] - mx);
+        c += (v[i] > tv || (v[i] == tv && e <= tid)) ? 1 : 0;
+    }
+    int C;
+    int pos = wave_excl_scan(c, &C);
+    if (C <= 64) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const int e = V * lane + i;
+            if (v[i] > tv || (v[i] == tv && e <= tid)) {
+                cand_v[pos] = v[i];
+                cand_id[pos] = e;
+                ++pos;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+        // rank of candidate `lane` among the C candidates (lane j's values read with readlane),
+        // then scatter by rank
+        const float cv = lane < C ? cand_v[lane] : -INFINITY;
+        const int ci = lane < C ? cand_id[lane] : 0x7fffffff;
+        int rank = 0;
+        for (int j = 0; j < C; ++j) {
+            const float ov = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), j));
+            const int oi = __builtin_amdgcn_readlane(ci, j);
+            rank += (ov > cv || (ov == cv && oi < ci)) ? 1 : 0;
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane < C && rank < K) {
+            cand_v[rank] = cv;
+            cand_id[rank] = ci;
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+        sel_l = lane < K ? cand_v[lane] : 0.0f;
+        sel_id = lane < K ? cand_id[lane] : 0;
+        return;
+    }
+    // heavily tied logits: K rounds over the lanes' sorted lists
+    int id[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) id[i] = V * lane + i;
+    sort_desc<V>(v, id);
+    sel_id = 0;
+    sel_l = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        const float m = wave_max(v[0]);
+        const uint64_t b = __ballot(v[0] == m);
+        const int win = __ffsll((long long)b) - 1;
+        const int sel = __builtin_amdgcn_readlane(id[0], win);
+        if (lane == win) {
+#pragma unroll
+            for (int i = 0; i + 1 < V; ++i) {
+                v[i] = v[i + 1];
+                id[i] = id[i + 1];
+            }
+            v[V - 1] = -INFINITY;
+        }
+        if (lane == k) {
+            sel_id = sel;
+            sel_l = m;
+        }
+    }
+}
+
+// The K weights from a selection (lane k holds the k-th), moe_ref.cu:146-164: p = exp(l - mx) / S
+// with S the sum over all experts; w = p / max(sum of the p in rank order, 2^-14).
+__device__ __forceinline__ float topk_weight(float sel_l, float mx, float S, int K) {
+    const int lane = threadIdx.x & 63;
+    float p = 0.0f;
+    if (lane < K) p = expf(sel_l - mx) / S;
+    float ws = 0.0f;
+    for (int k = 0; k < K; ++k) ws += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k));
+    ws = fmaxf(ws, 6.103515625e-5f);
+    return p / ws;
+}
+
+// One token by one wave: ids/wts [K] written by lanes 0..K-1; returns lane k's id.
+template <int V>
+__device__ __forceinline__ int topk_wave(const float* __restrict__ l, int E, int K, int32_t* ids, float* wts,
+                                         float* cand_v, int* cand_id) {
+    int sel_id;
+    float sel_l, mx, se;
+    topk_select<V>(l, E, K, cand_v, cand_id, sel_id, sel_l, mx, se);
+    const float S = wave_sum_tree(se);
+    const float w = topk_weight(sel_l, mx, S, K);
+    if ((threadIdx.x & 63) < K) {
+        ids[threadIdx.x & 63] = sel_id;
+        wts[threadIdx.x & 63] = w;
+    }
+    return sel_id;
+}
+
+// Canonical RMS scale of one token by one wave: chains j = 64 lanes over contiguous L = n / 64
+// values (fmaf(x, x, acc) ascending from 0), the adjacent pairwise tree over the chains, then
+// r = 1 / sqrt(sum / n + 1e-6) with correctly rounded division and square root.
+// xc points at this lane's chain (stride between chain elements: 1).
+template <int L>
+__device__ __forceinline__ float rms_scale_wave(const float* xc, int n) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < L; ++i) acc = fmaf(xc[i], xc[i], acc);
+    acc = wave_sum_tree(acc);
+    const float ms = acc / float(n);
+    return 1.0f / sqrtf(ms + 1e-6f);
+}
+
+}  // namespace frt

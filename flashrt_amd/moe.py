@@ -19,7 +19,7 @@ from types import SimpleNamespace
 
 import torch
 
-from ._lib import FrtArena, FrtError, FrtMoeLayer, check, lib
+from ._lib import LAYER_NORM_INPUT, FrtArena, FrtError, FrtMoeLayer, check, lib
 
 __all__ = ["FrtError", "ExpertArena", "arena_alloc", "arena_free", "moe_route_topk", "router_logits", "quantize_q8",
            "moe_dispatch", "moe_q2", "moe_hits_scratch_bytes", "moe_hits", "MoeLayer", "expert_bytes", "gen"]
@@ -159,13 +159,14 @@ def moe_hits(hit_ptr, hit_n, K: int, x, n: int, ff: int, scratch, yh, stream=Non
 
 class MoeLayer:
     """One MoE layer on the HBM arena: router -> top-k -> routed experts + shared expert *
-    sigmoid(gate). T <= 4 runs the decode GEMV path, larger T the grouped MFMA path."""
+    sigmoid(gate). T <= 4 runs the decode GEMV path, larger T the grouped MFMA path. norm_input:
+    the layer's input is x / rms(x) (the stack's pre-MoE RMS norm)."""
 
     def __init__(self, experts: int, stride: int, n_expert: int, shared: int, router_w, gate_w, d_model: int,
-                 d_ff: int, top_k: int, router_bias=None):
+                 d_ff: int, top_k: int, router_bias=None, norm_input: bool = False):
         self._keep = (router_w, gate_w, router_bias)
         self.raw = FrtMoeLayer(experts, stride, n_expert, shared, _p(router_w), _p(router_bias), _p(gate_w),
-                               d_model, d_ff, top_k)
+                               d_model, d_ff, top_k, LAYER_NORM_INPUT if norm_input else 0)
         self.d_model, self.top_k, self.n_expert = d_model, top_k, n_expert
         self._ws = None
 

@@ -34,6 +34,14 @@ const char* frt_last_error(void);
 /* Library version string. */
 const char* frt_version(void);
 
+/* Per-kernel timing for measurement harnesses (no reference counterpart; the reference times
+ * kernels with CUDA events in its tests, tests/test_moe_hits.cpp:183-208). Between begin and end,
+ * each library call records a hipEvent on its stream after every kernel it launches; end
+ * synchronises and writes, per kernel name, the summed milliseconds and launch count (names in
+ * rows of name_len bytes). Returns the number of names. Do not use under graph capture. */
+void frt_timing_begin(void);
+int frt_timing_end(char* names, int name_len, double* total_ms, int* launches, int max);
+
 /* ---- planar Q2_0 sizes (quant/q2_0/q2_0.hpp:40,51: mat_bytes, expert_bytes) ---- */
 size_t frt_q2_mat_bytes(int rows, int cols);
 size_t frt_q2_expert_bytes(int d_model, int d_ff);
@@ -101,8 +109,11 @@ int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, con
 /* ---- one whole MoE layer on an HBM-resident arena: router logits -> route_topk -> routed experts
  * + shared expert * sigmoid(gate) (moe_block_fast, arch/qwen4exp/moe_fast.hpp:144-147, for T <= 4;
  * moe_block_stream, arch/qwen4exp/moe_stream.hpp:35, for prefill chunks; same math as moe_block,
- * arch/qwen4exp/blocks.hpp:286). out [T][n] = (resid ? resid : 0) + moe(x). ids/wts [T][K]
+ * arch/qwen4exp/blocks.hpp:286). out [T][n] = (resid ? resid : 0) + moe(u), with u = x, or with
+ * flags & FRT_LAYER_NORM_INPUT u = x / rms(x) (the unweighted RMS norm that precedes the MoE in the
+ * model, r = 1/sqrt(sum(x^2)/n + 1e-6) summed in the router's canonical order). ids/wts [T][K]
  * (optional outputs), counts [E] optional. */
+#define FRT_LAYER_NORM_INPUT 1
 typedef struct frt_moe_layer {
     const uint8_t* experts;   /* routed expert 0 of this layer; expert e at experts + e * stride */
     size_t stride;
@@ -112,6 +123,7 @@ typedef struct frt_moe_layer {
     const float* router_bias; /* [E] added to the logits, or NULL */
     const float* gate_w;      /* [n] fp32 (ffn_gate_inp_shexp) */
     int d_model, d_ff, top_k;
+    int flags;                /* FRT_LAYER_* */
 } frt_moe_layer;
 size_t frt_moe_layer_workspace_bytes(const frt_moe_layer* L, int T);
 int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out, int32_t* ids,

@@ -131,6 +131,14 @@ void quant_block(const float* x32, int8_t* q, float* d) {
     for (int j = 0; j < kQ8; ++j) q[j] = int8_t(std::roundf(x32[j] * id));
 }
 
+// The canonical reduction of 64 chain sums: the adjacent pairwise tree
+// ((s0+s1)+(s2+s3))+... (level by level, pairs of neighbouring blocks).
+float tree64(float* s) {
+    for (int step = 1; step < 64; step *= 2)
+        for (int j = 0; j < 64; j += 2 * step) s[j] = s[j] + s[j + step];
+    return s[0];
+}
+
 }  // namespace
 
 extern "C" {
@@ -250,9 +258,23 @@ float orc_dot_canon(const float* w, const float* x, int n) {
         for (int k = j * L; k < (j + 1) * L; ++k) acc = std::fmaf(w[k], x[k], acc);
         s[j] = acc;
     }
-    for (int half = 32; half >= 1; half >>= 1)
-        for (int j = 0; j < half; ++j) s[j] = s[j] + s[j + half];
-    return s[0];
+    return tree64(s);
+}
+
+void orc_rmsnorm(const float* x, int T, int n, float* u) {
+    const int L = n / 64;
+    for (int t = 0; t < T; ++t) {
+        const float* xt = x + size_t(t) * n;
+        float s[64];
+        for (int j = 0; j < 64; ++j) {
+            float acc = 0.0f;
+            for (int k = j * L; k < (j + 1) * L; ++k) acc = std::fmaf(xt[k], xt[k], acc);
+            s[j] = acc;
+        }
+        const float ms = tree64(s) / float(n);
+        const float r = 1.0f / std::sqrt(ms + 1e-6f);
+        for (int i = 0; i < n; ++i) u[size_t(t) * n + i] = xt[i] * r;
+    }
 }
 
 void orc_router_logits(const float* x, int T, const float* W, const float* bias, int E, int n, float* logits) {
@@ -372,7 +394,13 @@ void orc_moe_cpu(int n, int ff, const uint8_t* const* blobs, const int* ntok, co
 
 void orc_moe_layer(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, const float* router_w,
                    const float* router_bias, const float* gate_w, int n, int ff, int K, const float* x, int T,
-                   int n_threads, int order, float* out, int32_t* ids, float* wts, float* logits_out) {
+                   int n_threads, int order, float* out, int32_t* ids, float* wts, float* logits_out, int norm_input) {
+    std::vector<float> un;
+    if (norm_input) {
+        un.resize(size_t(T) * n);
+        orc_rmsnorm(x, T, n, un.data());
+        x = un.data();
+    }
     std::vector<float> logits(size_t(T) * E);
     orc_router_logits(x, T, router_w, router_bias, E, n, logits.data());
     if (logits_out) std::memcpy(logits_out, logits.data(), logits.size() * 4);

@@ -46,11 +46,17 @@ void orc_expert_ffn(const uint8_t* blob, int n, int ff, const int8_t* xq, const 
 
 /* ---- router logits in the canonical order shared with the HIP kernels:
  * for each (t,e): 64 chains, chain j = fmaf over k in [j*L, (j+1)*L) ascending (L = n/64) from 0,
- * then a butterfly tree s_m(j) = s_{m-1}(j) + s_{m-1}(j + 64>>m), then + bias[e] (bias may be NULL).
+ * then the adjacent pairwise tree ((c0+c1)+(c2+c3))+... over the chains, then + bias[e] (bias may
+ * be NULL).
  * The reference computes the logits with ggml's dense linear (blocks.hpp:85), which no reference
  * test pins; this order is this build's definition. */
 void orc_router_logits(const float* x, int T, const float* W, const float* bias, int E, int n, float* logits);
 float orc_dot_canon(const float* w, const float* x, int n);
+
+/* ---- the stack's pre-MoE RMS norm in the canonical order shared with the HIP kernels:
+ * ss = the same pairwise tree over 64 chains of fmaf(x, x, acc) over contiguous L = n/64 values; r = 1/sqrtf(ss/n +
+ * 1e-6f); u = x * r (this build's synthetic-stack definition; the model's own norm has a weight). */
+void orc_rmsnorm(const float* x, int T, int n, float* u);
 
 /* ---- routing as moe_block's host code (arch/qwen4exp/moe_ref.cu:146-164), with the selection
  * rank defined as in test_route_topk (tests/test_route_topk.cpp:52-55): by logit descending, ties
@@ -71,10 +77,11 @@ void orc_moe_cpu(int n, int ff, const uint8_t* const* blobs, const int* ntok, co
  * logits (canonical router) -> routing -> misses grouped per expert (<= 4 tokens each, token
  * order, experts ascending) -> moe_cpu -> + shared expert * sigmoid(gate logit) (moe_ref.cu:90-97).
  * Routed expert e of the layer is at arena + e*stride. The shared expert is a Q2_0 blob of the
- * same shape (the BASELINE configuration's choice). Outputs: out [T][n], ids/wts [T][K]. */
+ * same shape (the BASELINE configuration's choice). Outputs: out [T][n], ids/wts [T][K].
+ * norm_input: the layer runs on u = orc_rmsnorm(x) instead of x. */
 void orc_moe_layer(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, const float* router_w,
                    const float* router_bias, const float* gate_w, int n, int ff, int K, const float* x, int T,
-                   int n_threads, int order, float* out, int32_t* ids, float* wts, float* logits_out);
+                   int n_threads, int order, float* out, int32_t* ids, float* wts, float* logits_out, int norm_input);
 
 /* ---- synthetic inputs: the seeded recipe restated independently in the HIP library ---- */
 uint64_t orc_gen_key(uint64_t seed, uint64_t cfg, uint64_t layer, uint64_t tensor);

@@ -65,7 +65,8 @@ def lib():
         L.orc_moe_cpu.argtypes = [C.c_int, C.c_int, C.c_void_p, _i32p, _i32p, _f32p, C.c_int, _i8p, _f32p, C.c_int,
                                   _f32p, C.c_int, C.c_int, C.c_int]
         L.orc_moe_layer.argtypes = [C.c_void_p, C.c_size_t, C.c_int, _u8p, _f32p, C.c_void_p, _f32p, C.c_int, C.c_int,
-                                    C.c_int, _f32p, C.c_int, C.c_int, C.c_int, _f32p, _i32p, _f32p, C.c_void_p]
+                                    C.c_int, _f32p, C.c_int, C.c_int, C.c_int, _f32p, _i32p, _f32p, C.c_void_p, C.c_int]
+        L.orc_rmsnorm.argtypes = [_f32p, C.c_int, C.c_int, _f32p]
         L.orc_gen_key.restype = C.c_uint64
         L.orc_gen_key.argtypes = [C.c_uint64] * 4
         L.orc_gen_u64.restype = C.c_uint64
@@ -224,8 +225,17 @@ def miss_list(ids: np.ndarray, wts: np.ndarray, E: int):
             np.array(wv, np.float32).reshape(-1, 4))
 
 
+def rmsnorm(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    T, n = x.reshape(-1, x.shape[-1]).shape
+    u = np.zeros((T, n), np.float32)
+    lib().orc_rmsnorm(x.reshape(-1), T, n, u)
+    return u
+
+
 def moe_layer(arena: np.ndarray, stride: int, E: int, shared: np.ndarray, router_w: np.ndarray, router_bias,
-              gate_w: np.ndarray, n: int, ff: int, K: int, x: np.ndarray, threads: int = 8, order: int = 0):
+              gate_w: np.ndarray, n: int, ff: int, K: int, x: np.ndarray, threads: int = 8, order: int = 0,
+              norm_input: bool = False):
     """The whole layer (moe_block semantics). arena: uint8 [E*stride] (or an object exposing
     .ctypes.data). Returns out [T][n], ids, wts, logits."""
     x = np.ascontiguousarray(x, np.float32).reshape(-1, n)
@@ -237,5 +247,5 @@ def moe_layer(arena: np.ndarray, stride: int, E: int, shared: np.ndarray, router
     b = None if router_bias is None else np.ascontiguousarray(router_bias, np.float32)
     lib().orc_moe_layer(arena.ctypes.data, stride, E, shared, np.ascontiguousarray(router_w, np.float32).reshape(-1),
                         None if b is None else b.ctypes.data, np.ascontiguousarray(gate_w, np.float32), n, ff, K,
-                        x.reshape(-1), T, threads, order, out, ids, wts, logits.ctypes.data)
+                        x.reshape(-1), T, threads, order, out, ids, wts, logits.ctypes.data, int(norm_input))
     return out, ids, wts, logits

@@ -38,10 +38,11 @@ class World:
     router and gate weights generated on the GPU by flashrt_amd.gen, and host copies."""
 
     def __init__(self, cfg: int, layer: int = 0, n: int = N, ff: int = FF, E: int = E, K: int = K,
-                 bias: np.ndarray | None = None):
+                 bias: np.ndarray | None = None, norm_input: bool = False):
         import torch
         import flashrt_amd as F
         self.cfg, self.layer, self.n, self.ff, self.E, self.K = cfg, layer, n, ff, E, K
+        self.norm_input = norm_input
         self.eb = F.expert_bytes(n, ff)
         self.stride = (self.eb + 4095) // 4096 * 4096
         g = F.gen
@@ -61,7 +62,7 @@ class World:
         self.router_h = self.router_w.cpu().numpy().reshape(E, n)
         self.gate_h = self.gate_w.cpu().numpy()
         self.layer_obj = F.MoeLayer(self.arena.data_ptr(), self.stride, E, self.shared.data_ptr(), self.router_w,
-                                    self.gate_w, n, ff, K, router_bias=self.bias)
+                                    self.gate_w, n, ff, K, router_bias=self.bias, norm_input=norm_input)
 
     def blob(self, e: int) -> np.ndarray:
         return self.arena_h[e * self.stride: e * self.stride + self.eb]
@@ -80,4 +81,4 @@ class World:
 
     def oracle_forward(self, x: np.ndarray, threads: int = 8):
         return O.moe_layer(self.arena_h, self.stride, self.E, self.shared_h, self.router_h, self.bias_h, self.gate_h,
-                           self.n, self.ff, self.K, x, threads=threads)
+                           self.n, self.ff, self.K, x, threads=threads, norm_input=self.norm_input)
