@@ -50,7 +50,10 @@ void timing_mark(hipStream_t stream, const char* kernel) {
 int router_logits(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
                   float* logits, float* gate, hipStream_t stream, int norm, int8_t* xq, float* xd);
 int rmsnorm(const float* x, int T, int n, float* u, hipStream_t stream);
-int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xq16, hipStream_t stream);
+int router_gemm(const float* x, int T, const float* W, const float* bias, int E, int n, float* logits,
+                hipStream_t stream);
+int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xhi, _Float16* xlo,
+                hipStream_t stream);
 int route_topk(hipStream_t stream, const float* logits, int T, int E, int K, int32_t* ids, float* wts, uint32_t* counts,
                uint32_t* tail_counts, int tail_from);
 // decode.hip
@@ -218,7 +221,7 @@ int frt_router_logits(void* stream, const float* x, int T, const float* W, const
 
 int frt_quantize_q8(void* stream, const float* x, int rows, int n, int8_t* xq, float* xd) {
     if (!x || !xq || !xd) return set_error(kErrNull, "quantize_q8: null pointer");
-    return quantize_q8(x, rows, n, xq, xd, nullptr, static_cast<hipStream_t>(stream));
+    return quantize_q8(x, rows, n, xq, xd, nullptr, nullptr, static_cast<hipStream_t>(stream));
 }
 
 size_t frt_moe_dispatch_workspace_bytes(int T, int K, int E) { return pf_dispatch_ws_bytes(T, K, E); }
@@ -229,7 +232,7 @@ int frt_moe_dispatch(void* stream, const int32_t* ids, int T, int K, int E, int3
 }
 
 size_t frt_moe_q2_workspace_bytes(int T, int K, int n, int ff, int E) {
-    return pf_workspace_bytes(T, K, n, ff, E, false, false);
+    return pf_workspace_bytes(T, K, n, ff, E, false, true);   // room for the fp32 outputs of yd_bf16
 }
 int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const float* x, const int32_t* ids,
                    int T, int K, void* yd, void* ws, size_t ws_bytes, void* stream, int block64, int yd_bf16) {
@@ -248,7 +251,7 @@ int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, con
     p += up256(size_t(T) * n);
     float* xd = reinterpret_cast<float*>(p);
     p += up256(size_t(T) * (n / kQ8) * 4);
-    if (int rc = quantize_q8(x, T, n, xq, xd, nullptr, s)) return rc;
+    if (int rc = quantize_q8(x, T, n, xq, xd, nullptr, nullptr, s)) return rc;
     return dec_hits(hit_ptr, hit_n, K, xq, xd, n, ff, p, yh, s, T);
 }
 
@@ -289,10 +292,12 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
         xin = w.u;
         timing_mark(s, "rmsnorm");
     }
-    if (int rc = router_logits(xin, T, L->router_w, L->router_bias, L->gate_w, E, n, w.logits, w.gate, s, 0, nullptr,
-                               nullptr))
+    // router logits as a register-tiled GEMM; the shared expert's gate logit as a one-row GEMV
+    if (int rc = router_gemm(xin, T, L->router_w, L->router_bias, E, n, w.logits, s)) return rc;
+    timing_mark(s, "router_gemm");
+    if (int rc = router_logits(xin, T, L->gate_w, nullptr, nullptr, 1, n, w.gate, nullptr, s, 0, nullptr, nullptr))
         return rc;
-    timing_mark(s, "router");
+    timing_mark(s, "gate");
     if (int rc = route_topk(s, w.logits, T, E, K, ids_o, wts_o, counts, nullptr, 1 << 30)) return rc;
     timing_mark(s, "route_topk");
     return pf_moe(L->experts, L->stride, E, L->shared, n, ff, xin, ids_o, wts_o, w.gate, T, K, resid, out, w.rest,

@@ -174,6 +174,15 @@ __device__ __forceinline__ half8 dequant8(uint32_t cw, int h, _Float16 d) {
     return r;
 }
 
+__device__ __forceinline__ int lane_xor16(int v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? int(r[0]) : int(r[1]);
+}
+__device__ __forceinline__ int lane_xor32(int v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? int(r[0]) : int(r[1]);
+}
+
 __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b) {
     const floatx4 z = {0.0f, 0.0f, 0.0f, 0.0f};
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, z, 0, 0, 0);
@@ -188,195 +197,231 @@ __device__ __forceinline__ int perm64_pos(int e) {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-// ---------------------------------------------------------------- gate + up
+// ---------------------------------------------------------------- grouped GEMMs (gate + up, down)
+//
+// Operands are exact in fp16 and the products exact in fp32: weights (q - 1) * d_w (dequantized in
+// registers from the code dwords) and activations a = code * d (Q8_0: at most 18 significant bits)
+// stored as a pair hi = fp16(a), lo = fp16(a - hi), so that A * hi + A * lo = A * a exactly. Each
+// 32-deep MFMA step is issued twice (hi, lo) into one fp32 accumulator: no per-block scaling on the
+// VALU (gfx950's MFMA keeps fp16 subnormals, which the lo parts often are).
+//
+// Workgroup: 512 threads (8 waves), 64 tokens x 512 A rows, K in stages of 128 through two LDS
+// buffers (the next stage is loaded into registers while the current one is multiplied). Each wave
+// owns 4 A tiles of 16 rows and all 4 token tiles, so every activation fragment read from LDS feeds
+// 8 MFMAs.
+//   gate+up: A rows 0..255 are gate rows f0 + 0..255, A rows 256..511 the same up rows; wave w owns
+//            ff rows f0 + 32 w .. +31 (gate and up). Epilogue: SwiGLU, Q8_0 of the 32-row block of h
+//            (quant/q2_0/moe_cpu.cpp:43-61), h written as hi/lo for the down GEMM.
+//   down:    A rows are output rows r0 + 0..511, wave w owns r0 + 64 w .. +63; yd[slot][row] fp32.
 
-constexpr int kKC = 128;   // K per LDS stage (2 blocks)
+constexpr int kKC = 128;          // K per stage
+constexpr int kLdB = kKC + 8;     // padded fp16 row of an activation stage
 
-// grid (ff / 64, max_tiles); 256 threads: wave w owns ff rows f0 + 16w .. +15 (gate and up).
-__global__ void __launch_bounds__(256) k_pf_gateup(const uint8_t* __restrict__ arena, size_t stride, int E,
-                                                   const uint8_t* __restrict__ shared_blob, int n, int ff,
-                                                   const _Float16* __restrict__ xq16, const float* __restrict__ xd,
-                                                   const int32_t* __restrict__ tok_of, const int32_t* __restrict__ bounds,
-                                                   const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-                                                   _Float16* __restrict__ hq16, float* __restrict__ hd) {
+struct MmStage {
+    uint32_t a[512][kKC / 64][4];   // codes: A row, block, dword
+    uint32_t sc[512];               // the A row's two fp16 block scales
+    _Float16 bh[kTN][kLdB];         // activations, hi part (perm64 order)
+    _Float16 bl[kTN][kLdB];         // activations, lo part
+};
+
+__device__ __forceinline__ floatx4 mfma_acc(half8 a, half8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void split_hi_lo(float a, _Float16& hi, _Float16& lo) {
+    hi = _Float16(a);
+    lo = _Float16(a - float(hi));
+}
+
+template <bool GATEUP>
+__global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena, size_t stride, int E,
+                                               const uint8_t* __restrict__ shared_blob, int n, int ff,
+                                               const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
+                                               const int32_t* __restrict__ tok_of, const int32_t* __restrict__ bounds,
+                                               const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
+                                               _Float16* __restrict__ hhi, _Float16* __restrict__ hlo,
+                                               float* __restrict__ yd, const int32_t* __restrict__ slot_of) {
     if (int(blockIdx.y) >= *n_tiles) return;
+    extern __shared__ __align__(16) uint8_t smem[];
+    MmStage* st = reinterpret_cast<MmStage*>(smem);
+    __shared__ int sTok[kTN];
     const int2 tile = tiles[blockIdx.y];
     const int grp = tile.x;
     const int row0 = bounds[grp] + tile.y;
     const int cnt = min(kTN, bounds[grp + 1] - row0);
     const uint8_t* blob = grp < E ? arena + size_t(grp) * stride : shared_blob;
-    const int nb = n / kBlock;
-    const int f0 = blockIdx.x * 64;
+    const int Kd = GATEUP ? n : ff;            // contraction length
+    const int nbk = Kd / kBlock;               // weight blocks per A row
+    const int rows_total = GATEUP ? ff : n;    // rows of each A matrix
     const size_t mb = mat_bytes(ff, n);
-
-    __shared__ __align__(16) uint32_t sA[128][kKC / 64][4];   // codes: row, block, dword
-    __shared__ uint16_t sS[128][kKC / 64];                    // weight scales
-    __shared__ __align__(16) _Float16 sB[kTN][kKC + 8];       // activation codes (perm64 order)
-    __shared__ float sD[kTN][kKC / 32];                       // activation scales
-    __shared__ int sTok[kTN];
-
+    const uint8_t* m0 = GATEUP ? blob : blob + 2 * mb;      // gate (or down)
+    const uint8_t* m1 = blob + mb;                          // up
+    const int rbase = blockIdx.x * (GATEUP ? 256 : 512);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    if (tid < kTN) sTok[tid] = tid < cnt ? tok_of[row0 + tid] : -1;
+    if (tid < kTN) sTok[tid] = tid < cnt ? (GATEUP ? tok_of[row0 + tid] : row0 + tid) : -1;
     __syncthreads();
 
-    floatx4 acc[2][4];
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[m][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const int li = lane & 15, lg = lane >> 4;
-    for (int k0 = 0; k0 < n; k0 += kKC) {
+    // the A row `ar` of the tile: matrix and row index
+    auto arow = [&](int ar, const uint8_t*& m, int& r) {
+        if (GATEUP) {
+            m = ar < 256 ? m0 : m1;
+            r = rbase + (ar & 255);
+        } else {
+            m = m0;
+            r = rbase + ar;
+        }
+    };
+    uint4 ra[2];
+    uint32_t rs;
+    uint4 rb[4];
+    auto load = [&](int k0) {
         const int b0 = k0 / kBlock;
-        // stage A: 128 rows x 2 blocks x 16 B (one uint4 per thread), scales
-        {
-            const int r = tid >> 1, bb = tid & 1;
-            const uint8_t* base = blob + (r < 64 ? 0 : mb);
-            const int fr = f0 + (r & 63);
-            const uint4 v = *reinterpret_cast<const uint4*>(base + (size_t(fr) * nb + b0 + bb) * 16);
-            *reinterpret_cast<uint4*>(&sA[r][bb][0]) = v;
-            const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + size_t(ff) * nb * 16);
-            sS[r][bb] = sc[size_t(fr) * nb + b0 + bb];
-        }
-        // stage B: 64 tokens x 128 fp16 (16 uint4 per token), scales 64 x 4
-        for (int i = tid; i < kTN * (kKC / 8); i += 256) {
-            const int j = i / (kKC / 8), q = i % (kKC / 8);
-            const int t = sTok[j];
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (t >= 0) v = *reinterpret_cast<const uint4*>(xq16 + size_t(t) * n + k0 + q * 8);
-            *reinterpret_cast<uint4*>(&sB[j][q * 8]) = v;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int idx = p * 512 + tid, ar = idx >> 1, blk = idx & 1;
+            const uint8_t* m;
+            int r;
+            arow(ar, m, r);
+            ra[p] = r < rows_total ? *reinterpret_cast<const uint4*>(m + (size_t(r) * nbk + b0 + blk) * 16)
+                                   : make_uint4(0, 0, 0, 0);
         }
         {
-            const int j = tid >> 2, q = tid & 3;
-            const int t = sTok[j];
-            sD[j][q] = t >= 0 ? xd[size_t(t) * (n / kQ8) + k0 / kQ8 + q] : 0.0f;
+            const uint8_t* m;
+            int r;
+            arow(tid, m, r);
+            const uint32_t* sc = reinterpret_cast<const uint32_t*>(m + size_t(rows_total) * nbk * 16 + (size_t(r) * nbk + b0) * 2);
+            rs = r < rows_total ? *sc : 0u;
         }
-        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int idx = p * 512 + tid, which = idx >> 10, rem = idx & 1023, j = rem >> 4, q = rem & 15;
+            const int t = sTok[j];
+            const _Float16* src = which ? blo : bhi;
+            rb[p] = t >= 0 ? *reinterpret_cast<const uint4*>(src + size_t(t) * Kd + k0 + q * 8) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store = [&](MmStage& S) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int idx = p * 512 + tid, ar = idx >> 1, blk = idx & 1;
+            *reinterpret_cast<uint4*>(&S.a[ar][blk][0]) = ra[p];
+        }
+        S.sc[tid] = rs;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int idx = p * 512 + tid, which = idx >> 10, rem = idx & 1023, j = rem >> 4, q = rem & 15;
+            _Float16* dst = which ? &S.bl[j][q * 8] : &S.bh[j][q * 8];
+            *reinterpret_cast<uint4*>(dst) = rb[p];
+        }
+    };
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[i][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int li = lane & 15, lg = lane >> 4;
+    int art[4];   // this lane's A row in the tile for each of its 4 A tiles
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        art[i] = GATEUP ? ((i < 2 ? 0 : 256) + 32 * wave + 16 * (i & 1) + li) : (64 * wave + 16 * i + li);
+
+    const int nstage = Kd / kKC;
+    load(0);
+    store(st[0]);
+    __syncthreads();
+    for (int sI = 0; sI < nstage; ++sI) {
+        MmStage& S = st[sI & 1];
+        if (sI + 1 < nstage) load((sI + 1) * kKC);
 #pragma unroll
         for (int bb = 0; bb < kKC / 64; ++bb) {
-            const int ra = wave * 16 + li;   // gate row in the tile; up row = ra + 64
-            const uint32_t cg = sA[ra][bb][lg], cu = sA[64 + ra][bb][lg];
-            const _Float16 dg = __builtin_bit_cast(_Float16, sS[ra][bb]);
-            const _Float16 du = __builtin_bit_cast(_Float16, sS[64 + ra][bb]);
+            uint32_t cw[4];
+            _Float16 dw[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                cw[i] = S.a[art[i]][bb][lg];
+                dw[i] = __builtin_bit_cast(_Float16, uint16_t(S.sc[art[i]] >> (16 * bb)));
+            }
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const half8 ag = dequant8(cg, h, dg), au = dequant8(cu, h, du);
+                half8 av[4];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const int col = t * 16 + li;
-                    const half8 b = *reinterpret_cast<const half8*>(&sB[col][bb * 64 + h * 32 + lg * 8]);
-                    const float da = sD[col][bb * 2 + h];
-                    const floatx4 cgv = mfma16(ag, b), cuv = mfma16(au, b);
+                for (int i = 0; i < 4; ++i) av[i] = dequant8(cw[i], h, dw[i]);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        acc[0][t][j] = fmaf(cgv[j], da, acc[0][t][j]);
-                        acc[1][t][j] = fmaf(cuv[j], da, acc[1][t][j]);
+                for (int c = 0; c < 4; ++c) {
+                    const int col = c * 16 + li, off = bb * 64 + h * 32 + lg * 8;
+                    const half8 bh = *reinterpret_cast<const half8*>(&S.bh[col][off]);
+                    const half8 bl = *reinterpret_cast<const half8*>(&S.bl[col][off]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        acc[i][c] = mfma_acc(av[i], bh, acc[i][c]);
+                        acc[i][c] = mfma_acc(av[i], bl, acc[i][c]);
                     }
                 }
             }
         }
-        __syncthreads();
-    }
-    // SwiGLU into LDS: hbuf[token][ff row in tile]; D layout: lane -> col li, rows 4*lg + j
-    float* hbuf = reinterpret_cast<float*>(&sB[0][0]);   // 64 x 64 floats = 16 KB (sB is 17 KB)
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) hbuf[(t * 16 + li) * 64 + wave * 16 + lg * 4 + j] = silu_mul(acc[0][t][j], acc[1][t][j]);
-    __syncthreads();
-    // Q8_0 per (token, 32-row block): half-wave per pair
-    const int hw = tid >> 5, hl = tid & 31;
-    for (int p = hw; p < kTN * 2; p += 8) {
-        const int j = p >> 1, qb = p & 1;
-        if (j >= cnt) continue;
-        const float v = hbuf[j * 64 + qb * 32 + hl];
-        const float am = half_max(fabsf(v));
-        const float d = q8_scale(am);
-        const float id = q8_inv(d);
-        const size_t row = size_t(row0 + j);
-        hq16[row * ff + f0 + perm64_pos(qb * 32 + hl)] = _Float16(float(q8_code(v, id)));
-        if (hl == 0) hd[row * (ff / kQ8) + f0 / kQ8 + qb] = f16_round(d);
-    }
-}
-
-// ---------------------------------------------------------------- down
-
-// grid (n / 64, max_tiles); 256 threads; the tile's h (64 tokens x ff, fp16) stays in LDS.
-template <typename OutT>
-__global__ void __launch_bounds__(256) k_pf_down(const uint8_t* __restrict__ arena, size_t stride, int E,
-                                                 const uint8_t* __restrict__ shared_blob, int n, int ff,
-                                                 const _Float16* __restrict__ hq16, const float* __restrict__ hd,
-                                                 const int32_t* __restrict__ slot_of, const int32_t* __restrict__ bounds,
-                                                 const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-                                                 OutT* __restrict__ yd) {
-    if (int(blockIdx.y) >= *n_tiles) return;
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int2 tile = tiles[blockIdx.y];
-    const int grp = tile.x;
-    const int row0 = bounds[grp] + tile.y;
-    const int cnt = min(kTN, bounds[grp + 1] - row0);
-    const uint8_t* blob = (grp < E ? arena + size_t(grp) * stride : shared_blob) + 2 * mat_bytes(ff, n);
-    const int nbf = ff / kBlock;
-    const int ldb = ff + 8;   // padded fp16 row
-    _Float16* sB = reinterpret_cast<_Float16*>(smem);                             // [64][ldb]
-    float* sD = reinterpret_cast<float*>(smem + size_t(kTN) * ldb * 2);           // [64][ff/32]
-    uint32_t* sA = reinterpret_cast<uint32_t*>(sD + kTN * (ff / kQ8));            // [64 rows][nbf][4]
-    uint16_t* sS = reinterpret_cast<uint16_t*>(sA + 64 * nbf * 4);                // [64][nbf]
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int r0 = blockIdx.x * 64;
-    for (int i = tid; i < kTN * (ff / 8); i += 256) {
-        const int j = i / (ff / 8), q = i % (ff / 8);
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (j < cnt) v = *reinterpret_cast<const uint4*>(hq16 + size_t(row0 + j) * ff + q * 8);
-        *reinterpret_cast<uint4*>(sB + j * ldb + q * 8) = v;
-    }
-    for (int i = tid; i < kTN * (ff / kQ8); i += 256) {
-        const int j = i / (ff / kQ8);
-        sD[i] = j < cnt ? hd[size_t(row0 + j) * (ff / kQ8) + i % (ff / kQ8)] : 0.0f;
-    }
-    for (int i = tid; i < 64 * nbf; i += 256) {
-        const int r = i / nbf, b = i % nbf;
-        *reinterpret_cast<uint4*>(sA + (r * nbf + b) * 4) =
-            *reinterpret_cast<const uint4*>(blob + (size_t(r0 + r) * nbf + b) * 16);
-        sS[i] = reinterpret_cast<const uint16_t*>(blob + size_t(n) * nbf * 16)[size_t(r0 + r) * nbf + b];
-    }
-    __syncthreads();
-    const int li = lane & 15, lg = lane >> 4;
-    const int ra = wave * 16 + li;
-    floatx4 acc[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int b = 0; b < nbf; ++b) {
-        const uint32_t cw = sA[(ra * nbf + b) * 4 + lg];
-        const _Float16 d = __builtin_bit_cast(_Float16, sS[ra * nbf + b]);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const half8 a = dequant8(cw, h, d);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int col = t * 16 + li;
-                const half8 bv = *reinterpret_cast<const half8*>(sB + col * ldb + b * 64 + h * 32 + lg * 8);
-                const float da = sD[col * (ff / kQ8) + 2 * b + h];
-                const floatx4 c = mfma16(a, bv);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[t][j] = fmaf(c[j], da, acc[t][j]);
-            }
+        if (sI + 1 < nstage) {
+            store(st[(sI + 1) & 1]);
+            __syncthreads();
         }
     }
+
+    if constexpr (GATEUP) {
+        // lane: token col c*16 + li; ff rows f = rbase + 32 wave + 16 i + 4 lg + j (i = 0, 1) for gate
+        // (acc[i]) and up (acc[2 + i]). The 32 rows of the wave are one Q8_0 block of h.
+        const int fbase = rbase + 32 * wave;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int col = t * 16 + li;
-        if (col >= cnt) continue;
-        const size_t slot = size_t(slot_of[row0 + col]);
-        OutT* dst = yd + slot * n + r0 + wave * 16 + lg * 4;
+        for (int c = 0; c < 4; ++c) {
+            const int col = c * 16 + li;
+            float hv[2][4];
+            float am = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dst[j] = OutT(acc[t][j]);
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    hv[i][j] = silu_mul(acc[i][c][j], acc[2 + i][c][j]);
+                    am = fmaxf(am, fabsf(hv[i][j]));
+                }
+            am = fmaxf(am, __builtin_bit_cast(float, lane_xor16(__builtin_bit_cast(int, am))));
+            am = fmaxf(am, __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(int, am))));
+            const float d = q8_scale(am);
+            const float id = q8_inv(d);
+            const float dr = f16_round(d);
+            if (col < cnt && fbase < ff) {
+                const size_t row = size_t(row0 + col);
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int f = fbase + 16 * i + 4 * lg + j;
+                        const float a = float(q8_code(hv[i][j], id)) * dr;
+                        _Float16 hi, lo;
+                        split_hi_lo(a, hi, lo);
+                        const size_t pos = row * ff + (f & ~63) + perm64_pos(f & 63);
+                        hhi[pos] = hi;
+                        hlo[pos] = lo;
+                    }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int col = c * 16 + li;
+            if (col >= cnt) continue;
+            const size_t slot = size_t(slot_of[row0 + col]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = rbase + 64 * wave + 16 * i + 4 * lg;
+                if (r < n) *reinterpret_cast<float4*>(yd + slot * n + r) = make_float4(acc[i][c][0], acc[i][c][1], acc[i][c][2], acc[i][c][3]);
+            }
+        }
     }
 }
 
 // ---------------------------------------------------------------- combine
 
-// out[t][i] = sum over the token's K slots in ascending expert id of w * yd (+ shared * sigmoid(g))
+// out[t][i] = sum over the token's K slots in ascending expert id of w * yd (+ shared * sigmoid(g));
+// grid (ceil(n / 1024), T), 4 consecutive outputs per thread
 template <typename InT>
 __global__ void __launch_bounds__(256) k_pf_combine(const InT* __restrict__ yd, const int32_t* __restrict__ ids,
                                                     const float* __restrict__ wts, const float* __restrict__ gate, int T,
@@ -384,38 +429,51 @@ __global__ void __launch_bounds__(256) k_pf_combine(const InT* __restrict__ yd, 
                                                     float* __restrict__ out) {
     __shared__ int order[32];
     const int t = blockIdx.y;
-    if (threadIdx.x == 0) {
-        int prev = -1;
-        for (int r = 0; r < K; ++r) {   // selection order by expert id (ids of one token are distinct)
-            int best = -1, bid = 0x7fffffff;
-            for (int k = 0; k < K; ++k) {
-                const int e = ids[t * K + k];
-                if (e > prev && e < bid) {
-                    bid = e;
-                    best = k;
-                }
-            }
-            order[r] = best;
-            prev = bid;
-        }
+    if (threadIdx.x < K) {   // rank of slot k by expert id (the ids of one token are distinct)
+        const int e = ids[t * K + threadIdx.x];
+        int r = 0;
+        for (int k = 0; k < K; ++k) r += ids[t * K + k] < e ? 1 : 0;
+        order[r] = threadIdx.x;
     }
     __syncthreads();
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
     if (i >= n) return;
-    float acc = 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int r = 0; r < K; ++r) {
         const int k = order[r];
-        const float p = wts[t * K + k] * float(yd[(size_t(t) * K + k) * n + i]);
-        acc = acc + p;
+        const float w = wts[t * K + k];
+        const InT* src = yd + (size_t(t) * K + k) * n + i;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float p = w * float(src[q]);
+            acc[q] = acc[q] + p;
+        }
     }
-    float o = acc;
+    float o[4] = {acc[0], acc[1], acc[2], acc[3]};
     if (shared) {
         const float g = 1.0f / (1.0f + expf(-gate[t]));
-        const float p = float(yd[(size_t(T) * K + t) * n + i]) * g;
-        o = acc + p;
+        const InT* src = yd + (size_t(T) * K + t) * n + i;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float p = float(src[q]) * g;
+            o[q] = acc[q] + p;
+        }
     }
-    if (resid) o = resid[size_t(t) * n + i] + o;
-    out[size_t(t) * n + i] = o;
+    if (resid)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = resid[size_t(t) * n + i + q] + o[q];
+    *reinterpret_cast<float4*>(out + size_t(t) * n + i) = make_float4(o[0], o[1], o[2], o[3]);
+}
+
+// fp32 -> bf16 (round to nearest even), 4 per thread (count % 4 == 0)
+__global__ void k_to_bf16(const float* __restrict__ src, __hip_bfloat16* __restrict__ dst, size_t count) {
+    const size_t i = (size_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+    if (i >= count) return;
+    const float4 v = *reinterpret_cast<const float4*>(src + i);
+    dst[i] = __float2bfloat16(v.x);
+    dst[i + 1] = __float2bfloat16(v.y);
+    dst[i + 2] = __float2bfloat16(v.z);
+    dst[i + 3] = __float2bfloat16(v.w);
 }
 
 }  // namespace
@@ -425,12 +483,11 @@ __global__ void __launch_bounds__(256) k_pf_combine(const InT* __restrict__ yd, 
 struct PfWs {
     int32_t *cnt, *bounds, *tok_of, *slot_of, *n_tiles;
     int2* tiles;
-    int8_t* xq;
-    float* xd;
-    _Float16* xq16;
-    _Float16* hq16;
-    float* hd;
-    float* yd;   // only when the layer path owns it
+    _Float16* xhi;
+    _Float16* xlo;
+    _Float16* hhi;
+    _Float16* hlo;
+    float* yd;   // fp32 per-slot outputs when the caller does not receive them as fp32
     size_t bytes;
 };
 
@@ -453,11 +510,10 @@ static PfWs pf_carve(void* base, int T, int K, int n, int ff, int E, bool shared
     w.slot_of = reinterpret_cast<int32_t*>(take(size_t(S) * 4));
     w.n_tiles = reinterpret_cast<int32_t*>(take(4));
     w.tiles = reinterpret_cast<int2*>(take(size_t(pf_max_tiles(S, G)) * 8));
-    w.xq = reinterpret_cast<int8_t*>(take(size_t(T) * n));
-    w.xd = reinterpret_cast<float*>(take(size_t(T) * (n / kQ8) * 4));
-    w.xq16 = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
-    w.hq16 = reinterpret_cast<_Float16*>(take(size_t(S) * ff * 2));
-    w.hd = reinterpret_cast<float*>(take(size_t(S) * (ff / kQ8) * 4));
+    w.xhi = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
+    w.xlo = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
+    w.hhi = reinterpret_cast<_Float16*>(take(size_t(S) * ff * 2));
+    w.hlo = reinterpret_cast<_Float16*>(take(size_t(S) * ff * 2));
     w.yd = own_yd ? reinterpret_cast<float*>(take(size_t(S) * n * 4)) : nullptr;
     w.bytes = size_t(p - static_cast<uint8_t*>(base));
     return w;
@@ -467,11 +523,13 @@ size_t pf_workspace_bytes(int T, int K, int n, int ff, int E, bool shared, bool 
     return pf_carve(nullptr, T, K, n, ff, E, shared, own_yd).bytes + 256;
 }
 
-int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xq16, hipStream_t stream);
+int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xhi, _Float16* xlo,
+                hipStream_t stream);
 
 int pf_check(int T, int K, int n, int ff, int E) {
     if (T < 1 || K < 1 || K > 32 || E < 1 || E > 4096 || K > E) return set_error(kErrShape, "prefill: T=%d K=%d E=%d", T, K, E);
-    if (n % 128 || ff % 64 || n < 128 || ff < 64 || ff > 4096) return set_error(kErrShape, "prefill: n=%d ff=%d (n %% 128, ff %% 64)", n, ff);
+    if (n % 256 || ff % 128 || n < 256 || ff < 128)
+        return set_error(kErrShape, "prefill: n=%d ff=%d (n a multiple of 256, ff of 128)", n, ff);
     return kOk;
 }
 
@@ -486,7 +544,7 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
     const int nchunk = (T * K + kChunk - 1) / kChunk;
     int id_bits = 1;
     while ((1 << id_bits) < E) ++id_bits;
-    if (int rc = quantize_q8(x, T, n, w.xq, w.xd, w.xq16, stream)) return rc;
+    if (int rc = quantize_q8(x, T, n, nullptr, nullptr, w.xhi, w.xlo, stream)) return rc;
     timing_mark(stream, "pf_quant_x");
     k_pf_hist<<<nchunk, 256, size_t(E) * 4, stream>>>(ids, T * K, E, w.cnt);
     k_pf_scan<<<1, 1024, 0, stream>>>(w.cnt, nchunk, E, T, K, shared ? 1 : 0, w.bounds, w.tiles, w.n_tiles);
@@ -494,23 +552,22 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
     if (shared) k_pf_place_shared<<<(T + 255) / 256, 256, 0, stream>>>(T, K, w.tok_of, w.slot_of);
     timing_mark(stream, "pf_dispatch");
     const int mt = pf_max_tiles(S, G);
-    k_pf_gateup<<<dim3(ff / 64, mt), 256, 0, stream>>>(arena, stride, E, shared_blob, n, ff, w.xq16, w.xd, w.tok_of,
-                                                       w.bounds, w.tiles, w.n_tiles, w.hq16, w.hd);
+    const size_t smem = 2 * sizeof(MmStage);
+    FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_mm<true>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                int(smem)));
+    FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_mm<false>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                int(smem)));
+    k_pf_mm<true><<<dim3((ff + 255) / 256, mt), 512, smem, stream>>>(arena, stride, E, shared_blob, n, ff, w.xhi, w.xlo,
+                                                                     w.tok_of, w.bounds, w.tiles, w.n_tiles, w.hhi, w.hlo,
+                                                                     nullptr, nullptr);
     timing_mark(stream, "pf_gateup");
-    const int nbf = ff / kBlock;
-    const size_t smem = size_t(kTN) * (ff + 8) * 2 + size_t(kTN) * (ff / kQ8) * 4 + size_t(64) * nbf * 16 + size_t(64) * nbf * 2;
+    float* ydf = yd_kind == 1 ? w.yd : static_cast<float*>(yd);
+    k_pf_mm<false><<<dim3((n + 511) / 512, mt), 512, smem, stream>>>(arena, stride, E, shared_blob, n, ff, w.hhi, w.hlo,
+                                                                      w.tok_of, w.bounds, w.tiles, w.n_tiles, nullptr,
+                                                                      nullptr, ydf, w.slot_of);
     if (yd_kind == 1) {
-        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_down<__hip_bfloat16>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(smem)));
-        k_pf_down<__hip_bfloat16><<<dim3(n / 64, mt), 256, smem, stream>>>(arena, stride, E, shared_blob, n, ff, w.hq16, w.hd,
-                                                                           w.slot_of, w.bounds, w.tiles, w.n_tiles,
-                                                                           static_cast<__hip_bfloat16*>(yd));
-    } else {
-        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_down<float>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(smem)));
-        k_pf_down<float><<<dim3(n / 64, mt), 256, smem, stream>>>(arena, stride, E, shared_blob, n, ff, w.hq16, w.hd,
-                                                                  w.slot_of, w.bounds, w.tiles, w.n_tiles,
-                                                                  static_cast<float*>(yd));
+        const size_t cntv = size_t(S) * n;
+        k_to_bf16<<<unsigned((cntv / 4 + 255) / 256), 256, 0, stream>>>(ydf, static_cast<__hip_bfloat16*>(yd), cntv);
     }
     timing_mark(stream, "pf_down");
     FRT_LAUNCHED("prefill experts");
@@ -523,7 +580,7 @@ int pf_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const fl
     if (int rc = pf_check(T, K, n, ff, E)) return rc;
     if (block64) return set_error(kErrShape, "moe_q2::run: block64 activations are not supported (Q8_0 blocks of 32 only)");
     if (!experts || !x || !ids || !yd || !ws) return set_error(kErrNull, "moe_q2::run: null pointer");
-    const PfWs w = pf_carve(ws, T, K, n, ff, E, false, false);
+    const PfWs w = pf_carve(ws, T, K, n, ff, E, false, yd_bf16 != 0);
     if (w.bytes > ws_bytes) return set_error(kErrWorkspace, "moe_q2::run: workspace %zu < %zu", ws_bytes, w.bytes);
     return pf_experts(experts, stride, E, nullptr, n, ff, x, ids, T, K, yd, yd_bf16 ? 1 : 0, w, stream);
 }
@@ -536,7 +593,7 @@ int pf_moe(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blo
     const PfWs w = pf_carve(ws, T, K, n, ff, E, true, true);
     if (w.bytes > ws_bytes) return set_error(kErrWorkspace, "prefill: workspace %zu < %zu", ws_bytes, w.bytes);
     if (int rc = pf_experts(arena, stride, E, shared_blob, n, ff, x, ids, T, K, w.yd, 0, w, stream)) return rc;
-    k_pf_combine<float><<<dim3((n + 255) / 256, T), 256, 0, stream>>>(w.yd, ids, wts, gate, T, K, n, 1, resid, out);
+    k_pf_combine<float><<<dim3((n + 1023) / 1024, T), 256, 0, stream>>>(w.yd, ids, wts, gate, T, K, n, 1, resid, out);
     timing_mark(stream, "pf_combine");
     FRT_LAUNCHED("prefill combine");
     return kOk;

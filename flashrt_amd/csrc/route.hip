@@ -131,27 +131,34 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, in
 // xq int8 [rows][n] natural order, xd [rows][n/32]. With xq16: the same codes as fp16 in the
 // prefill GEMM's operand order (perm64 below), [rows][n].
 __global__ void k_quant_q8(const float* __restrict__ x, int n_blocks, int8_t* __restrict__ xq, float* __restrict__ xd,
-                           _Float16* __restrict__ xq16, int n) {
+                           _Float16* __restrict__ xhi, _Float16* __restrict__ xlo, int n) {
     const int gw = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;   // global wave
     const int lane = threadIdx.x & 63;
     const int blk = gw * 2 + (lane >> 5);
-    if (blk >= n_blocks) return;
+    if (gw * 2 >= n_blocks) return;   // whole waves only (the max below is across the wave's rows)
+    const bool live = blk < n_blocks;
     const int j = lane & 31;
-    const float v = x[size_t(blk) * kQ8 + j];
+    const float v = live ? x[size_t(blk) * kQ8 + j] : 0.0f;
     const float am = half_max(fabsf(v));
     const float d = q8_scale(am);
     const float id = q8_inv(d);
     const int q = q8_code(v, id);
-    xq[size_t(blk) * kQ8 + j] = int8_t(q);
-    if (j == 0) xd[blk] = f16_round(d);
-    if (xq16) {
-        // position of element e of a 64-block in the permuted order: inverse of perm64_elem
-        const int e = (blk & 1) * 32 + j;   // element within the 64-block
+    if (!live) return;
+    if (xq) xq[size_t(blk) * kQ8 + j] = int8_t(q);
+    const float dr = f16_round(d);
+    if (xd && j == 0) xd[blk] = dr;
+    if (xhi) {
+        // the activation q * d as an exact fp16 pair, at its position in the perm64 order of the
+        // prefill GEMM (element 16 s + 4 g + c of a 64-block sits at 32 (s / 2) + 8 g + 4 (s % 2) + ci,
+        // ci = 0, 2, 1, 3 for c = 0, 1, 2, 3)
+        const int e = (blk & 1) * 32 + j;
         const int s = e >> 4, g = (e >> 2) & 3, c = e & 3;
-        const int h = s >> 1, ci = c == 0 ? 0 : c == 1 ? 2 : c == 2 ? 1 : 3;
-        const int slot = (s & 1) * 4 + ci;
-        const size_t base = size_t(blk >> 1) * kBlock;
-        xq16[base + h * 32 + g * 8 + slot] = _Float16(float(q));
+        const int ci = c == 0 ? 0 : c == 1 ? 2 : c == 2 ? 1 : 3;
+        const size_t pos = size_t(blk >> 1) * kBlock + (s >> 1) * 32 + g * 8 + (s & 1) * 4 + ci;
+        const float a = float(q) * dr;
+        const _Float16 hi = _Float16(a);
+        xhi[pos] = hi;
+        xlo[pos] = _Float16(a - float(hi));
     }
 }
 
@@ -226,11 +233,12 @@ int rmsnorm(const float* x, int T, int n, float* u, hipStream_t stream) {
     return kOk;
 }
 
-int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xq16, hipStream_t stream) {
+int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xhi, _Float16* xlo,
+                hipStream_t stream) {
     if (rows < 1 || n % 64) return set_error(kErrShape, "quantize_q8: n=%d not a multiple of 64", n);
     const int nb = rows * (n / kQ8);
     const int waves = (nb + 1) / 2;
-    k_quant_q8<<<(waves + 3) / 4, 256, 0, stream>>>(x, nb, xq, xd, xq16, n);
+    k_quant_q8<<<(waves + 3) / 4, 256, 0, stream>>>(x, nb, xq, xd, xhi, xlo, n);
     FRT_LAUNCHED("quantize_q8");
     return kOk;
 }
@@ -244,6 +252,135 @@ int route_topk(hipStream_t stream, const float* logits, int T, int E, int K, int
     if (E <= 512) k_route_topk<8><<<grid, 256, 0, stream>>>(logits, T, E, K, ids, wts, counts, tail_counts, tail_from);
     else k_route_topk<16><<<grid, 256, 0, stream>>>(logits, T, E, K, ids, wts, counts, tail_counts, tail_from);
     FRT_LAUNCHED("moe_route_topk");
+    return kOk;
+}
+
+}  // namespace frt
+
+// ---------------------------------------------------------------- prefill router GEMM
+namespace frt {
+namespace {
+
+// logits [T][E] for many tokens, canonical order: K runs in natural order in tiles of L = n / 64
+// (one chain each); after each tile the chain sum joins a pairwise-tree stack (the adjacent pairwise
+// tree over chains 0..63 is a binary counter: chain j merges with the completed subtrees named by
+// the trailing one bits of j + 1), so the result equals the tree ((c0+c1)+(c2+c3))+... exactly.
+// Workgroup tile 64 tokens x 64 experts, 256 threads, 4 x 4 outputs per thread; x and W tiles in
+// LDS as [k][64] so a thread reads its 4 tokens and 4 experts as one float4 each.
+template <int L>
+__global__ void __launch_bounds__(256) k_router_gemm(const float* __restrict__ x, int T, const float* __restrict__ W,
+                                                     const float* __restrict__ bias, int E, float* __restrict__ logits) {
+    __shared__ __align__(16) float sx[2][L][64];
+    __shared__ __align__(16) float sw[2][L][64];
+    const int n = 64 * L;
+    const int t0 = blockIdx.y * 64, e0 = blockIdx.x * 64;
+    const int tid = threadIdx.x;
+    const int tr = (tid & 15) * 4, er = (tid >> 4) * 4;   // this thread's 4 tokens and 4 experts
+    // level registers of the pairwise tree: after chain c, lv[m] holds the pending subtree of level m
+    // when bit m of c + 1 ... (see merge below)
+    float lv[4][4][6];
+    constexpr int F4 = L / 4;                    // float4 per row and chain
+    constexpr int NP = (64 * F4 + 255) / 256;    // staging passes
+    float4 rx[NP], rw[NP];
+    auto load = [&](int c) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const int idx = p * 256 + tid;
+            const int row = idx / F4, q = idx % F4;
+            const int t = t0 + row, e = e0 + row;
+            const bool in = idx < 64 * F4;
+            rx[p] = in && t < T ? *reinterpret_cast<const float4*>(x + size_t(t) * n + c * L + q * 4) : make_float4(0, 0, 0, 0);
+            rw[p] = in && e < E ? *reinterpret_cast<const float4*>(W + size_t(e) * n + c * L + q * 4) : make_float4(0, 0, 0, 0);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const int idx = p * 256 + tid;
+            if (idx >= 64 * F4) continue;
+            const int row = idx / F4, q = idx % F4;
+            sx[buf][q * 4 + 0][row] = rx[p].x;
+            sx[buf][q * 4 + 1][row] = rx[p].y;
+            sx[buf][q * 4 + 2][row] = rx[p].z;
+            sx[buf][q * 4 + 3][row] = rx[p].w;
+            sw[buf][q * 4 + 0][row] = rw[p].x;
+            sw[buf][q * 4 + 1][row] = rw[p].y;
+            sw[buf][q * 4 + 2][row] = rw[p].z;
+            sw[buf][q * 4 + 3][row] = rw[p].w;
+        }
+    };
+    load(0);
+    store(0);
+    __syncthreads();
+    float total[4][4];
+    for (int c = 0; c < 64; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < 64) load(c + 1);
+        float acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < L; ++k) {
+            const float4 xv = *reinterpret_cast<const float4*>(&sx[buf][k][tr]);
+            const float4 wv = *reinterpret_cast<const float4*>(&sw[buf][k][er]);
+            const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, wa[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(wa[j], xa[i], acc[i][j]);
+        }
+        // chain c joins the tree: for each level m while bit m of c is set, merge with the pending
+        // left subtree of that level; the first clear bit parks the value there (uniform branches)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v = acc[i][j];
+                bool parked = false;
+#pragma unroll
+                for (int m = 0; m < 6; ++m) {
+                    if (parked) continue;
+                    if (((c >> m) & 1) == 0) {
+                        lv[i][j][m] = v;
+                        parked = true;
+                    } else {
+                        v = lv[i][j][m] + v;
+                    }
+                }
+                if (!parked) total[i][j] = v;   // c == 63: the whole tree
+            }
+        if (c + 1 < 64) {
+            store(buf ^ 1);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = t0 + tr + i, e = e0 + er + j;
+            if (t < T && e < E) logits[size_t(t) * E + e] = bias ? total[i][j] + bias[e] : total[i][j];
+        }
+}
+
+}  // namespace
+
+int router_gemm(const float* x, int T, const float* W, const float* bias, int E, int n, float* logits,
+                hipStream_t stream) {
+    if (n != 2048 && n != 2560 && n != 1024 && n != 3072 && n != 4096)
+        return set_error(kErrShape, "router_gemm: n=%d", n);
+    dim3 grid((E + 63) / 64, (T + 63) / 64);
+    switch (n / 64) {
+        case 16: k_router_gemm<16><<<grid, 256, 0, stream>>>(x, T, W, bias, E, logits); break;
+        case 32: k_router_gemm<32><<<grid, 256, 0, stream>>>(x, T, W, bias, E, logits); break;
+        case 40: k_router_gemm<40><<<grid, 256, 0, stream>>>(x, T, W, bias, E, logits); break;
+        case 48: k_router_gemm<48><<<grid, 256, 0, stream>>>(x, T, W, bias, E, logits); break;
+        case 64: k_router_gemm<64><<<grid, 256, 0, stream>>>(x, T, W, bias, E, logits); break;
+        default: return set_error(kErrShape, "router_gemm: n=%d", n);
+    }
+    FRT_LAUNCHED("router_gemm");
     return kOk;
 }
 

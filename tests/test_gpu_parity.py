@@ -268,7 +268,7 @@ def test_moe_q2_run(F, w0, yd_bf16):
             ref = O.expert_ffn(w0.blob(int(ids[t, k])), H.N, H.FF, x[t])
             assert H.out_rel(y[t, k][None], ref) <= tol, (t, k)
     with pytest.raises(F.FrtError) as e:
-        F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, nb - 1024)
+        F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, 4096)
     assert e.value.code == -2
     with pytest.raises(F.FrtError):
         F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, nb, None, True)
