@@ -199,51 +199,49 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 
 // ---------------------------------------------------------------- grouped GEMMs (gate + up, down)
 //
-// Operands are exact in fp16 and the products exact in fp32: weights (q - 1) * d_w (dequantized in
-// registers from the code dwords) and activations a = code * d (Q8_0: at most 18 significant bits)
-// stored as a pair hi = fp16(a), lo = fp16(a - hi), so that A * hi + A * lo = A * a exactly. Each
-// 32-deep MFMA step is issued twice (hi, lo) into one fp32 accumulator: no per-block scaling on the
-// VALU (gfx950's MFMA keeps fp16 subnormals, which the lo parts often are).
+// Weights enter the MFMA exactly: (q - 1) * d_w in fp16, dequantized in registers from the code
+// dwords. Activations a = code * d (Q8_0: up to 18 significant bits) enter in NP fp16 parts:
+//   NP = 2 (gate/up): hi = fp16(a), lo = fp16(a - hi), so that A * hi + A * lo = A * a exactly; each
+//          32-deep MFMA step is issued for both parts into one fp32 accumulator (gfx950's MFMA keeps
+//          fp16 subnormals, which the lo parts often are). Exactness here matters because h is
+//          requantized to Q8_0 after SwiGLU.
+//   NP = 1 (down): fp16(a), 2^-12 relative per element, with no requantization after it.
+// No per-block scaling on the VALU either way.
 //
 // Workgroup: 512 threads (8 waves), 64 tokens x 512 A rows, K in stages of 128 through two LDS
 // buffers (the next stage is loaded into registers while the current one is multiplied). Each wave
 // owns 4 A tiles of 16 rows and all 4 token tiles, so every activation fragment read from LDS feeds
-// 8 MFMAs.
+// 4 NP MFMAs.
 //   gate+up: A rows 0..255 are gate rows f0 + 0..255, A rows 256..511 the same up rows; wave w owns
 //            ff rows f0 + 32 w .. +31 (gate and up). Epilogue: SwiGLU, Q8_0 of the 32-row block of h
-//            (quant/q2_0/moe_cpu.cpp:43-61), h written as hi/lo for the down GEMM.
+//            (quant/q2_0/moe_cpu.cpp:43-61), h = code * d written as fp16 for the down GEMM.
 //   down:    A rows are output rows r0 + 0..511, wave w owns r0 + 64 w .. +63; yd[slot][row] fp32.
 
 constexpr int kKC = 128;          // K per stage
 constexpr int kLdB = kKC + 8;     // padded fp16 row of an activation stage
 
+template <int NP>
 struct MmStage {
     uint32_t a[512][kKC / 64][4];   // codes: A row, block, dword
     uint32_t sc[512];               // the A row's two fp16 block scales
-    _Float16 bh[kTN][kLdB];         // activations, hi part (perm64 order)
-    _Float16 bl[kTN][kLdB];         // activations, lo part
+    _Float16 b[NP][kTN][kLdB];      // activations (perm64 order): [0] fp16(a), [1] a - [0] when NP == 2
 };
 
 __device__ __forceinline__ floatx4 mfma_acc(half8 a, half8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ void split_hi_lo(float a, _Float16& hi, _Float16& lo) {
-    hi = _Float16(a);
-    lo = _Float16(a - float(hi));
-}
-
-template <bool GATEUP>
+template <bool GATEUP, int NP>
 __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena, size_t stride, int E,
                                                const uint8_t* __restrict__ shared_blob, int n, int ff,
                                                const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
                                                const int32_t* __restrict__ tok_of, const int32_t* __restrict__ bounds,
                                                const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-                                               _Float16* __restrict__ hhi, _Float16* __restrict__ hlo,
+                                               _Float16* __restrict__ hout,
                                                float* __restrict__ yd, const int32_t* __restrict__ slot_of) {
     if (int(blockIdx.y) >= *n_tiles) return;
     extern __shared__ __align__(16) uint8_t smem[];
-    MmStage* st = reinterpret_cast<MmStage*>(smem);
+    MmStage<NP>* st = reinterpret_cast<MmStage<NP>*>(smem);
     __shared__ int sTok[kTN];
     const int2 tile = tiles[blockIdx.y];
     const int grp = tile.x;
@@ -273,7 +271,7 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
     };
     uint4 ra[2];
     uint32_t rs;
-    uint4 rb[4];
+    uint4 rb[2 * NP];
     auto load = [&](int k0) {
         const int b0 = k0 / kBlock;
 #pragma unroll
@@ -293,14 +291,14 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
             rs = r < rows_total ? *sc : 0u;
         }
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
+        for (int p = 0; p < 2 * NP; ++p) {
             const int idx = p * 512 + tid, which = idx >> 10, rem = idx & 1023, j = rem >> 4, q = rem & 15;
             const int t = sTok[j];
             const _Float16* src = which ? blo : bhi;
             rb[p] = t >= 0 ? *reinterpret_cast<const uint4*>(src + size_t(t) * Kd + k0 + q * 8) : make_uint4(0, 0, 0, 0);
         }
     };
-    auto store = [&](MmStage& S) {
+    auto store = [&](MmStage<NP>& S) {
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const int idx = p * 512 + tid, ar = idx >> 1, blk = idx & 1;
@@ -308,10 +306,9 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
         }
         S.sc[tid] = rs;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
+        for (int p = 0; p < 2 * NP; ++p) {
             const int idx = p * 512 + tid, which = idx >> 10, rem = idx & 1023, j = rem >> 4, q = rem & 15;
-            _Float16* dst = which ? &S.bl[j][q * 8] : &S.bh[j][q * 8];
-            *reinterpret_cast<uint4*>(dst) = rb[p];
+            *reinterpret_cast<uint4*>(&S.b[which][j][q * 8]) = rb[p];
         }
     };
 
@@ -331,7 +328,7 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
     store(st[0]);
     __syncthreads();
     for (int sI = 0; sI < nstage; ++sI) {
-        MmStage& S = st[sI & 1];
+        MmStage<NP>& S = st[sI & 1];
         if (sI + 1 < nstage) load((sI + 1) * kKC);
 #pragma unroll
         for (int bb = 0; bb < kKC / 64; ++bb) {
@@ -350,12 +347,11 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int col = c * 16 + li, off = bb * 64 + h * 32 + lg * 8;
-                    const half8 bh = *reinterpret_cast<const half8*>(&S.bh[col][off]);
-                    const half8 bl = *reinterpret_cast<const half8*>(&S.bl[col][off]);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        acc[i][c] = mfma_acc(av[i], bh, acc[i][c]);
-                        acc[i][c] = mfma_acc(av[i], bl, acc[i][c]);
+                    for (int part = 0; part < NP; ++part) {
+                        const half8 bv = *reinterpret_cast<const half8*>(&S.b[part][col][off]);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[i][c] = mfma_acc(av[i], bv, acc[i][c]);
                     }
                 }
             }
@@ -395,11 +391,8 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
                     for (int j = 0; j < 4; ++j) {
                         const int f = fbase + 16 * i + 4 * lg + j;
                         const float a = float(q8_code(hv[i][j], id)) * dr;
-                        _Float16 hi, lo;
-                        split_hi_lo(a, hi, lo);
                         const size_t pos = row * ff + (f & ~63) + perm64_pos(f & 63);
-                        hhi[pos] = hi;
-                        hlo[pos] = lo;
+                        hout[pos] = _Float16(a);   // h for the down GEMM, one fp16 part
                     }
             }
         }
@@ -486,7 +479,6 @@ struct PfWs {
     _Float16* xhi;
     _Float16* xlo;
     _Float16* hhi;
-    _Float16* hlo;
     float* yd;   // fp32 per-slot outputs when the caller does not receive them as fp32
     size_t bytes;
 };
@@ -513,7 +505,6 @@ static PfWs pf_carve(void* base, int T, int K, int n, int ff, int E, bool shared
     w.xhi = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
     w.xlo = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
     w.hhi = reinterpret_cast<_Float16*>(take(size_t(S) * ff * 2));
-    w.hlo = reinterpret_cast<_Float16*>(take(size_t(S) * ff * 2));
     w.yd = own_yd ? reinterpret_cast<float*>(take(size_t(S) * n * 4)) : nullptr;
     w.bytes = size_t(p - static_cast<uint8_t*>(base));
     return w;
@@ -530,6 +521,35 @@ int pf_check(int T, int K, int n, int ff, int E) {
     if (T < 1 || K < 1 || K > 32 || E < 1 || E > 4096 || K > E) return set_error(kErrShape, "prefill: T=%d K=%d E=%d", T, K, E);
     if (n % 256 || ff % 128 || n < 256 || ff < 128)
         return set_error(kErrShape, "prefill: n=%d ff=%d (n a multiple of 256, ff of 128)", n, ff);
+    return kOk;
+}
+
+template <bool GATEUP, int NP>
+static int pf_mm_attr() {
+    static bool done = false;   // per process; the attribute is a property of the kernel
+    if (!done) {
+        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_mm<GATEUP, NP>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(2 * sizeof(MmStage<NP>))));
+        done = true;
+    }
+    return kOk;
+}
+
+// The two grouped GEMMs. gate/up reads x as exact hi/lo pairs: h is requantized to Q8_0 after
+// SwiGLU, and an fp16 rounding of x (2^-12 relative) moves enough h values across a code boundary
+// to be seen at the output. down reads h as single fp16 values (2^-12 relative per element,
+// summed with no requantization after it).
+static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, int n, int ff,
+                           const PfWs& w, int mt, float* ydf, hipStream_t stream) {
+    if (int rc = pf_mm_attr<true, 2>()) return rc;
+    if (int rc = pf_mm_attr<false, 1>()) return rc;
+    k_pf_mm<true, 2><<<dim3((ff + 255) / 256, mt), 512, 2 * sizeof(MmStage<2>), stream>>>(
+        arena, stride, E, shared_blob, n, ff, w.xhi, w.xlo, w.tok_of, w.bounds, w.tiles, w.n_tiles, w.hhi, nullptr,
+        nullptr);
+    timing_mark(stream, "pf_gateup");
+    k_pf_mm<false, 1><<<dim3((n + 511) / 512, mt), 512, 2 * sizeof(MmStage<1>), stream>>>(
+        arena, stride, E, shared_blob, n, ff, w.hhi, nullptr, w.tok_of, w.bounds, w.tiles, w.n_tiles, nullptr, ydf,
+        w.slot_of);
     return kOk;
 }
 
@@ -552,19 +572,8 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
     if (shared) k_pf_place_shared<<<(T + 255) / 256, 256, 0, stream>>>(T, K, w.tok_of, w.slot_of);
     timing_mark(stream, "pf_dispatch");
     const int mt = pf_max_tiles(S, G);
-    const size_t smem = 2 * sizeof(MmStage);
-    FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_mm<true>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                int(smem)));
-    FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_mm<false>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                int(smem)));
-    k_pf_mm<true><<<dim3((ff + 255) / 256, mt), 512, smem, stream>>>(arena, stride, E, shared_blob, n, ff, w.xhi, w.xlo,
-                                                                     w.tok_of, w.bounds, w.tiles, w.n_tiles, w.hhi, w.hlo,
-                                                                     nullptr, nullptr);
-    timing_mark(stream, "pf_gateup");
     float* ydf = yd_kind == 1 ? w.yd : static_cast<float*>(yd);
-    k_pf_mm<false><<<dim3((n + 511) / 512, mt), 512, smem, stream>>>(arena, stride, E, shared_blob, n, ff, w.hhi, w.hlo,
-                                                                      w.tok_of, w.bounds, w.tiles, w.n_tiles, nullptr,
-                                                                      nullptr, ydf, w.slot_of);
+    if (int rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, w, mt, ydf, stream)) return rc;
     if (yd_kind == 1) {
         const size_t cntv = size_t(S) * n;
         k_to_bf16<<<unsigned((cntv / 4 + 255) / 256), 256, 0, stream>>>(ydf, static_cast<__hip_bfloat16*>(yd), cntv);

@@ -266,7 +266,8 @@ def test_moe_q2_run(F, w0, yd_bf16):
     for t in range(0, T, 5):
         for k in range(K):
             ref = O.expert_ffn(w0.blob(int(ids[t, k])), H.N, H.FF, x[t])
-            assert H.out_rel(y[t, k][None], ref) <= tol, (t, k)
+            err = H.out_rel(y[t, k][None], ref)
+            assert err <= tol, (t, k, err)
     with pytest.raises(F.FrtError) as e:
         F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, 4096)
     assert e.value.code == -2
