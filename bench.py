@@ -36,6 +36,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 N, FF, E, K, LAYERS = 2048, 512, 512, 10, 48
 ZIPF_STACK, ZIPF_PREFILL, PREFILL_ALPHA = 1.1, 1.2, 0.4
+SPIN_CYCLES = 100_000_000   # torch.cuda._sleep ahead of an eager timing pass (tens of ms)
 
 
 def log(*a):
@@ -130,15 +131,18 @@ def run_stack(args, F, torch):
     log(f"stack: {args.steps} steps x {layers} layers: {gpu_ms:.2f} ms on the stream ({wall * 1e3:.2f} ms wall), "
         f"{ms_per_step * 1e3:.1f} us/token")
 
-    # per-kernel durations, eager launches on the same stream
-    def eager():
+    # per-kernel durations: eager launches on the same stream, queued behind a spin kernel so that
+    # the host has enqueued them all before the GPU reaches them (the event deltas then measure the
+    # GPU, not the host's launch rate)
+    def eager(n_steps):
         with torch.cuda.stream(stream):
-            for s in range(min(32, total_steps)):
+            torch.cuda._sleep(SPIN_CYCLES)
+            for s in range(n_steps):
                 xin.copy_(xs[s:s + 1])
                 step_body()
-    eager()
+    eager(1)
     stream.synchronize()
-    kt = kernel_times(F, eager)
+    kt = kernel_times(F, lambda: eager(args.timing_steps))
     del graph
     res = dict(ms_per_step=ms_per_step, wall_s=wall, kernels=kt)
     res["_keep"] = (arena, shared, router, gate, bias, mls, xs, ws)
@@ -184,6 +188,7 @@ def run_prefill(args, F, torch):
 
     def eager():
         with torch.cuda.stream(stream):
+            torch.cuda._sleep(SPIN_CYCLES)
             for _ in range(reps):
                 ml.forward(x, out, T=T, ws=ws)
     kt = kernel_times(F, eager)
@@ -309,6 +314,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="first run 3 plain device copies of MIB MiB (scales the HBM byte counters of a profile)")
+    ap.add_argument("--timing-steps", type=int, default=3, help="decode steps in the per-kernel timing pass")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=4)
@@ -321,6 +329,13 @@ def main():
     import flashrt_amd as F
     F.lib()
     torch.cuda.set_device(0)
+    if args.calib_copy:
+        src = torch.ones(args.calib_copy << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     st = run_stack(args, F, torch)
     ms = st["ms_per_step"]
@@ -331,10 +346,10 @@ def main():
 
     # roofline of the dominant decode kernel
     kt = st["kernels"]
-    per_launch_bytes = {
-        "dec_gateup": (K + 1) * 2 * F.lib().frt_q2_mat_bytes(FF, N),
+    per_launch_bytes = {   # algorithmic HBM bytes per launch (weights read once; activations are KB)
+        "dec_route_gateup": (K + 1) * 2 * F.lib().frt_q2_mat_bytes(FF, N),
         "dec_down": (K + 1) * F.lib().frt_q2_mat_bytes(N, FF),
-        "router": E * N * 4 + N * 4,
+        "router_quant": E * N * 4 + N * 4,
     }
     dom = max(kt, key=lambda k: kt[k][0])
     dom_avg_ms = kt[dom][0] / kt[dom][1]
@@ -351,7 +366,7 @@ def main():
     tf = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tf):
         with open(tf) as f:
-            traffic = json.load(f).get(dom)
+            traffic = (json.load(f).get(dom) or {}).get("bytes")   # HBM bytes per launch, from rocprofv3 PMC
 
     line = {
         "metric": METRIC,
