@@ -62,3 +62,13 @@ def test_product_does_not_use_the_oracle():
                 text = open(os.path.join(dirpath, f)).read()
                 assert not re.search(r"(import\s+oracle|from\s+oracle|liboracle|libfrref|oracle/)", text), \
                     os.path.join(dirpath, f)
+
+
+def test_cpp_mirror_host():
+    """The C++ mirror (include/flashrt_moe.hpp) compiles into a client and maps status codes to
+    std::runtime_error (built by `make -C flashrt_amd/csrc`)."""
+    import subprocess
+    exe = os.path.join(ROOT, "tests", "cpp", "_build", "test_shim")
+    assert os.path.exists(exe), "build first: make -C flashrt_amd/csrc"
+    r = subprocess.run([exe, "--host"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and "all passed" in r.stdout, r.stdout + r.stderr

@@ -5,6 +5,8 @@ Bars: ids and the dispatch permutation bit-exact; routing weights <= 1e-6 relati
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -298,6 +300,37 @@ def test_layer_prefill_config3(F):
     assert np.isfinite(out).all()
 
 
+def test_layer_mixed_config4(F):
+    """Config 4: an 8192-token bf16 prefill chunk plus 16 uncorrelated fp32 decode tokens in one
+    launch (T = 8208), with adversarial popularity: +2.8 on the logits of 16 seeded hot experts puts
+    about 90% of the top-10 selections on them. All 8208 tokens' ids are bit-exact and the weights
+    in tolerance; the outputs of 32 prefill and all 16 decode tokens are checked against the oracle."""
+    import torch
+    T_pf, T_dec = 8192, 16
+    hot = np.random.default_rng(4).permutation(H.E)[:16]
+    bias = np.zeros(H.E, np.float32)
+    bias[hot] = 2.8
+    w4 = H.World(cfg=4, bias=bias)
+    xp = torch.empty((T_pf, H.N), dtype=torch.float32, device="cuda")
+    F.gen.normal(xp, 4, 0, O.X_TENSOR, 1.0, round_bf16=True)
+    xd = torch.empty((T_dec, H.N), dtype=torch.float32, device="cuda")
+    F.gen.normal(xd, 4, 0, O.X_TENSOR + 1, 1.0)
+    x = np.concatenate([xp.cpu().numpy(), xd.cpu().numpy()])
+    out, ids, wts = w4.gpu_forward(x)
+    lg = O.router_logits(x, w4.router_h, bias)
+    rid, rw, _ = O.route_topk(lg, H.K)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    frac = float(np.isin(ids, hot).mean())
+    print(f"hot-expert share of the selections: {frac:.3f}")
+    assert 0.85 <= frac <= 0.95
+    sel = np.concatenate([np.random.default_rng(1).choice(T_pf, size=32, replace=False), np.arange(T_pf, T_pf + T_dec)])
+    ref, sid, _, _ = w4.oracle_forward(x[sel])
+    assert np.array_equal(sid, ids[sel])
+    assert H.out_rel(out[sel], ref) <= H.OUT_REL
+    assert np.isfinite(out).all()
+
+
 def test_layer_errors(F, w0):
     x = torch.zeros((1, H.N), dtype=torch.float32, device="cuda")
     out = torch.zeros((1, H.N), dtype=torch.float32, device="cuda")
@@ -333,3 +366,15 @@ def test_rmsnorm_router_bit_exact(F):
     x = (rng.standard_normal((2, H.N)) * 5).astype(np.float32)
     u = O.rmsnorm(x)
     assert np.allclose((u.astype(np.float64) ** 2).mean(axis=1), 1.0, rtol=1e-5)
+
+
+def test_cpp_mirror_gpu():
+    """The C++ client of include/flashrt_moe.hpp on the GPU: moe_route_topk on the test_route_topk
+    recipe against std::stable_sort and a double softmax, and an arena round trip."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "tests", "cpp", "_build",
+                       "test_shim")
+    assert os.path.exists(exe), "build first: make -C flashrt_amd/csrc"
+    r = subprocess.run([exe, "--gpu"], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0 and "all passed" in r.stdout, r.stdout + r.stderr
