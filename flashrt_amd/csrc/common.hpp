@@ -53,7 +53,58 @@ void timing_mark(hipStream_t stream, const char* kernel);
 
 inline size_t up256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Phase probes for latency work (compiled out unless FRT_PHASE_PROBE is defined). Thread 0 of
+// each workgroup keeps the constant-rate (100 MHz) GPU clock of point i of slot k in LDS
+// (FRT_PROBE), and FRT_PROBE_END writes the table to frt_probe[k][workgroup][i] once at the end of
+// the kernel: a global store per point would make the next wait for a load also wait for the store.
+// The instrumented library exports frt_probe_dump() to read the table.
+#ifdef FRT_PHASE_PROBE
+extern __device__ unsigned long long frt_probe[4][2048][8];
+__device__ __forceinline__ unsigned long long* frt_probe_lds() {
+    __shared__ unsigned long long t[32];
+    return t;
+}
+#define FRT_PROBE_BEGIN()                                                  \
+    do {                                                                   \
+        if (threadIdx.x < 32) frt_probe_lds()[threadIdx.x] = 0;            \
+    } while (0)
+#define FRT_PROBE(k, i)                                                    \
+    do {                                                                   \
+        if (threadIdx.x == 0) frt_probe_lds()[(k) * 8 + (i)] = wall_clock64(); \
+    } while (0)
+#define FRT_PROBE_END()                                                                            \
+    do {                                                                                           \
+        if (threadIdx.x < 32 && frt_probe_lds()[threadIdx.x])                                      \
+            frt_probe[threadIdx.x / 8][blockIdx.x + blockIdx.y * gridDim.x][threadIdx.x % 8] =     \
+                frt_probe_lds()[threadIdx.x];                                                      \
+    } while (0)
+#else
+#define FRT_PROBE_BEGIN() \
+    do {                  \
+    } while (0)
+#define FRT_PROBE(k, i) \
+    do {                \
+    } while (0)
+#define FRT_PROBE_END() \
+    do {                \
+    } while (0)
+#endif
+
 // ---- device helpers
+
+// A load through the global address space; p must point into device global memory (an LDS or
+// private address given here is read as a global one). Pointers read from memory (the expert blob pointers of
+// an entry list) are otherwise generic, and generic (flat) loads share the wait counter of LDS and
+// scalar loads, so each LDS or scalar wait after them would also wait for the HBM round trip.
+template <class T>
+__device__ __forceinline__ T gld(const void* p) {
+    return *(const __attribute__((address_space(1))) T*)p;
+}
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 gld_u4(const void* p) {
+    const u32x4_t v = gld<u32x4_t>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 __device__ __forceinline__ float h2f(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 

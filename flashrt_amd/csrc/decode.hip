@@ -20,6 +20,7 @@
 #include "common.hpp"
 #include "topk.hpp"
 
+
 namespace frt {
 
 struct DecEntry {
@@ -38,16 +39,23 @@ namespace {
 
 __device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + expf(-g)); }
 
-// ---- the window's routing and its entry list, built in LDS by one 256-thread workgroup: wave t
-// routes token t (topk_wave); then wave 0, one lane per selection, orders the distinct experts
-// ascending (first occurrences ranked by id), the shared expert last, and numbers the compact slots.
-// Needs T * K <= 63. Returns the number of entries (every thread).
+// ---- the window's routing and its entry list, built in LDS by one 1024-thread workgroup: the 4
+// waves of group g route token g together (topk_group4); then wave 0, one lane per selection,
+// orders the distinct experts ascending (first occurrences ranked by id), the shared expert last,
+// and numbers the compact slots. Needs T * K <= 63. Returns the number of entries (every thread).
+// Each token's combine list: its K routed compact slots and weights in ascending expert id, then
+// the shared expert's slot and sigmoid(gate) at index K (moe_cpu.cpp:63-80 phase B order).
+struct DecComb {
+    int32_t slot[kDecMaxT][33];
+    float w[kDecMaxT][33];
+};
+
 struct WinLds {
     DecEntry ent[64];
     int32_t ids[kDecMaxT][32];
     float w[kDecMaxT][32];
-    float cand_v[kDecMaxT][64];
-    int32_t cand_id[kDecMaxT][64];
+    DecComb comb;
+    TopkLds tk[kDecMaxT];
     int32_t n_ent;
 };
 
@@ -55,14 +63,17 @@ template <int V>
 __device__ __forceinline__ int window_entries(const float* __restrict__ logits, const float* __restrict__ gate, int T,
                                               int E, int K, const uint8_t* __restrict__ arena, size_t stride,
                                               const uint8_t* __restrict__ shared_blob, WinLds& L) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (T == 1) {   // one token: the entries are its K experts by ascending id, then the shared expert
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int g = wave >> 2, q = wave & 3;
+    const bool active = g < T;
+    const float gl = (wave == 0 && lane < T) ? gate[lane] : 0.0f;   // shared gate logits, loaded early
+    float mx;
+    topk_group4<V>(logits + size_t(active ? g : 0) * E, E, K, q, active, L.tk[active ? g : 0], mx);
+    if (T == 1) {   // one token: entries are its K experts by ascending id (slot = entry), then the shared expert
         if (wave == 0) {
-            const float g = gate[0];
-            int sel_id;
-            float sel_l, mx, se;
-            topk_select<V>(logits, E, K, L.cand_v[0], L.cand_id[0], sel_id, sel_l, mx, se);
-            const float w = topk_weight(sel_l, mx, wave_sum_tree(se), K);
+            const float sel_l = lane < K ? L.tk[0].sel_v[lane] : 0.0f;
+            const int sel_id = lane < K ? L.tk[0].sel_id[lane] : 0x7fffffff;
+            const float w = topk_weight_sel(sel_l, mx, K);
             int rank = 0;
             for (int j = 0; j < K; ++j) rank += __builtin_amdgcn_readlane(sel_id, j) < sel_id ? 1 : 0;
             if (lane < K) {
@@ -77,36 +88,57 @@ __device__ __forceinline__ int window_entries(const float* __restrict__ logits, 
                 d.slot[1] = d.slot[2] = d.slot[3] = -1;
                 d.w[0] = w;
                 d.w[1] = d.w[2] = d.w[3] = 0.0f;
+                L.comb.slot[0][rank] = rank;
+                L.comb.w[0][rank] = w;
             } else if (lane == K) {
+                const float sw = sigmoidf_(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gl), 0)));
                 DecEntry& d = L.ent[K];
                 d.blob = shared_blob;
                 d.ntok = 1;
                 d.base = K;
                 d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
                 d.slot[0] = d.slot[1] = d.slot[2] = d.slot[3] = -1;
-                d.w[0] = sigmoidf_(g);
+                d.w[0] = sw;
                 d.w[1] = d.w[2] = d.w[3] = 0.0f;
+                L.comb.slot[0][K] = K;
+                L.comb.w[0][K] = sw;
                 L.n_ent = K + 1;
             }
         }
         __syncthreads();
+        FRT_PROBE(3, 6);
         return K + 1;
     }
-    if (wave < T) topk_wave<V>(logits + size_t(wave) * E, E, K, L.ids[wave], L.w[wave], L.cand_v[wave], L.cand_id[wave]);
+    if (active && q == 0) {
+        const float sel_l = lane < K ? L.tk[g].sel_v[lane] : 0.0f;
+        const float w = topk_weight_sel(sel_l, mx, K);
+        if (lane < K) {
+            L.ids[g][lane] = L.tk[g].sel_id[lane];
+            L.w[g][lane] = w;
+        }
+    }
     __syncthreads();
+    FRT_PROBE(3, 6);
     if (wave == 0) {
         const int S = T * K;
         const int e = lane < S ? L.ids[lane / K][lane % K] : 0x7fffffff;
         bool first = lane < S;
+        int pos = 0;   // earlier selections of the same expert (their tokens come first in the entry)
         for (int j = 0; j < S; ++j) {
             const int ej = __builtin_amdgcn_readlane(e, j);
-            if (j < lane && ej == e) first = false;
+            if (j < lane && ej == e) {
+                first = false;
+                ++pos;
+            }
         }
         const uint64_t fm = __ballot(first);
-        int rank = 0;
+        int rank = 0;   // entry of this lane's expert: distinct experts with a smaller id
+        int rk = 0;     // position in its token's list: the token's experts with a smaller id
+        const int tl = lane / K;
         for (int j = 0; j < S; ++j) {
             const int ej = __builtin_amdgcn_readlane(e, j);
             if (((fm >> j) & 1ull) && ej < e) ++rank;
+            if (j / K == tl && ej < e) ++rk;
         }
         const int U = __popcll(fm);
         if (first) {
@@ -123,10 +155,10 @@ __device__ __forceinline__ int window_entries(const float* __restrict__ logits, 
                 }
             }
             d.ntok = nt;
-            for (int q = nt; q < 4; ++q) {
-                d.tok[q] = 0;
-                d.slot[q] = -1;
-                d.w[q] = 0.0f;
+            for (int qq = nt; qq < 4; ++qq) {
+                d.tok[qq] = 0;
+                d.slot[qq] = -1;
+                d.w[qq] = 0.0f;
             }
         }
         if (lane < 4) {   // the shared expert, every token, weight sigmoid(gate)
@@ -137,7 +169,7 @@ __device__ __forceinline__ int window_entries(const float* __restrict__ logits, 
             }
             d.tok[lane] = lane < T ? lane : 0;
             d.slot[lane] = -1;
-            d.w[lane] = lane < T ? sigmoidf_(gate[lane]) : 0.0f;
+            d.w[lane] = lane < T ? sigmoidf_(gl) : 0.0f;
         }
         __builtin_amdgcn_s_waitcnt(0);
         __builtin_amdgcn_wave_barrier();
@@ -146,6 +178,17 @@ __device__ __forceinline__ int window_entries(const float* __restrict__ logits, 
         const int base = wave_excl_scan(nt, &tot);
         if (lane <= U) L.ent[lane].base = base;
         if (lane == 0) L.n_ent = U + 1;
+        // combine lists: slot = base of the expert's entry + pos; the shared expert's slot is its base + t
+        const int eb = __shfl(base, rank, 64);
+        const int sb = __builtin_amdgcn_readlane(base, U);
+        if (lane < S) {
+            L.comb.slot[tl][rk] = eb + pos;
+            L.comb.w[tl][rk] = L.w[tl][lane % K];
+        }
+        if (lane < T) {
+            L.comb.slot[lane][K] = sb + lane;
+            L.comb.w[lane][K] = sigmoidf_(gl);
+        }
     }
     __syncthreads();
     return L.n_ent;
@@ -188,13 +231,14 @@ __global__ void k_hits_group(const uint8_t* const* __restrict__ hit_ptr, const i
     *n_ent = U;
 }
 
-// ---- gate + up for 32 ff rows of one entry. NB = n / 64 blocks per row. 256 threads.
-// RPW rows per wave pass (64 / NB when NB divides 64, else 1 with NB <= 64 lanes live).
-template <int NB>
-__device__ __forceinline__ void gateup_body(const DecEntry& e, const int8_t* __restrict__ xq, const float* __restrict__ xd, int n,
-                            int ff, int8_t* __restrict__ hq, float* __restrict__ hd, float (*hrow)[32]) {
+// ---- gate + up for 32 ff rows of one entry by NW waves (32 / NW rows each). NB = n / 64 blocks
+// per row; RPW rows per wave pass (64 / NB when NB divides 64, else 1 with NB <= 64 lanes live).
+template <int NB, int NW>
+__device__ __forceinline__ void gateup_body(const DecEntry& e, int rb, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                            int n, int ff, int8_t* __restrict__ hq, float* __restrict__ hd, float (*hrow)[32]) {
     constexpr int RPW = (64 % NB == 0) ? 64 / NB : 1;
-    constexpr int PASSES = 8 / RPW;   // 8 rows per wave, 4 waves = 32 rows
+    constexpr int ROWS = 32 / NW;                       // rows per wave
+    constexpr int PASSES = (ROWS + RPW - 1) / RPW;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rsub = lane / NB, b = lane % NB;
     const bool live = rsub < RPW;
@@ -206,20 +250,21 @@ __device__ __forceinline__ void gateup_body(const DecEntry& e, const int8_t* __r
     const uint16_t* uscal = reinterpret_cast<const uint16_t*>(e.blob + mb + size_t(ff) * nb * 16);
     // issue every pass's loads first
     uint4 cg[PASSES], cu[PASSES];
-    uint16_t sg[PASSES], su[PASSES];
+    uint32_t sg[PASSES], su[PASSES];   // fp16 scale bits, one per register (no packing waits)
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-        const int r = blockIdx.x * 32 + wave * 8 + p * RPW + rsub;
-        if (live) {
-            cg[p] = *reinterpret_cast<const uint4*>(gcodes + (size_t(r) * nb + b) * 16);
-            cu[p] = *reinterpret_cast<const uint4*>(ucodes + (size_t(r) * nb + b) * 16);
-            sg[p] = gscal[size_t(r) * nb + b];
-            su[p] = uscal[size_t(r) * nb + b];
+        const int r = rb * 32 + wave * ROWS + p * RPW + rsub;
+        if (live && p * RPW + rsub < ROWS) {
+            cg[p] = gld_u4(gcodes + (size_t(r) * nb + b) * 16);
+            cu[p] = gld_u4(ucodes + (size_t(r) * nb + b) * 16);
+            sg[p] = gld<uint16_t>(gscal + size_t(r) * nb + b);
+            su[p] = gld<uint16_t>(uscal + size_t(r) * nb + b);
         } else {
             cg[p] = cu[p] = make_uint4(0, 0, 0, 0);
             sg[p] = su[p] = 0;
         }
     }
+    FRT_PROBE(1, 2);
     // this lane's activation block for each token: 16 dwords, scales, and the halves' code sums
     int xa[kDecMaxT][16];
     float xd0[kDecMaxT], xd1[kDecMaxT];
@@ -256,7 +301,7 @@ __device__ __forceinline__ void gateup_body(const DecEntry& e, const int8_t* __r
     for (int p = 0; p < PASSES; ++p) {
         const uint32_t wg[4] = {cg[p].x, cg[p].y, cg[p].z, cg[p].w};
         const uint32_t wu[4] = {cu[p].x, cu[p].y, cu[p].z, cu[p].w};
-        const float dg = h2f(sg[p]), du = h2f(su[p]);
+        const float dg = h2f(uint16_t(sg[p])), du = h2f(uint16_t(su[p]));
         float ag[kDecMaxT], au[kDecMaxT];
 #pragma unroll
         for (int j = 0; j < kDecMaxT; ++j) ag[j] = au[j] = 0.0f;
@@ -296,10 +341,11 @@ __device__ __forceinline__ void gateup_body(const DecEntry& e, const int8_t* __r
                 c = wave_sum_tree(c);
                 writer = lane == 0;
             }
-            if (writer) hrow[j][wave * 8 + p * RPW + rsub] = a / (1.0f + expf(-a)) * c;
+            if (writer && p * RPW + rsub < ROWS) hrow[j][wave * ROWS + p * RPW + rsub] = a / (1.0f + expf(-a)) * c;
         }
     }
     __syncthreads();
+    FRT_PROBE(1, 3);
     // Q8_0 of the 32-row block of h for each token: wave w < ntok, lanes 0..31
     if (wave < e.ntok) {   // the whole wave takes part in the DPP max; lanes 0..31 hold the block
         const float v = lane < 32 ? hrow[wave][lane] : 0.0f;
@@ -307,34 +353,41 @@ __device__ __forceinline__ void gateup_body(const DecEntry& e, const int8_t* __r
         const float d = q8_scale(am);
         const float id = q8_inv(d);
         const int c = e.base + wave;
-        if (lane < 32) hq[size_t(c) * ff + blockIdx.x * 32 + lane] = int8_t(q8_code(v, id));
-        if (lane == 0) hd[size_t(c) * (ff / kQ8) + blockIdx.x] = f16_round(d);
+        if (lane < 32) hq[size_t(c) * ff + rb * 32 + lane] = int8_t(q8_code(v, id));
+        if (lane == 0) hd[size_t(c) * (ff / kQ8) + rb] = f16_round(d);
     }
 }
 
 template <int NB>
-__global__ void __launch_bounds__(256) k_dec_gateup(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
+__global__ void __launch_bounds__(1024) k_dec_gateup(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
                                                     const int8_t* __restrict__ xq, const float* __restrict__ xd, int n,
                                                     int ff, int8_t* __restrict__ hq, float* __restrict__ hd) {
     __shared__ float hrow[kDecMaxT][32];
     if (int(blockIdx.y) >= *n_ent) return;
     const DecEntry e = ent[blockIdx.y];
-    gateup_body<NB>(e, xq, xd, n, ff, hq, hd, hrow);
+    gateup_body<NB, 16>(e, blockIdx.x, xq, xd, n, ff, hq, hd, hrow);
 }
 
 template <int NB, int V>
-__global__ void __launch_bounds__(256) k_dec_route_gateup(const float* __restrict__ logits,
+__global__ void __launch_bounds__(1024) k_dec_route_gateup(const float* __restrict__ logits,
                                                           const float* __restrict__ gate, int T, int E, int K,
                                                           const uint8_t* __restrict__ arena, size_t stride,
                                                           const uint8_t* __restrict__ shared_blob,
                                                           const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                           int n, int ff, int8_t* __restrict__ hq,
                                                           float* __restrict__ hd, DecEntry* __restrict__ ent_out,
-                                                          int32_t* __restrict__ n_ent_out, int32_t* __restrict__ ids,
-                                                          float* __restrict__ wts, uint32_t* counts) {
+                                                          int32_t* __restrict__ n_ent_out, DecComb* __restrict__ comb_out,
+                                                          int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                          uint32_t* counts) {
     __shared__ WinLds L;
     __shared__ float hrow[kDecMaxT][32];
+    FRT_PROBE_BEGIN();
+#ifdef FRT_PROBE_TWICE
+    window_entries<V>(logits, gate, T, E, K, arena, stride, shared_blob, L);
+#endif
+    FRT_PROBE(1, 0);
     const int U1 = window_entries<V>(logits, gate, T, E, K, arena, stride, shared_blob, L);
+    FRT_PROBE(1, 1);
     if (blockIdx.x == 0 && blockIdx.y == 0) {
         for (int i = threadIdx.x; i < U1 * int(sizeof(DecEntry) / 4); i += blockDim.x)
             reinterpret_cast<int32_t*>(ent_out)[i] = reinterpret_cast<const int32_t*>(L.ent)[i];
@@ -344,121 +397,222 @@ __global__ void __launch_bounds__(256) k_dec_route_gateup(const float* __restric
             wts[t * K + k] = L.w[t][k];
             if (counts) atomicAdd(counts + L.ids[t][k], 1u);
         }
+        for (int i = threadIdx.x; i < int(sizeof(DecComb) / 4); i += blockDim.x)
+            reinterpret_cast<int32_t*>(comb_out)[i] = reinterpret_cast<const int32_t*>(&L.comb)[i];
         if (threadIdx.x == 0) *n_ent_out = U1;
     }
     if (int(blockIdx.y) >= U1) return;
     const DecEntry e = L.ent[blockIdx.y];
-    gateup_body<NB>(e, xq, xd, n, ff, hq, hd, hrow);
+    gateup_body<NB, 16>(e, blockIdx.x, xq, xd, n, ff, hq, hd, hrow);
+    FRT_PROBE(1, 4);
+    FRT_PROBE_END();
+}
+
+// ---- down GEMV rows, split into loads (issued early, into registers) and the dot products, so
+// that a persistent kernel can prefetch a batch of down rows across a grid barrier.
+// Wave w takes entries u0 + 4 i (i < BATCH) of the list, u0 = w + 4 BATCH b for batch b; each
+// of its lanes holds one 64-block of one of the RD = 8 rows r0 .. r0 + 7.
+template <int NBF, int BATCH>
+struct DownRegs {
+    static constexpr int RPP = 64 / NBF;   // rows per wave pass
+    static constexpr int RD = 8;           // rows per workgroup
+    static constexpr int PASSES = (RD + RPP - 1) / RPP;
+    uint4 cd[BATCH][PASSES];
+    uint32_t sd[BATCH][PASSES];   // fp16 scale bits, one per register
+    uint32_t ok;                  // bit i * PASSES + p: that row load is real (else it counts as 0)
+};
+
+template <int NBF, int BATCH>
+__device__ __forceinline__ void down_load(const DecEntry* ent, int U, int u0, int r0, int n, int ff,
+                                          DownRegs<NBF, BATCH>& R) {
+    using D = DownRegs<NBF, BATCH>;
+    const int lane = threadIdx.x & 63;
+    const int rsub = lane / NBF, b = lane % NBF;
+    const bool live = rsub < D::RPP;
+    const size_t dbase = 2 * mat_bytes(ff, n);
+    // The entries' blob pointers in one vector load (lane i < BATCH: entry u0 + 4 i; lane BATCH:
+    // entry 0, which stands in for entries past U; the entry array holds at least 4 BATCH entries,
+    // so the load need not wait for U), then every row load, unconditional (clamped entry and row;
+    // the ok mask zeroes the invalid ones where they are used), so that they issue back to back.
+    // Needs U >= 1.
+    const int le = lane < BATCH ? u0 + 4 * lane : 0;
+    const uint64_t bp = gld<uint64_t>(&ent[le].blob);
+    const uint64_t b0 = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(bp >> 32)), BATCH))) << 32) |
+                        uint32_t(__builtin_amdgcn_readlane(int(uint32_t(bp)), BATCH));
+    const uint8_t* db[BATCH];
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+        const uint64_t bi = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(bp >> 32)), i))) << 32) |
+                            uint32_t(__builtin_amdgcn_readlane(int(uint32_t(bp)), i));
+        db[i] = reinterpret_cast<const uint8_t*>(u0 + 4 * i < U ? bi : b0) + dbase;
+    }
+    R.ok = 0;
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+#pragma unroll
+        for (int p = 0; p < D::PASSES; ++p) {
+            const int rl = p * D::RPP + rsub;
+            if (u0 + 4 * i < U && live && rl < D::RD) R.ok |= 1u << (i * D::PASSES + p);
+            const int r = r0 + min(rl, D::RD - 1);
+            const int bb = live ? b : 0;
+            R.cd[i][p] = gld_u4(db[i] + (size_t(r) * NBF + bb) * 16);
+            R.sd[i][p] = gld<uint16_t>(db[i] + size_t(n) * NBF * 16 + (size_t(r) * NBF + bb) * 2);
+        }
+    }
+}
+
+// sh_q [S][ff] int8 and sh_d [S][ff/32] are the Q8_0 hidden vectors by compact slot; writes
+// sh_y[c * 8 + rl], the down row r0 + rl of slot c (pairwise tree over the row's NBF blocks)
+template <int NBF, int BATCH>
+__device__ __forceinline__ void down_compute(const DecEntry* ent, int U, int u0, const DownRegs<NBF, BATCH>& R,
+                                             const int8_t* sh_q, const float* sh_d, float* sh_y, int ff) {
+    using D = DownRegs<NBF, BATCH>;
+    const int lane = threadIdx.x & 63;
+    const int rsub = lane / NBF, b = lane % NBF;
+    const bool live = rsub < D::RPP;
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+        const int u = u0 + 4 * i;
+        if (u >= U) break;
+        const DecEntry& e = ent[u];
+#pragma unroll
+        for (int p = 0; p < D::PASSES; ++p) {
+            const int rl = p * D::RPP + rsub;
+            const bool ok = (R.ok >> (i * D::PASSES + p)) & 1u;
+            const uint32_t wd[4] = {ok ? R.cd[i][p].x : 0u, ok ? R.cd[i][p].y : 0u, ok ? R.cd[i][p].z : 0u,
+                                    ok ? R.cd[i][p].w : 0u};
+            const float dw = ok ? h2f(uint16_t(R.sd[i][p])) : 0.0f;
+            for (int j = 0; j < e.ntok; ++j) {
+                const int c = e.base + j;
+                float part = 0.0f;
+                if (live && rl < D::RD) {
+                    const int4* hp = reinterpret_cast<const int4*>(sh_q + size_t(c) * ff + b * kBlock);
+                    int ha[16];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int4 v = hp[q];
+                        ha[4 * q] = v.x;
+                        ha[4 * q + 1] = v.y;
+                        ha[4 * q + 2] = v.z;
+                        ha[4 * q + 3] = v.w;
+                    }
+                    int s0 = 0, s1 = 0, q0 = 0, q1 = 0;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        q0 = dot4(int(wd[w] & 0x03030303u), ha[w], q0);
+                        q0 = dot4(int((wd[w] >> 2) & 0x03030303u), ha[4 + w], q0);
+                        q1 = dot4(int((wd[w] >> 4) & 0x03030303u), ha[8 + w], q1);
+                        q1 = dot4(int((wd[w] >> 6) & 0x03030303u), ha[12 + w], q1);
+                    }
+#pragma unroll
+                    for (int i2 = 0; i2 < 8; ++i2) s0 = dot4(ha[i2], 0x01010101, s0);
+#pragma unroll
+                    for (int i2 = 8; i2 < 16; ++i2) s1 = dot4(ha[i2], 0x01010101, s1);
+                    const float f = float(q0 - s0) * sh_d[size_t(c) * (ff / kQ8) + 2 * b] +
+                                    float(q1 - s1) * sh_d[size_t(c) * (ff / kQ8) + 2 * b + 1];
+                    part = f * dw;
+                }
+                if ((NBF & (NBF - 1)) == 0 && NBF <= 16) {
+                    part = group_sum<(NBF <= 16 ? NBF : 16)>(part);
+                } else {
+                    // segments of NBF lanes: gather the row's partials from its first lane
+                    float acc = 0.0f;
+                    for (int q = 0; q < NBF; ++q) acc += __shfl(part, rsub * NBF + q, 64);
+                    part = acc;
+                }
+                if (live && b == 0 && rl < D::RD) sh_y[c * D::RD + rl] = part;
+            }
+        }
+    }
+}
+
+// copies count >= 1 elements of global src to LDS dst over the workgroup, B * blockDim.x per round:
+// in a round every thread issues its B loads before its first LDS write (clamped indices, no
+// branches; the threads past the end rewrite the last element with its own value)
+template <class T, int B>
+__device__ __forceinline__ void stage_lds(T* dst, const T* __restrict__ src, int count) {
+    const int bd = int(blockDim.x), t = int(threadIdx.x);
+    if (count <= B * bd) {
+        T v[B];
+#pragma unroll
+        for (int k = 0; k < B; ++k) v[k] = src[min(t + k * bd, count - 1)];
+#pragma unroll
+        for (int k = 0; k < B; ++k) dst[min(t + k * bd, count - 1)] = v[k];
+    } else {   // larger windows
+        for (int i = t; i < count; i += bd) dst[i] = src[i];
+    }
+}
+
+// combine of token t, down row rl (of the workgroup's 8) from its combine list: the K routed slots
+// in ascending expert id, each weight * y summed from 0, then + the shared expert's y * sigmoid(gate)
+// (moe_cpu.cpp:63-80 phase B order; moe_ref.cu:90-97). Every LDS read is issued before the sum.
+__device__ __forceinline__ float combine_list(const DecComb& C, int K, int t, int rl, const float* sh_y) {
+    constexpr int RD = 8;
+    float wv[32], yv[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        const int kk = k < K ? k : 0;
+        wv[k] = C.w[t][kk];
+        yv[k] = sh_y[C.slot[t][kk] * RD + rl];
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+        if (k < K) {
+            const float p = wv[k] * yv[k];
+            acc = acc + p;
+        }
+    const float p = sh_y[C.slot[t][K] * RD + rl] * C.w[t][K];
+    return acc + p;
 }
 
 // ---- down for 8 output rows x every entry, then the combine. NBF = ff / 64 (8 lanes per row
 // when ff = 512). 256 threads; wave w takes entries w, w + 4, ...
-template <int NBF>
-__global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent, const int32_t* __restrict__ n_ent,
+template <int NBF, bool MAYBE_EMPTY>
+__global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent_g, const int32_t* __restrict__ n_ent,
+                                                  const DecComb* __restrict__ comb,
                                                   const int8_t* __restrict__ hq, const float* __restrict__ hd, int n,
                                                   int ff, int T, int K, const float* __restrict__ resid,
                                                   float* __restrict__ out, float* __restrict__ yh, int U_max,
                                                   int S_max) {
-    constexpr int RPP = 64 / NBF;   // rows per wave pass
-    constexpr int RD = 8;           // rows per workgroup
-    constexpr int PASSES = (RD + RPP - 1) / RPP;
+    constexpr int RD = 8;   // rows per workgroup
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ DecEntry s_ent[64];
-    // the entry list, its length and the quantized hidden vectors are independent loads: issue them
-    // together (hq/hd for the largest possible slot count S_max), then one barrier
+    __shared__ DecComb s_comb;
+    // every global load is issued before the first wait: the residual this thread adds in the
+    // combine, the entry count, the LDS staging of the entry list and the quantized hidden vectors,
+    // and the first batch of down rows (their blob pointers read straight from the global entry list)
+    FRT_PROBE_BEGIN();
+    FRT_PROBE(2, 0);
+    const int r0 = blockIdx.x * RD;
+    const int ti = threadIdx.x / RD, rli = threadIdx.x % RD;
+    const float res = (resid && ti < T) ? resid[size_t(ti) * n + r0 + rli] : 0.0f;
     const int U = *n_ent;
-    for (int i = threadIdx.x; i < U_max * int(sizeof(DecEntry) / 4); i += blockDim.x)
-        reinterpret_cast<int32_t*>(s_ent)[i] = reinterpret_cast<const int32_t*>(ent)[i];
+    if (MAYBE_EMPTY && U == 0) return;   // moe_hits with no hits: nothing to write
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // the staging loads go first: a wait for them (wait counts run in issue order) then does not
+    // also wait for the down rows issued after them
     int8_t* sh_q = reinterpret_cast<int8_t*>(smem);                        // [S_max][ff]
     float* sh_d = reinterpret_cast<float*>(smem + size_t(S_max) * ff);    // [S_max][ff/32]
     float* sh_y = sh_d + size_t(S_max) * (ff / kQ8);                       // [S_max][RD]
-    for (int i = threadIdx.x; i < S_max * ff / 16; i += blockDim.x)
-        reinterpret_cast<int4*>(sh_q)[i] = reinterpret_cast<const int4*>(hq)[i];
-    for (int i = threadIdx.x; i < S_max * (ff / kQ8); i += blockDim.x) sh_d[i] = hd[i];
+    stage_lds<int4, 1>(reinterpret_cast<int4*>(s_ent), reinterpret_cast<const int4*>(ent_g), U_max * int(sizeof(DecEntry) / 16));
+    if (!yh) stage_lds<int32_t, 2>(reinterpret_cast<int32_t*>(&s_comb), reinterpret_cast<const int32_t*>(comb), int(sizeof(DecComb) / 4));
+    stage_lds<int4, 7>(reinterpret_cast<int4*>(sh_q), reinterpret_cast<const int4*>(hq), S_max * ff / 16);
+    stage_lds<float, 1>(sh_d, hd, S_max * (ff / kQ8));
+    DownRegs<NBF, 4> R;
+    down_load<NBF, 4>(ent_g, U, wave, r0, n, ff, R);   // global entry list (down_load reads it as global)
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-    if (U == 0) return;
-    ent = s_ent;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rsub = lane / NBF, b = lane % NBF;
-    const bool live = rsub < RPP;
-    const int r0 = blockIdx.x * RD;
-    const int nbf = NBF;
-    const size_t dbase = 2 * mat_bytes(ff, n);
-    for (int u0 = wave; u0 < U; u0 += 16) {
-        // up to 4 entries per batch, all loads issued before use
-        uint4 cd[4][PASSES];
-        uint16_t sd[4][PASSES];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int u = u0 + 4 * i;
-#pragma unroll
-            for (int p = 0; p < PASSES; ++p) {
-                const int rl = p * RPP + rsub;
-                if (u < U && live && rl < RD) {
-                    const uint8_t* db = ent[u].blob + dbase;
-                    const int r = r0 + rl;
-                    cd[i][p] = *reinterpret_cast<const uint4*>(db + (size_t(r) * nbf + b) * 16);
-                    sd[i][p] = reinterpret_cast<const uint16_t*>(db + size_t(n) * nbf * 16)[size_t(r) * nbf + b];
-                } else {
-                    cd[i][p] = make_uint4(0, 0, 0, 0);
-                    sd[i][p] = 0;
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int u = u0 + 4 * i;
-            if (u >= U) break;
-            const DecEntry& e = ent[u];
-#pragma unroll
-            for (int p = 0; p < PASSES; ++p) {
-                const int rl = p * RPP + rsub;
-                const uint32_t wd[4] = {cd[i][p].x, cd[i][p].y, cd[i][p].z, cd[i][p].w};
-                const float dw = h2f(sd[i][p]);
-                for (int j = 0; j < e.ntok; ++j) {
-                    const int c = e.base + j;
-                    float part = 0.0f;
-                    if (live && rl < RD) {
-                        const int4* hp = reinterpret_cast<const int4*>(sh_q + size_t(c) * ff + b * kBlock);
-                        int ha[16];
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const int4 v = hp[q];
-                            ha[4 * q] = v.x;
-                            ha[4 * q + 1] = v.y;
-                            ha[4 * q + 2] = v.z;
-                            ha[4 * q + 3] = v.w;
-                        }
-                        int s0 = 0, s1 = 0, q0 = 0, q1 = 0;
-#pragma unroll
-                        for (int w = 0; w < 4; ++w) {
-                            q0 = dot4(int(wd[w] & 0x03030303u), ha[w], q0);
-                            q0 = dot4(int((wd[w] >> 2) & 0x03030303u), ha[4 + w], q0);
-                            q1 = dot4(int((wd[w] >> 4) & 0x03030303u), ha[8 + w], q1);
-                            q1 = dot4(int((wd[w] >> 6) & 0x03030303u), ha[12 + w], q1);
-                        }
-#pragma unroll
-                        for (int i2 = 0; i2 < 8; ++i2) s0 = dot4(ha[i2], 0x01010101, s0);
-#pragma unroll
-                        for (int i2 = 8; i2 < 16; ++i2) s1 = dot4(ha[i2], 0x01010101, s1);
-                        const float f = float(q0 - s0) * sh_d[size_t(c) * (ff / kQ8) + 2 * b] +
-                                        float(q1 - s1) * sh_d[size_t(c) * (ff / kQ8) + 2 * b + 1];
-                        part = f * dw;
-                    }
-                    if ((NBF & (NBF - 1)) == 0 && NBF <= 16) {
-                        part = group_sum<(NBF <= 16 ? NBF : 16)>(part);
-                    } else {
-                        // segments of NBF lanes: gather the row's partials from its first lane
-                        float acc = 0.0f;
-                        for (int q = 0; q < NBF; ++q) acc += __shfl(part, rsub * NBF + q, 64);
-                        part = acc;
-                    }
-                    if (live && b == 0 && rl < RD) sh_y[c * RD + rl] = part;
-                }
-            }
-        }
+    FRT_PROBE(2, 1);
+    const DecEntry* ent = s_ent;
+    down_compute<NBF, 4>(ent, U, wave, R, sh_q, sh_d, sh_y, ff);
+    for (int u0 = wave + 16; u0 < U; u0 += 16) {
+        DownRegs<NBF, 4> R2;
+        down_load<NBF, 4>(ent_g, U, u0, r0, n, ff, R2);
+        down_compute<NBF, 4>(ent, U, u0, R2, sh_q, sh_d, sh_y, ff);
     }
     __syncthreads();
+    FRT_PROBE(2, 2);
     if (yh) {   // moe_hits: per-slot outputs
         const int S = ent[U - 1].base + ent[U - 1].ntok;
         for (int i = threadIdx.x; i < S * RD; i += blockDim.x) {
@@ -470,39 +624,34 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent, const int
         }
         return;
     }
-    // combine: token t, row rl; routed entries in order (ascending expert), then the shared expert
-    for (int i = threadIdx.x; i < T * RD; i += blockDim.x) {
-        const int t = i / RD, rl = i % RD;
-        float acc = 0.0f;
-        for (int u = 0; u < U - 1; ++u) {
-            const DecEntry& e = ent[u];
-            for (int j = 0; j < e.ntok; ++j)
-                if (e.tok[j] == t) {
-                    const float p = e.w[j] * sh_y[(e.base + j) * RD + rl];
-                    acc = acc + p;
-                }
-        }
-        const DecEntry& sh = ent[U - 1];
-        const float p = sh_y[(sh.base + t) * RD + rl] * sh.w[t];
-        float o = acc + p;
-        if (resid) o = resid[size_t(t) * n + r0 + rl] + o;
-        out[size_t(t) * n + r0 + rl] = o;
+    if (ti < T) {
+        float o = combine_list(s_comb, K, ti, rli, sh_y);
+        if (resid) o = res + o;
+        out[size_t(ti) * n + r0 + rli] = o;
     }
+    FRT_PROBE(2, 3);
+    FRT_PROBE_END();
 }
+
 
 }  // namespace
 
 // ---------------------------------------------------------------- host side
 
-// scratch: entries, counts, hq, hd for T tokens with K routes (+ the shared expert)
+// scratch: entries, counts, hq, hd for T tokens with K routes (+ the shared expert). The entry array
+// has 16 spare slots: the down kernel reads the blob pointers of 4 entries per wave per batch
+// before it knows how many entries there are (it uses only those below the count).
+static size_t dec_ent_bytes(int T, int K) { return up256(size_t(T * K + 1 + 16) * sizeof(DecEntry)); }
 size_t dec_scratch_bytes(int T, int K, int ff) {
     const int S = T * (K + 1);
-    return up256(size_t(T * K + 1) * sizeof(DecEntry)) + 256 + up256(size_t(S) * ff) + up256(size_t(S) * (ff / kQ8) * 4);
+    return dec_ent_bytes(T, K) + 256 + up256(sizeof(DecComb)) + up256(size_t(S) * ff) +
+           up256(size_t(S) * (ff / kQ8) * 4);
 }
 
 struct DecScratch {
     DecEntry* ent;
     int32_t* n_ent;
+    DecComb* comb;
     int8_t* hq;
     float* hd;
 };
@@ -510,9 +659,11 @@ static DecScratch dec_carve(void* base, int T, int K, int ff) {
     uint8_t* p = static_cast<uint8_t*>(base);
     DecScratch s;
     s.ent = reinterpret_cast<DecEntry*>(p);
-    p += up256(size_t(T * K + 1) * sizeof(DecEntry));
+    p += dec_ent_bytes(T, K);
     s.n_ent = reinterpret_cast<int32_t*>(p);
     p += 256;
+    s.comb = reinterpret_cast<DecComb*>(p);
+    p += up256(sizeof(DecComb));
     s.hq = reinterpret_cast<int8_t*>(p);
     p += up256(size_t(T * (K + 1)) * ff);
     s.hd = reinterpret_cast<float*>(p);
@@ -527,8 +678,12 @@ static int dec_down(const DecScratch& s, int n, int ff, int T, int K, const floa
     const size_t smem = size_t(S) * ff + size_t(S) * (ff / kQ8) * 4 + size_t(S) * 8 * 4;
 #define FRT_DN(NBFV)                                                                                           \
     case NBFV:                                                                                                 \
-        k_dec_down<NBFV><<<n / 8, 256, smem, stream>>>(s.ent, s.n_ent, s.hq, s.hd, n, ff, T, K, resid, out, yh,  \
-                                                       U_max, S);                                               \
+        if (yh)                                                                                                \
+            k_dec_down<NBFV, true><<<n / 8, 256, smem, stream>>>(s.ent, s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid,  \
+                                                                 out, yh, U_max, S);                            \
+        else                                                                                                   \
+            k_dec_down<NBFV, false><<<n / 8, 256, smem, stream>>>(s.ent, s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid, \
+                                                                  out, yh, U_max, S);                           \
         break;
     switch (nbf) {
         FRT_DN(4) FRT_DN(8) FRT_DN(10) FRT_DN(16)
@@ -557,8 +712,8 @@ int dec_moe(const float* logits, const float* gate, int T, int E, int K, const u
     const int nb = n / kBlock;
     dim3 g1(ff / 32, T * K + 1);
 #define FRT_RG(NBV, VV)                                                                                         \
-    k_dec_route_gateup<NBV, VV><<<g1, 256, 0, stream>>>(logits, gate, T, E, K, arena, stride, shared_blob, xq, xd, \
-                                                        n, ff, s.hq, s.hd, s.ent, s.n_ent, ids, wts, counts)
+    k_dec_route_gateup<NBV, VV><<<g1, 1024, 0, stream>>>(logits, gate, T, E, K, arena, stride, shared_blob, xq, xd, \
+                                                        n, ff, s.hq, s.hd, s.ent, s.n_ent, s.comb, ids, wts, counts)
 #define FRT_RGN(NBV)                       \
     case NBV:                              \
         if (E <= 512) FRT_RG(NBV, 8);      \
@@ -584,7 +739,7 @@ int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const i
     const int nb = n / kBlock;
     dim3 g1(ff / 32, T * K);
 #define FRT_GU(NBV) \
-    case NBV: k_dec_gateup<NBV><<<g1, 256, 0, stream>>>(s.ent, s.n_ent, xq, xd, n, ff, s.hq, s.hd); break;
+    case NBV: k_dec_gateup<NBV><<<g1, 1024, 0, stream>>>(s.ent, s.n_ent, xq, xd, n, ff, s.hq, s.hd); break;
     switch (nb) {
         FRT_GU(16) FRT_GU(32) FRT_GU(40) FRT_GU(48) FRT_GU(64)
         default: return set_error(kErrShape, "decode: n=%d unsupported (n/64 in {16,32,40,48,64})", n);
@@ -595,3 +750,12 @@ int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const i
 }
 
 }  // namespace frt
+
+#ifdef FRT_PHASE_PROBE
+namespace frt {
+__device__ unsigned long long frt_probe[4][2048][8];
+}
+extern "C" int frt_probe_dump(unsigned long long* host) {
+    return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(frt::frt_probe), sizeof(frt::frt_probe)));
+}
+#endif

@@ -24,7 +24,8 @@ __device__ __forceinline__ void quant32(float v, int j, int8_t* q, float* d) {
     if (j == 0) *d = f16_round(dd);
 }
 
-// ---- router: grid (ceil(rows / 4), ceil(T / tok_per_wg)); 4 waves, one router row each.
+// ---- router: grid (ceil(rows / W), ceil(T / tok_per_wg)), W = blockDim.x / 64 waves, one router row
+// each (W = 2 for decode windows, so that the 4 MiB of router rows spread over twice as many CUs).
 // Rows 0..E-1 are the router (bias optional); row E (when gate_w) is the shared expert's gate.
 // x tiles of TT tokens are staged in LDS with each 64-chain padded by one float (conflict-free).
 // norm: the layer input is u = x * r, r the canonical RMS scale of the token (topk.hpp); u_i is
@@ -39,9 +40,11 @@ __global__ void __launch_bounds__(256) k_router(const float* __restrict__ x, int
                                                 float* __restrict__ xd) {
     extern __shared__ float xs[];   // [TT][64][L + 1]
     __shared__ float s_r[64];
+    FRT_PROBE_BEGIN();
+    FRT_PROBE(0, 0);
     const int n = 64 * L;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + wave;
+    const int row = blockIdx.x * (blockDim.x >> 6) + wave;
     const bool is_gate = row == E;
     const bool live = row < E || (is_gate && gate_w);
     const float* w = is_gate ? gate_w : W + size_t(row < E ? row : 0) * n;
@@ -72,8 +75,9 @@ __global__ void __launch_bounds__(256) k_router(const float* __restrict__ x, int
             dst[3] = v.w;
         }
         __syncthreads();
+        FRT_PROBE(0, 1);
         if (norm) {
-            for (int t = wave; t < tn; t += 4) {
+            for (int t = wave; t < tn; t += int(blockDim.x >> 6)) {
                 const float r = rms_scale_wave<L>(xs + (t * 64 + lane) * (L + 1), n);
                 if (lane == 0) s_r[t] = r;
             }
@@ -82,13 +86,15 @@ __global__ void __launch_bounds__(256) k_router(const float* __restrict__ x, int
         if (xq && blockIdx.y == 0) {   // Q8_0 of the layer input: item = (token, 32-block)
             const int hw = threadIdx.x >> 5, j = threadIdx.x & 31;
             const int nblk = tn * (n / kQ8);
-            for (int it = blockIdx.x * 8 + hw; it < nblk; it += gridDim.x * 8) {
+            const int nhw = int(blockDim.x >> 5);
+            for (int it = blockIdx.x * nhw + hw; it < nblk; it += gridDim.x * nhw) {
                 const int t = it / (n / kQ8), k = (it % (n / kQ8)) * kQ8 + j;
                 float v = xs[(t * 64 + k / L) * (L + 1) + k % L];
                 if (norm) v = v * s_r[t];
                 quant32(v, j, xq + size_t(t0 + t) * n + (k - j), xd + size_t(t0 + t) * (n / kQ8) + k / kQ8);
             }
         }
+        FRT_PROBE(0, 2);
         if (!live) continue;
         for (int t = 0; t < tn; ++t) {
             const float* xc = xs + (t * 64 + lane) * (L + 1);
@@ -111,6 +117,8 @@ __global__ void __launch_bounds__(256) k_router(const float* __restrict__ x, int
             }
         }
     }
+    FRT_PROBE(0, 3);
+    FRT_PROBE_END();
 }
 
 // ---- u = x * r per token (canonical RMS scale), one wave per token (prefill inputs)
@@ -201,13 +209,14 @@ int router_logits(const float* x, int T, const float* W, const float* bias, cons
     // with the 4 router rows kept in registers across its tiles
     const int tok_per_wg = T <= TT ? T : 64;
     if (xq && T > TT) return set_error(kErrShape, "router: fused quantization needs T <= %d", TT);
-    dim3 grid((rows + 3) / 4, (T + tok_per_wg - 1) / tok_per_wg);
+    const int wg_rows = T <= TT ? 2 : 4;   // decode: 2 rows per workgroup; token tiles: 4
+    dim3 grid((rows + wg_rows - 1) / wg_rows, (T + tok_per_wg - 1) / tok_per_wg);
 #define FRT_ROUTER_L(LL)                                                                                         \
     case LL:                                                                                                     \
         if (smem > 65536)                                                                                        \
             FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_router<LL>),                            \
                                         hipFuncAttributeMaxDynamicSharedMemorySize, int(smem)));                 \
-        k_router<LL><<<grid, 256, smem, stream>>>(x, T, W, bias, gate_w, E, logits, gate, TT, tok_per_wg, norm, xq, xd); \
+        k_router<LL><<<grid, 64 * wg_rows, smem, stream>>>(x, T, W, bias, gate_w, E, logits, gate, TT, tok_per_wg, norm, xq, xd); \
         break;
     switch (L) {
         FRT_ROUTER_L(8) FRT_ROUTER_L(16) FRT_ROUTER_L(24) FRT_ROUTER_L(32) FRT_ROUTER_L(40) FRT_ROUTER_L(48)

@@ -225,6 +225,19 @@ __device__ __forceinline__ float topk_weight(float sel_l, float mx, float S, int
     return p / ws;
 }
 
+// The K weights when E <= 16384 (lane k holds the k-th selection): the selected p are at least
+// p_1 = 1 / sum_e exp(l_e - mx) >= 1 / E > 2^-14, so the clamp of moe_ref.cu:146-164 never applies
+// and the common factor 1 / sum cancels: w_k = e_k / sum_j e_j with e = exp(l - mx), the sum over
+// the selection in rank order. (Against p / sum p with p rounded to float first, this differs by a
+// few float roundings, far inside the 1e-6 relative bound.)
+__device__ __forceinline__ float topk_weight_sel(float sel_l, float mx, int K) {
+    const int lane = threadIdx.x & 63;
+    const float e = lane < K ? expf(sel_l - mx) : 0.0f;
+    float ws = 0.0f;
+    for (int k = 0; k < K; ++k) ws += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), k));
+    return e / ws;
+}
+
 // One token by one wave: ids/wts [K] written by lanes 0..K-1; returns lane k's id.
 template <int V>
 __device__ __forceinline__ int topk_wave(const float* __restrict__ l, int E, int K, int32_t* ids, float* wts,
@@ -239,6 +252,167 @@ __device__ __forceinline__ int topk_wave(const float* __restrict__ l, int E, int
         wts[threadIdx.x & 63] = w;
     }
     return sel_id;
+}
+
+// ---- Top-K of one token by a group of 4 waves (q = 0..3 the wave's index in the group), for
+// latency: the same selection and order as topk_select, with the two ranking passes split over the
+// group. Lane l of every wave loads experts V l .. V l + V - 1 (the same data in all 4 waves).
+//   1. rank of each lane maximum among the 64 (wave q compares against lanes 16 q .. 16 q + 15;
+//      the 4 partial counts meet in LDS); the lane maximum of rank K - 1 is the threshold tv.
+//   2. the logits that rank at or above tv are the candidates (at least K, typically a few more);
+//      wave 0 compacts them into LDS; each candidate's rank among them is again split over the
+//      group; ranks < K are the selection, written in rank order to sel_v / sel_id.
+//   (More than 64 candidates, only with coarse heavily tied logits: wave 0 selects by K rounds of
+//   wave maxima, as topk_select does.)
+// Every wave of the workgroup must call this the same number of times (it holds __syncthreads);
+// a group with no token passes active = false. mx (the largest logit) comes back in every wave of
+// the group.
+struct TopkLds {
+    int32_t part[4][64];
+    alignas(16) float cand_v[64];
+    alignas(16) int32_t cand_id[64];
+    float sel_v[32];
+    int32_t sel_id[32];
+};
+
+template <int V>
+__device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, int K, int q, bool active,
+                                            TopkLds& S, float& mx) {
+    const int lane = threadIdx.x & 63;
+    FRT_PROBE(3, 0);
+    if (!active) {   // a group without a token only keeps the workgroup's barrier count (its SIMDs
+                     // are shared with the working groups)
+        mx = 0.0f;
+        __syncthreads();
+        __syncthreads();
+        __syncthreads();
+        __syncthreads();
+        return;
+    }
+    float v[V];
+    if (active && E == 64 * V) {
+        const float4* l4 = reinterpret_cast<const float4*>(l + V * lane);
+#pragma unroll
+        for (int i = 0; i < V / 4; ++i) {
+            const float4 f = l4[i];
+            v[4 * i] = f.x;
+            v[4 * i + 1] = f.y;
+            v[4 * i + 2] = f.z;
+            v[4 * i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = (active && V * lane + i < E) ? l[V * lane + i] : -INFINITY;
+    }
+#ifdef FRT_PHASE_PROBE
+    __builtin_amdgcn_s_waitcnt(0);
+#endif
+    FRT_PROBE(3, 1);
+    float lm = v[0];
+    int li = V * lane;
+#pragma unroll
+    for (int i = 1; i < V; ++i)
+        if (v[i] > lm) {
+            lm = v[i];
+            li = V * lane + i;
+        }
+    // 1. partial rank of the lane maximum (equal maxima: the lower lane holds the lower id)
+    int cnt = 0;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+        const int j = 16 * q + jj;
+        const float mj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lm), j));
+        cnt += (mj > lm || (mj == lm && j < lane)) ? 1 : 0;
+    }
+    if (active) S.part[q][lane] = cnt;
+    __syncthreads();
+    FRT_PROBE(3, 2);
+    const int rank = S.part[0][lane] + S.part[1][lane] + S.part[2][lane] + S.part[3][lane];
+    const int kl = __ffsll((long long)__ballot(rank == K - 1)) - 1;
+    const int l0 = __ffsll((long long)__ballot(rank == 0)) - 1;
+    const float tv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lm), kl));
+    const int tid = __builtin_amdgcn_readlane(li, kl);
+    mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lm), l0));
+    // 2. candidates
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) c += (v[i] > tv || (v[i] == tv && V * lane + i <= tid)) ? 1 : 0;
+    int C;
+    int pos = wave_excl_scan(c, &C);
+    if (active && q == 0 && C <= 64) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const int e = V * lane + i;
+            if (v[i] > tv || (v[i] == tv && e <= tid)) {
+                S.cand_v[pos] = v[i];
+                S.cand_id[pos] = e;
+                ++pos;
+            }
+        }
+    }
+    __syncthreads();
+    FRT_PROBE(3, 3);
+    if (C <= 64) {
+        const float cv = lane < C ? S.cand_v[lane] : -INFINITY;
+        const int ci = lane < C ? S.cand_id[lane] : 0x7fffffff;
+        // this wave's 16 candidates as four 16-byte LDS reads of each array (same address in every
+        // lane), all issued before the compares; slots >= C are masked
+        float ov[16];
+        int oi[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 a = reinterpret_cast<const float4*>(S.cand_v + 16 * q)[k];
+            const int4 c4 = reinterpret_cast<const int4*>(S.cand_id + 16 * q)[k];
+            ov[4 * k] = a.x;
+            ov[4 * k + 1] = a.y;
+            ov[4 * k + 2] = a.z;
+            ov[4 * k + 3] = a.w;
+            oi[4 * k] = c4.x;
+            oi[4 * k + 1] = c4.y;
+            oi[4 * k + 2] = c4.z;
+            oi[4 * k + 3] = c4.w;
+        }
+        int cnt2 = 0;
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj)
+            cnt2 += (16 * q + jj < C && (ov[jj] > cv || (ov[jj] == cv && oi[jj] < ci))) ? 1 : 0;
+        if (active) S.part[q][lane] = cnt2;
+        __syncthreads();
+        FRT_PROBE(3, 4);
+        const int r2 = S.part[0][lane] + S.part[1][lane] + S.part[2][lane] + S.part[3][lane];
+        if (active && q == 0 && lane < C && r2 < K) {
+            S.sel_v[r2] = cv;
+            S.sel_id[r2] = ci;
+        }
+    } else {
+        __syncthreads();
+        if (active && q == 0) {   // heavily tied logits: K rounds over the lanes' sorted lists
+            int id[V];
+#pragma unroll
+            for (int i = 0; i < V; ++i) id[i] = V * lane + i;
+            sort_desc<V>(v, id);
+            for (int k = 0; k < K; ++k) {
+                const float m = wave_max(v[0]);
+                const uint64_t b = __ballot(v[0] == m);
+                const int win = __ffsll((long long)b) - 1;
+                const int sel = __builtin_amdgcn_readlane(id[0], win);
+                if (lane == win) {
+#pragma unroll
+                    for (int i = 0; i + 1 < V; ++i) {
+                        v[i] = v[i + 1];
+                        id[i] = id[i + 1];
+                    }
+                    v[V - 1] = -INFINITY;
+                }
+                if (lane == 0) {
+                    S.sel_v[k] = m;
+                    S.sel_id[k] = sel;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    FRT_PROBE(3, 5);
 }
 
 // Canonical RMS scale of one token by one wave: chains j = 64 lanes over contiguous L = n / 64
