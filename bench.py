@@ -79,6 +79,9 @@ def build_stack(F, torch, layers):
         bias[l] = torch.from_numpy(g.zipf_bias(2, l, E, ZIPF_STACK))
     mls = [F.MoeLayer(arena.blob(l, 0), arena.stride, E, shared[l].data_ptr(), router[l], gate[l], N, FF, K,
                       router_bias=bias[l], norm_input=True) for l in range(layers)]
+    if not os.environ.get("FRT_NO_ROUTER_WARM"):
+        for l in range(layers):   # the call after layer l reads layer l + 1's router (layer 0's after the last)
+            mls[l].set_next_router(router[(l + 1) % layers])
     torch.cuda.synchronize()
     return arena, shared, router, gate, bias, mls
 

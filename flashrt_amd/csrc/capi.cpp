@@ -60,7 +60,8 @@ int route_topk(hipStream_t stream, const float* logits, int T, int E, int K, int
 size_t dec_scratch_bytes(int T, int K, int ff);
 int dec_moe(const float* logits, const float* gate, int T, int E, int K, const uint8_t* arena, size_t stride,
             const uint8_t* shared_blob, const int8_t* xq, const float* xd, int n, int ff, int32_t* ids, float* wts,
-            uint32_t* counts, const float* resid, float* out, void* scratch, hipStream_t stream);
+            uint32_t* counts, const float* resid, float* out, void* scratch, hipStream_t stream,
+            const float* prefetch = nullptr);
 int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const int8_t* xq, const float* xd, int n,
              int ff, void* scratch, float* yh, hipStream_t stream, int T);
 int dec_check(int T, int K, int n, int ff);
@@ -283,7 +284,7 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
             return rc;
         timing_mark(s, "router_quant");
         return dec_moe(w.logits, w.gate, T, E, K, L->experts, L->stride, L->shared, w.xq, w.xd, n, ff, ids_o, wts_o,
-                       counts, resid, out, w.rest, s);
+                       counts, resid, out, w.rest, s, L->next_router_w);
     }
     if (int rc = pf_check(T, K, n, ff, E)) return rc;
     const float* xin = x;

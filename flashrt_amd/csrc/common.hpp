@@ -68,9 +68,14 @@ __device__ __forceinline__ unsigned long long* frt_probe_lds() {
     do {                                                                   \
         if (threadIdx.x < 32) frt_probe_lds()[threadIdx.x] = 0;            \
     } while (0)
-#define FRT_PROBE(k, i)                                                    \
-    do {                                                                   \
-        if (threadIdx.x == 0) frt_probe_lds()[(k) * 8 + (i)] = wall_clock64(); \
+#ifdef FRT_PROBE_CYCLES   // shader cycles instead (one workgroup's own timeline)
+#define FRT_PROBE_CLOCK() __builtin_amdgcn_s_memtime()
+#else
+#define FRT_PROBE_CLOCK() wall_clock64()
+#endif
+#define FRT_PROBE(k, i)                                                         \
+    do {                                                                        \
+        if (threadIdx.x == 0) frt_probe_lds()[(k) * 8 + (i)] = FRT_PROBE_CLOCK(); \
     } while (0)
 #define FRT_PROBE_END()                                                                            \
     do {                                                                                           \

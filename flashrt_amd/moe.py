@@ -170,6 +170,12 @@ class MoeLayer:
         self.d_model, self.top_k, self.n_expert = d_model, top_k, n_expert
         self._ws = None
 
+    def set_next_router(self, router_w) -> None:
+        """The router matrix the next layer call reads; decode calls warm it into the caches
+        during their last kernel (frt_moe_layer.next_router_w)."""
+        self._next = router_w
+        self.raw.next_router_w = _p(router_w)
+
     def workspace_bytes(self, T: int) -> int:
         return int(lib().frt_moe_layer_workspace_bytes(C.byref(self.raw), T))
 

@@ -124,6 +124,11 @@ typedef struct frt_moe_layer {
     const float* gate_w;      /* [n] fp32 (ffn_gate_inp_shexp) */
     int d_model, d_ff, top_k;
     int flags;                /* FRT_LAYER_* */
+    /* Optional (NULL: none): the router matrix [E][n] the NEXT layer call will read. A decode call
+     * loads it into the GPU's caches during its last kernel, each 2-row slice on the XCD whose L2
+     * the next router kernel reads it from, so that the next router kernel does not wait on HBM.
+     * No reference counterpart (the reference's router is a ggml linear, blocks.hpp:85). */
+    const float* next_router_w;
 } frt_moe_layer;
 size_t frt_moe_layer_workspace_bytes(const frt_moe_layer* L, int T);
 int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out, int32_t* ids,
