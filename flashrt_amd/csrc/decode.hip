@@ -66,7 +66,9 @@ __device__ __forceinline__ int window_entries(const float* __restrict__ logits, 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g = wave >> 2, q = wave & 3;
     const bool active = g < T;
-    const float gl = (wave == 0 && lane < T) ? gate[lane] : 0.0f;   // shared gate logits, loaded early
+    // shared gate logits, loaded here (a volatile load stays where it is issued: the compiler would
+    // otherwise sink it to its use, after the top-k, and wait out a whole round trip there)
+    const float gl = (wave == 0 && lane < T) ? *reinterpret_cast<const volatile float*>(gate + lane) : 0.0f;
     float mx;
     topk_group4<V>(logits + size_t(active ? g : 0) * E, E, K, q, active, L.tk[active ? g : 0], mx);
     if (T == 1) {   // one token: entries are its K experts by ascending id (slot = entry), then the shared expert
@@ -75,7 +77,7 @@ __device__ __forceinline__ int window_entries(const float* __restrict__ logits, 
             const int sel_id = lane < K ? L.tk[0].sel_id[lane] : 0x7fffffff;
             const float w = topk_weight_sel(sel_l, mx, K);
             int rank = 0;
-            for (int j = 0; j < K; ++j) rank += __builtin_amdgcn_readlane(sel_id, j) < sel_id ? 1 : 0;
+            for (int j = 0; j < K; ++j) rank += int(__builtin_amdgcn_readlane(sel_id, j) < sel_id);
             if (lane < K) {
                 L.ids[0][lane] = sel_id;
                 L.w[0][lane] = w;

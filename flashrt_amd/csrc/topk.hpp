@@ -269,10 +269,11 @@ __device__ __forceinline__ int topk_wave(const float* __restrict__ l, int E, int
 // the group.
 struct TopkLds {
     int32_t part[4][64];
-    alignas(16) float cand_v[64];
-    alignas(16) int32_t cand_id[64];
-    float sel_v[32];
-    int32_t sel_id[32];
+    alignas(16) float cand_v[128];     // 64 candidates + one junk slot per lane
+    alignas(16) int32_t cand_id[128];
+    alignas(16) float sel_v[32];
+    alignas(16) int32_t sel_id[32];
+    alignas(16) float e[32];   // scratch of the weight step
 };
 
 template <int V>
@@ -322,7 +323,7 @@ __device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, 
     for (int jj = 0; jj < 16; ++jj) {
         const int j = 16 * q + jj;
         const float mj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lm), j));
-        cnt += (mj > lm || (mj == lm && j < lane)) ? 1 : 0;
+        cnt += int((mj > lm) | ((mj == lm) & (j < lane)));
     }
     if (active) S.part[q][lane] = cnt;
     __syncthreads();
@@ -336,18 +337,18 @@ __device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, 
     // 2. candidates
     int c = 0;
 #pragma unroll
-    for (int i = 0; i < V; ++i) c += (v[i] > tv || (v[i] == tv && V * lane + i <= tid)) ? 1 : 0;
+    for (int i = 0; i < V; ++i) c += int((v[i] > tv) | ((v[i] == tv) & (V * lane + i <= tid)));
     int C;
     int pos = wave_excl_scan(c, &C);
-    if (active && q == 0 && C <= 64) {
+    if (active && q == 0 && C <= 64) {   // branch-free compaction: a non-candidate goes to junk slot 64 + lane
 #pragma unroll
         for (int i = 0; i < V; ++i) {
             const int e = V * lane + i;
-            if (v[i] > tv || (v[i] == tv && e <= tid)) {
-                S.cand_v[pos] = v[i];
-                S.cand_id[pos] = e;
-                ++pos;
-            }
+            const bool is_c = (v[i] > tv) | ((v[i] == tv) & (e <= tid));
+            const int slot = is_c ? pos : 64 + lane;
+            S.cand_v[slot] = v[i];
+            S.cand_id[slot] = e;
+            pos += int(is_c);
         }
     }
     __syncthreads();
@@ -375,7 +376,7 @@ __device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, 
         int cnt2 = 0;
 #pragma unroll
         for (int jj = 0; jj < 16; ++jj)
-            cnt2 += (16 * q + jj < C && (ov[jj] > cv || (ov[jj] == cv && oi[jj] < ci))) ? 1 : 0;
+            cnt2 += int((16 * q + jj < C) & ((ov[jj] > cv) | ((ov[jj] == cv) & (oi[jj] < ci))));
         if (active) S.part[q][lane] = cnt2;
         __syncthreads();
         FRT_PROBE(3, 4);
