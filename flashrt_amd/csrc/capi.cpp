@@ -50,8 +50,9 @@ void timing_mark(hipStream_t stream, const char* kernel) {
 int router_logits(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
                   float* logits, float* gate, hipStream_t stream, int norm, int8_t* xq, float* xd);
 int rmsnorm(const float* x, int T, int n, float* u, hipStream_t stream);
-int router_gemm(const float* x, int T, const float* W, const float* bias, int E, int n, float* logits,
-                hipStream_t stream);
+int router_gemm(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
+                float* logits, float* gate, float* part, hipStream_t stream);
+size_t router_gemm_ws_bytes(int T, int E, bool gate);
 int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xhi, _Float16* xlo,
                 hipStream_t stream);
 int route_topk(hipStream_t stream, const float* logits, int T, int E, int K, int32_t* ids, float* wts, uint32_t* counts,
@@ -95,7 +96,8 @@ static size_t hits_bytes(int K, int ff, int T, int n) {
 struct LayerWs {
     float* logits;
     float* gate;
-    float* u;   // normalised input (prefill with FRT_LAYER_NORM_INPUT)
+    float* u;      // normalised input (prefill with FRT_LAYER_NORM_INPUT)
+    float* part;   // router GEMM split partial sums (prefill)
     int32_t* ids;
     float* wts;
     int8_t* xq;
@@ -125,6 +127,7 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
         w.rest_bytes = dec_scratch_bytes(T, K, ff);
     } else {
         if (L.flags & FRT_LAYER_NORM_INPUT) w.u = reinterpret_cast<float*>(take(size_t(T) * n * 4));
+        w.part = reinterpret_cast<float*>(take(router_gemm_ws_bytes(T, E, true)));
         w.rest_bytes = pf_workspace_bytes(T, K, n, ff, E, true, true);
     }
     w.rest = take(w.rest_bytes);
@@ -293,12 +296,10 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
         xin = w.u;
         timing_mark(s, "rmsnorm");
     }
-    // router logits as a register-tiled GEMM; the shared expert's gate logit as a one-row GEMV
-    if (int rc = router_gemm(xin, T, L->router_w, L->router_bias, E, n, w.logits, s)) return rc;
-    timing_mark(s, "router_gemm");
-    if (int rc = router_logits(xin, T, L->gate_w, nullptr, nullptr, 1, n, w.gate, nullptr, s, 0, nullptr, nullptr))
+    // router logits and the shared expert's gate logit (row E) as one K-split register-tiled GEMM
+    if (int rc = router_gemm(xin, T, L->router_w, L->router_bias, L->gate_w, E, n, w.logits, w.gate, w.part, s))
         return rc;
-    timing_mark(s, "gate");
+    timing_mark(s, "router_gemm");
     if (int rc = route_topk(s, w.logits, T, E, K, ids_o, wts_o, counts, nullptr, 1 << 30)) return rc;
     timing_mark(s, "route_topk");
     return pf_moe(L->experts, L->stride, E, L->shared, n, ff, xin, ids_o, wts_o, w.gate, T, K, resid, out, w.rest,

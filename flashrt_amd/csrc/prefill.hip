@@ -346,6 +346,7 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
                 for (int i = 0; i < 4; ++i) av[i] = dequant8(cw[i], h, dw[i]);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
+                    if (c * 16 >= cnt) break;   // token columns past the group's end (ragged tiles)
                     const int col = c * 16 + li, off = bb * 64 + h * 32 + lg * 8;
 #pragma unroll
                     for (int part = 0; part < NP; ++part) {

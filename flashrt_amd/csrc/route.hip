@@ -270,24 +270,31 @@ int route_topk(hipStream_t stream, const float* logits, int T, int E, int K, int
 namespace frt {
 namespace {
 
-// logits [T][E] for many tokens, canonical order: K runs in natural order in tiles of L = n / 64
-// (one chain each); after each tile the chain sum joins a pairwise-tree stack (the adjacent pairwise
-// tree over chains 0..63 is a binary counter: chain j merges with the completed subtrees named by
-// the trailing one bits of j + 1), so the result equals the tree ((c0+c1)+(c2+c3))+... exactly.
-// Workgroup tile 64 tokens x 64 experts, 256 threads, 4 x 4 outputs per thread; x and W tiles in
-// LDS as [k][64] so a thread reads its 4 tokens and 4 experts as one float4 each.
+// logits [T][E] (and the shared gate [T] as row E) for many tokens in the canonical order, as a
+// K-split GEMM that follows the order's own tree: the adjacent pairwise tree over the 64 chains is
+// ((S0 + S1) + (S2 + S3)) with S_s the tree over chains 16 s .. 16 s + 15, so workgroup split s
+// computes S_s and k_router_combine forms the top two levels (and adds the bias) exactly.
+// Within a split, K runs in natural order in tiles of L = n / 64 (one chain each); after each tile
+// the chain sum joins a pairwise-tree stack (a binary counter: chain j merges with the completed
+// subtrees named by the trailing one bits of j + 1).
+// Workgroup tile 64 tokens x 64 rows, 256 threads, 4 x 4 outputs per thread; x and W tiles in LDS
+// as [k][64 (+4 pad)] (a thread reads its 4 tokens and 4 rows as one float4 each); the next chain's tiles
+// are loaded into registers while the current one is multiplied.
+constexpr int kRgSplit = 4, kRgChains = 64 / kRgSplit;
+
 template <int L>
-__global__ void __launch_bounds__(256) k_router_gemm(const float* __restrict__ x, int T, const float* __restrict__ W,
-                                                     const float* __restrict__ bias, int E, float* __restrict__ logits) {
-    __shared__ __align__(16) float sx[2][L][64];
-    __shared__ __align__(16) float sw[2][L][64];
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+k_router_gemm(const float* __restrict__ x, int T, const float* __restrict__ W, const float* __restrict__ gate_w, int E,
+                                                     float* __restrict__ part) {
+    // [k][64 + 4]: the transposing writes of 8 lanes (same row, 8 k) land in distinct bank groups
+    __shared__ __align__(16) float sx[2][L][68];
+    __shared__ __align__(16) float sw[2][L][68];
     const int n = 64 * L;
-    const int t0 = blockIdx.y * 64, e0 = blockIdx.x * 64;
+    const int E1 = E + (gate_w ? 1 : 0);
+    const int t0 = blockIdx.y * 64, e0 = blockIdx.x * 64, c0 = blockIdx.z * kRgChains;
     const int tid = threadIdx.x;
-    const int tr = (tid & 15) * 4, er = (tid >> 4) * 4;   // this thread's 4 tokens and 4 experts
-    // level registers of the pairwise tree: after chain c, lv[m] holds the pending subtree of level m
-    // when bit m of c + 1 ... (see merge below)
-    float lv[4][4][6];
+    const int tr = (tid & 15) * 4, er = (tid >> 4) * 4;   // this thread's 4 tokens and 4 rows
+    float lv[4][4][4];   // pending subtrees of the levels 0..3
     constexpr int F4 = L / 4;                    // float4 per row and chain
     constexpr int NP = (64 * F4 + 255) / 256;    // staging passes
     float4 rx[NP], rw[NP];
@@ -296,10 +303,11 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float* __restrict__ x
         for (int p = 0; p < NP; ++p) {
             const int idx = p * 256 + tid;
             const int row = idx / F4, q = idx % F4;
-            const int t = t0 + row, e = e0 + row;
+            const int t = min(t0 + row, T - 1), e = e0 + row;
+            const float* wrow = e < E ? W + size_t(e) * n : gate_w;   // row E: the gate vector
             const bool in = idx < 64 * F4;
-            rx[p] = in && t < T ? *reinterpret_cast<const float4*>(x + size_t(t) * n + c * L + q * 4) : make_float4(0, 0, 0, 0);
-            rw[p] = in && e < E ? *reinterpret_cast<const float4*>(W + size_t(e) * n + c * L + q * 4) : make_float4(0, 0, 0, 0);
+            rx[p] = in ? *reinterpret_cast<const float4*>(x + size_t(t) * n + c * L + q * 4) : make_float4(0, 0, 0, 0);
+            rw[p] = in && e < E1 ? *reinterpret_cast<const float4*>(wrow + c * L + q * 4) : make_float4(0, 0, 0, 0);
         }
     };
     auto store = [&](int buf) {
@@ -318,19 +326,19 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float* __restrict__ x
             sw[buf][q * 4 + 3][row] = rw[p].w;
         }
     };
-    load(0);
+    load(c0);
     store(0);
     __syncthreads();
     float total[4][4];
-    for (int c = 0; c < 64; ++c) {
+    for (int c = 0; c < kRgChains; ++c) {
         const int buf = c & 1;
-        if (c + 1 < 64) load(c + 1);
+        if (c + 1 < kRgChains) load(c0 + c + 1);
         float acc[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-#pragma unroll
+#pragma unroll 8
         for (int k = 0; k < L; ++k) {
             const float4 xv = *reinterpret_cast<const float4*>(&sx[buf][k][tr]);
             const float4 wv = *reinterpret_cast<const float4*>(&sw[buf][k][er]);
@@ -349,7 +357,7 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float* __restrict__ x
                 float v = acc[i][j];
                 bool parked = false;
 #pragma unroll
-                for (int m = 0; m < 6; ++m) {
+                for (int m = 0; m < 4; ++m) {
                     if (parked) continue;
                     if (((c >> m) & 1) == 0) {
                         lv[i][j][m] = v;
@@ -358,9 +366,9 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float* __restrict__ x
                         v = lv[i][j][m] + v;
                     }
                 }
-                if (!parked) total[i][j] = v;   // c == 63: the whole tree
+                if (!parked) total[i][j] = v;   // c == 15: the split's whole subtree
             }
-        if (c + 1 < 64) {
+        if (c + 1 < kRgChains) {
             store(buf ^ 1);
             __syncthreads();
         }
@@ -370,26 +378,45 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float* __restrict__ x
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int t = t0 + tr + i, e = e0 + er + j;
-            if (t < T && e < E) logits[size_t(t) * E + e] = bias ? total[i][j] + bias[e] : total[i][j];
+            if (t < T && e < E1) part[(size_t(blockIdx.z) * T + t) * E1 + e] = total[i][j];
         }
+}
+
+// top of the tree: v = (S0 + S1) + (S2 + S3); logits [T][E] = v + bias, gate [T] = row E's v
+__global__ void __launch_bounds__(256) k_router_combine(const float* __restrict__ part, int T, int E, int E1,
+                                                        const float* __restrict__ bias, float* __restrict__ logits,
+                                                        float* __restrict__ gate) {
+    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x, N = size_t(T) * E1;
+    if (i >= N) return;
+    const int t = int(i / E1), e = int(i % E1);
+    const float v = (part[i] + part[N + i]) + (part[2 * N + i] + part[3 * N + i]);
+    if (e < E) logits[size_t(t) * E + e] = bias ? v + bias[e] : v;
+    else gate[t] = v;
 }
 
 }  // namespace
 
-int router_gemm(const float* x, int T, const float* W, const float* bias, int E, int n, float* logits,
-                hipStream_t stream) {
+size_t router_gemm_ws_bytes(int T, int E, bool gate) { return size_t(kRgSplit) * T * (E + (gate ? 1 : 0)) * 4; }
+
+int router_gemm(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
+                float* logits, float* gate, float* part, hipStream_t stream) {
     if (n != 2048 && n != 2560 && n != 1024 && n != 3072 && n != 4096)
         return set_error(kErrShape, "router_gemm: n=%d", n);
-    dim3 grid((E + 63) / 64, (T + 63) / 64);
+    if (T < 1 || E < 1 || !part || (gate_w && !gate)) return set_error(kErrShape, "router_gemm: T=%d E=%d", T, E);
+    const int E1 = E + (gate_w ? 1 : 0);
+    dim3 grid((E1 + 63) / 64, (T + 63) / 64, kRgSplit);
     switch (n / 64) {
-        case 16: k_router_gemm<16><<<grid, 256, 0, stream>>>(x, T, W, bias, E, logits); break;
-        case 32: k_router_gemm<32><<<grid, 256, 0, stream>>>(x, T, W, bias, E, logits); break;
-        case 40: k_router_gemm<40><<<grid, 256, 0, stream>>>(x, T, W, bias, E, logits); break;
-        case 48: k_router_gemm<48><<<grid, 256, 0, stream>>>(x, T, W, bias, E, logits); break;
-        case 64: k_router_gemm<64><<<grid, 256, 0, stream>>>(x, T, W, bias, E, logits); break;
+        case 16: k_router_gemm<16><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+        case 32: k_router_gemm<32><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+        case 40: k_router_gemm<40><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+        case 48: k_router_gemm<48><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+        case 64: k_router_gemm<64><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
         default: return set_error(kErrShape, "router_gemm: n=%d", n);
     }
     FRT_LAUNCHED("router_gemm");
+    const size_t N = size_t(T) * E1;
+    k_router_combine<<<unsigned((N + 255) / 256), 256, 0, stream>>>(part, T, E, E1, bias, logits, gate);
+    FRT_LAUNCHED("router_combine");
     return kOk;
 }
 
