@@ -22,6 +22,15 @@ constexpr int kWave = 64;
 __host__ __device__ inline size_t mat_bytes(int rows, int cols) { return size_t(rows) * (cols / kBlock) * 18; }
 __host__ __device__ inline size_t expert_bytes(int n, int ff) { return 2 * mat_bytes(ff, n) + mat_bytes(n, ff); }
 
+// K order of a 64-block in the prefill GEMM operands (perm64). Lane group g of an MFMA A operand
+// holds code dword g of its row's block: code k of that dword (bits 2k, 2k+1; element
+// 16 (k % 4) + 4 g + k / 4) is dequantized into K-step (k / 4) % 2, slot 2 (k % 4) + k / 8 of
+// the lane's 8 operand values. Position of element j (0..63) of the block in that order:
+__host__ __device__ inline int perm64_pos(int j) {
+    const int s = j >> 4, g = (j >> 2) & 3, b = j & 3;
+    return 32 * (b & 1) + 8 * g + 2 * s + (b >> 1);
+}
+
 // C-ABI status codes
 enum Status : int {
     kOk = 0,

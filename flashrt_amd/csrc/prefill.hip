@@ -9,16 +9,9 @@
 //               placement is stable and needs no atomics.
 //   The shared expert, when present, is group E holding every token in order (rows T*K + t).
 //
-// GEMMs. Operands are exact in fp16: weights (q - 1) * d_w (a small integer times an fp16 scale)
-// and activation codes (int8). One v_mfma_f32_16x16x32_f16 covers exactly one 32-value
-// activation block, so its result (exact: integer multiples of d_w's ulp below 2^24) is scaled by
-// that block's d_a with one fp32 FMA: the float error is that of an fp32 dot product, and the Q8_0
-// quantization of h matches the CPU path's almost everywhere.
-//   K order of a 64-block as the MFMA lanes use it (perm64): half h, lane group g, slot i ->
-//   element 16 s + 4 g + c with s = 2h + i/4, c = (0, 2, 1, 3)[i % 4]; lane group g of a weight
-//   row then needs only code dword g of the block. Activations are stored in this order.
-//   k_pf_gateup  tile (64 tokens of one group) x 64 ff rows: gate and up, SwiGLU, Q8_0 of h
-//   k_pf_down    tile x 64 output rows: down -> yd[slot][n]
+// GEMMs (k_pf_gemm, below): Q2_0 weights dequantized exactly to fp16 in registers, activations
+// as exact fp16 (hi, lo) pairs (gate/up) or fp16 (down), fp32 accumulation on MFMA; tiles of 64
+// tokens of one group; the gate/up epilogue applies SwiGLU and the Q8_0 quantization of h.
 //   k_pf_combine out[t] = sum_k (in expert order) w * yd[t*K+k] + yd[shared t] * sigmoid(gate)
 #include "common.hpp"
 
@@ -155,23 +148,122 @@ __global__ void k_pf_place_shared(int T, int K, int32_t* __restrict__ tok_of, in
     }
 }
 
-// ---------------------------------------------------------------- GEMM pieces
+// ---------------------------------------------------------------- grouped GEMMs (gate + up, down)
+//
+// Operands enter the MFMA exactly, so the products are exact and only the fp32 accumulation rounds:
+//   A (weights): (q - 1) * d_w in fp16, dequantized in registers from the code dwords.
+//   B (activations a = code * d_a, Q8_0: up to 18 significant bits), in NP fp16 parts:
+//     NP = 2 (gate/up): hi = fp16(a), lo = fp16(a - hi); every 32-deep MFMA step is issued for
+//            both parts into one fp32 accumulator (gfx950's MFMA keeps the fp16 subnormals that
+//            the lo parts can be). Exactness matters here because h is requantized to Q8_0 after
+//            SwiGLU: a rounding difference would move h codes across rounding boundaries.
+//     NP = 1 (down): fp16(a), 2^-12 relative per element, with no requantization after it.
+//   No per-block scaling happens on the VALU.
+//
+// Dequantization: code k of a weight dword sits at bits 2k, 2k+1. Masked in place (p = 2k mod 8
+// within each 16-bit half) and OR'ed with the fp16 bits of M = 2^(10-p), whose ulp is 2^(p-10),
+// it reads as M + q exactly; (M + q) - (M + 1) = q - 1 and the product with d_w are exact too.
+// Codes 4..7 of each half are shifted down by 8 first. Per pair of weights: one v_and_or_b32,
+// one v_pk_add_f16 and one v_pk_mul_f16 (plus one shift per 16 weights).
+//
+// Workgroup: 512 threads (8 waves), 64 tokens x 512 A rows; each wave owns 4 A tiles of 16 rows
+// and all 4 token columns of 16, so every activation fragment read from LDS feeds 4 MFMAs and
+// every dequantized weight fragment up to 4 NP.
+//   gate+up: A rows 0..255 are gate rows f0 + 0..255, A rows 256..511 the same up rows; wave w owns
+//            ff rows f0 + 32 w .. +31 (gate and up). Epilogue: SwiGLU, Q8_0 of the 32-row block of h
+//            (quant/q2_0/moe_cpu.cpp:43-61), h = code * d written as fp16 for the down GEMM.
+//   down:    A rows are output rows r0 + 0..511, wave w owns r0 + 64 w .. +63; yd[slot][row] fp32.
+//
+// Staging (direct global-to-LDS loads, global_load_lds: each lane's bytes land at the wave's LDS
+// base + lane * size, so the loads take no registers):
+//   A, per super-stage of 4 blocks (K = 256), double-buffered: 4 adjacent lanes load one row's 64
+//   contiguous code bytes (and 2 lanes its 8 scale bytes). A weight row is a separate 512-byte
+//   (gate/up) or 128-byte (down) stretch of HBM, so this is what keeps the loads coalesced: one lane
+//   per row and block makes every lane a separate cache-line request, and the request rate, not
+//   the bytes, then bounds the kernel.
+//     codes  [512 rows][4 chunks of 16 B], block b of row r at chunk b ^ ((r >> 2) & 3): the MFMA
+//            read (16 rows x dword g of one block) then hits 64 distinct banks
+//     scales [512 rows][2 dwords] (fp16 scales of the 4 blocks)
+//   B, per stage of one block (K = 64), in a ring of kStages slots, issued kStages - 1 stages before
+//   the stage's operands are read from LDS into registers (which happens while the stage before it
+//   is multiplied, so neither the loads nor the LDS reads wait in line with the MFMAs):
+//     [NP][64 tokens][8 chunks of 8 fp16], chunk kc of token j at j * 8 + (kc ^ (j & 7)), so that the
+//     8 lanes of a 128-bit read phase hit 8 distinct bank groups.
+//   A super-stage k is issued just before the B loads of stage 4k, so waiting for a stage's B loads
+//   (loads complete in issue order) also covers its A super-stage.
+constexpr int kRows = 512;    // A rows per workgroup
+constexpr int kStages = 4;    // B ring slots
+constexpr int kSuper = 4;     // blocks per A super-stage
+constexpr int kSlotA = kRows * kSuper * 16, kSlotAs = kRows * kSuper * 2, kSlotB = kTN * kBlock * 2;
+template <int NP>
+constexpr int smem_bytes() { return 2 * (kSlotA + kSlotAs) + kStages * NP * kSlotB; }
 
-// A operand (8 fp16) of half h for one weight row's code dword g (see perm64 above), scaled by d.
-__device__ __forceinline__ half8 dequant8(uint32_t cw, int h, _Float16 d) {
-    const half2v one025 = {_Float16(1025.0f), _Float16(1025.0f)};
-    const half2v dd = {d, d};
-    half8 r;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
+// direct global -> LDS loads of 16 / 4 bytes per lane to lds_base + lane * size (lds_base uniform)
+__device__ __forceinline__ void ldsdma16(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((gbl_ptr_t)g, (lds_ptr_t)lds_base, 16, 0, 0);
+}
+__device__ __forceinline__ void ldsdma4(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((gbl_ptr_t)g, (lds_ptr_t)lds_base, 4, 0, 0);
+}
+// A workgroup barrier that does not wait for outstanding global loads (__syncthreads' release fence
+// would wait for all of them, the ring's later stages included): this wave's LDS accesses complete,
+// then s_barrier; the memory clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// s_waitcnt with vmcnt = N (gfx9 encoding; expcnt and lgkmcnt not waited for)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+// s_waitcnt vmcnt(n) for a run-time n in 0..31
+__device__ __forceinline__ void wait_vm_dyn(int n) {
+    switch (n) {
+#define FRT_WAIT_CASE(k) \
+    case k: wait_vm<k>(); break;
+        FRT_WAIT_CASE(0) FRT_WAIT_CASE(1) FRT_WAIT_CASE(2) FRT_WAIT_CASE(3) FRT_WAIT_CASE(4) FRT_WAIT_CASE(5)
+        FRT_WAIT_CASE(6) FRT_WAIT_CASE(7) FRT_WAIT_CASE(8) FRT_WAIT_CASE(9) FRT_WAIT_CASE(10) FRT_WAIT_CASE(11)
+        FRT_WAIT_CASE(12) FRT_WAIT_CASE(13) FRT_WAIT_CASE(14) FRT_WAIT_CASE(15)
+#undef FRT_WAIT_CASE
+        default: wait_vm<0>(); break;
+    }
+}
+
+// (x & mask) | bits as one v_and_or_b32 (with literal operands the compiler splits it in two)
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(bits));
+    return r;
+}
+
+// The fp16 bits of 2^(10 - 2m) in both halves, m = 0..3, held in VGPRs
+struct DqMagic {
+    uint32_t v[4];
+};
+__device__ __forceinline__ DqMagic dq_magic() {
+    DqMagic r;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int sh = 4 * h + ((k & 2) ? 2 : 0) + ((k & 1) ? 8 : 0);
-        const uint32_t x = ((cw >> sh) & 0x00030003u) | 0x64006400u;   // fp16 1024 + q in both halves
-        half2v v = __builtin_bit_cast(half2v, x);
-        v = (v - one025) * dd;                                        // (q - 1) * d, exact
-        r[2 * k] = v[0];
-        r[2 * k + 1] = v[1];
+    for (int m = 0; m < 4; ++m) {
+        r.v[m] = (0x6400u - 0x0800u * m) * 0x00010001u;
+        asm volatile("" : "+v"(r.v[m]));
     }
     return r;
+}
+
+// The 8 A operand values of K-step h of one weight row's code dword: pass cw for h = 0 and cw >> 8
+// for h = 1; dd = the row's block scale in both halves.
+__device__ __forceinline__ half8 dequant8(uint32_t c, half2v dd, const DqMagic& mg) {
+    half8 a;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const _Float16 off = _Float16(float((1 << (10 - 2 * m)) + 1));
+        const half2v offs = {off, off};
+        half2v v = __builtin_bit_cast(half2v, and_or(c, 0x00030003u << (2 * m), mg.v[m]));
+        v = (v - offs) * dd;
+        a[2 * m] = v[0];
+        a[2 * m + 1] = v[1];
+    }
+    return a;
 }
 
 __device__ __forceinline__ int lane_xor16(int v) {
@@ -183,133 +275,88 @@ __device__ __forceinline__ int lane_xor32(int v) {
     return (threadIdx.x & 32) ? int(r[0]) : int(r[1]);
 }
 
-__device__ __forceinline__ floatx4 mfma16(half8 a, half8 b) {
-    const floatx4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, z, 0, 0, 0);
-}
-
-// position of element e (0..63) of a 64-block in the perm64 order
-__device__ __forceinline__ int perm64_pos(int e) {
-    const int s = e >> 4, g = (e >> 2) & 3, c = e & 3;
-    const int ci = c == 0 ? 0 : c == 1 ? 2 : c == 2 ? 1 : 3;
-    return (s >> 1) * 32 + g * 8 + (s & 1) * 4 + ci;
-}
-
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
-
-// ---------------------------------------------------------------- grouped GEMMs (gate + up, down)
-//
-// Weights enter the MFMA exactly: (q - 1) * d_w in fp16, dequantized in registers from the code
-// dwords. Activations a = code * d (Q8_0: up to 18 significant bits) enter in NP fp16 parts:
-//   NP = 2 (gate/up): hi = fp16(a), lo = fp16(a - hi), so that A * hi + A * lo = A * a exactly; each
-//          32-deep MFMA step is issued for both parts into one fp32 accumulator (gfx950's MFMA keeps
-//          fp16 subnormals, which the lo parts often are). Exactness here matters because h is
-//          requantized to Q8_0 after SwiGLU.
-//   NP = 1 (down): fp16(a), 2^-12 relative per element, with no requantization after it.
-// No per-block scaling on the VALU either way.
-//
-// Workgroup: 512 threads (8 waves), 64 tokens x 512 A rows, K in stages of 128 through two LDS
-// buffers (the next stage is loaded into registers while the current one is multiplied). Each wave
-// owns 4 A tiles of 16 rows and all 4 token tiles, so every activation fragment read from LDS feeds
-// 4 NP MFMAs.
-//   gate+up: A rows 0..255 are gate rows f0 + 0..255, A rows 256..511 the same up rows; wave w owns
-//            ff rows f0 + 32 w .. +31 (gate and up). Epilogue: SwiGLU, Q8_0 of the 32-row block of h
-//            (quant/q2_0/moe_cpu.cpp:43-61), h = code * d written as fp16 for the down GEMM.
-//   down:    A rows are output rows r0 + 0..511, wave w owns r0 + 64 w .. +63; yd[slot][row] fp32.
-
-constexpr int kKC = 128;          // K per stage
-constexpr int kLdB = kKC + 8;     // padded fp16 row of an activation stage
-
-template <int NP>
-struct MmStage {
-    uint32_t a[512][kKC / 64][4];   // codes: A row, block, dword
-    uint32_t sc[512];               // the A row's two fp16 block scales
-    _Float16 b[NP][kTN][kLdB];      // activations (perm64 order): [0] fp16(a), [1] a - [0] when NP == 2
-};
-
 __device__ __forceinline__ floatx4 mfma_acc(half8 a, half8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-template <bool GATEUP, int NP>
-__global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena, size_t stride, int E,
-                                               const uint8_t* __restrict__ shared_blob, int n, int ff,
-                                               const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
-                                               const int32_t* __restrict__ tok_of, const int32_t* __restrict__ bounds,
-                                               const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-                                               _Float16* __restrict__ hout,
-                                               float* __restrict__ yd, const int32_t* __restrict__ slot_of) {
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+template <bool GATEUP>
+__global__ void __launch_bounds__(512) k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E,
+                                                 const uint8_t* __restrict__ shared_blob, int n, int ff,
+                                                 const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
+                                                 const int32_t* __restrict__ tok_of, const int32_t* __restrict__ bounds,
+                                                 const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
+                                                 _Float16* __restrict__ hout,
+                                                 float* __restrict__ yd, const int32_t* __restrict__ slot_of) {
+    constexpr int NP = GATEUP ? 2 : 1;
+    constexpr int kDA = kSlotA / 16 / 512 + kSlotAs / 4 / 512;   // A loads per lane per super-stage (4 + 2)
     if (int(blockIdx.y) >= *n_tiles) return;
     extern __shared__ __align__(16) uint8_t smem[];
-    MmStage<NP>* st = reinterpret_cast<MmStage<NP>*>(smem);
-    __shared__ int sTok[kTN];
+    __shared__ int sRow[kTN];
+    FRT_PROBE_BEGIN();
+    FRT_PROBE(GATEUP ? 0 : 1, 0);
     const int2 tile = tiles[blockIdx.y];
     const int grp = tile.x;
     const int row0 = bounds[grp] + tile.y;
     const int cnt = min(kTN, bounds[grp + 1] - row0);
     const uint8_t* blob = grp < E ? arena + size_t(grp) * stride : shared_blob;
     const int Kd = GATEUP ? n : ff;            // contraction length
-    const int nbk = Kd / kBlock;               // weight blocks per A row
+    const int nbk = Kd / kBlock;               // weight blocks per A row (a multiple of kSuper)
     const int rows_total = GATEUP ? ff : n;    // rows of each A matrix
     const size_t mb = mat_bytes(ff, n);
-    const uint8_t* m0 = GATEUP ? blob : blob + 2 * mb;      // gate (or down)
-    const uint8_t* m1 = blob + mb;                          // up
-    const int rbase = blockIdx.x * (GATEUP ? 256 : 512);
+    const int rbase = blockIdx.x * (GATEUP ? kRows / 2 : kRows);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    if (tid < kTN) sTok[tid] = tid < cnt ? (GATEUP ? tok_of[row0 + tid] : row0 + tid) : -1;
+    // B row of each tile token: x row = token (gate/up), h row = dispatched row (down); a token
+    // past the group's end repeats the first (its columns are skipped and never written)
+    if (tid < kTN) sRow[tid] = GATEUP ? tok_of[row0 + min(tid, cnt - 1)] : row0 + min(tid, cnt - 1);
     __syncthreads();
 
-    // the A row `ar` of the tile: matrix and row index
-    auto arow = [&](int ar, const uint8_t*& m, int& r) {
-        if (GATEUP) {
-            m = ar < 256 ? m0 : m1;
-            r = rbase + (ar & 255);
-        } else {
-            m = m0;
-            r = rbase + ar;
-        }
+    // A row t of the tile -> its matrix row (rows past the end load any row; never stored)
+    auto a_mat = [&](int t, const uint8_t*& m, int& r) {
+        m = GATEUP ? (t < kRows / 2 ? blob : blob + mb) : blob + 2 * mb;
+        r = min(rbase + (GATEUP ? (t & (kRows / 2 - 1)) : t), rows_total - 1);
     };
-    uint4 ra[2];
-    uint32_t rs;
-    uint4 rb[2 * NP];
-    auto load = [&](int k0) {
-        const int b0 = k0 / kBlock;
+    // this thread's A loads of a super-stage: code chunks at LDS positions P = 512 p + tid (row P / 4,
+    // block (P % 4) ^ ((row / 4) % 4)), scale dwords at Q = 512 p + tid (row Q / 2, blocks 2 (Q % 2) + 0..1)
+    const uint8_t* acode[4];
+    const uint8_t* ascale[2];
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int idx = p * 512 + tid, ar = idx >> 1, blk = idx & 1;
-            const uint8_t* m;
-            int r;
-            arow(ar, m, r);
-            ra[p] = r < rows_total ? *reinterpret_cast<const uint4*>(m + (size_t(r) * nbk + b0 + blk) * 16)
-                                   : make_uint4(0, 0, 0, 0);
-        }
-        {
-            const uint8_t* m;
-            int r;
-            arow(tid, m, r);
-            const uint32_t* sc = reinterpret_cast<const uint32_t*>(m + size_t(rows_total) * nbk * 16 + (size_t(r) * nbk + b0) * 2);
-            rs = r < rows_total ? *sc : 0u;
-        }
+    for (int p = 0; p < 4; ++p) {
+        const int P = 512 * p + tid, t = P >> 2, blk = (P & 3) ^ ((t >> 2) & 3);
+        const uint8_t* m;
+        int r;
+        a_mat(t, m, r);
+        acode[p] = m + (size_t(r) * nbk + blk) * 16;
+    }
 #pragma unroll
-        for (int p = 0; p < 2 * NP; ++p) {
-            const int idx = p * 512 + tid, which = idx >> 10, rem = idx & 1023, j = rem >> 4, q = rem & 15;
-            const int t = sTok[j];
-            const _Float16* src = which ? blo : bhi;
-            rb[p] = t >= 0 ? *reinterpret_cast<const uint4*>(src + size_t(t) * Kd + k0 + q * 8) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store = [&](MmStage<NP>& S) {
+    for (int p = 0; p < 2; ++p) {
+        const int Q = 512 * p + tid, t = Q >> 1;
+        const uint8_t* m;
+        int r;
+        a_mat(t, m, r);
+        ascale[p] = m + size_t(rows_total) * nbk * 16 + size_t(r) * nbk * 2 + (Q & 1) * 4;
+    }
+    size_t boff;
+    {
+        const int j = tid >> 3, kc = (tid & 7) ^ (j & 7);
+        boff = size_t(sRow[j]) * Kd + kc * 8;
+    }
+    uint8_t* const sA = smem;                                   // [2][kSlotA + kSlotAs]
+    uint8_t* const sB = smem + 2 * (kSlotA + kSlotAs);         // [kStages][NP][kSlotB]
+    // the loads of stage u: A super-stage u / 4 first when u % 4 == 0, then u's B parts
+    auto issue = [&](int u) {
+        if (u % kSuper == 0) {
+            const int k = u / kSuper;
+            uint8_t* a = sA + (k & 1) * (kSlotA + kSlotAs);
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int idx = p * 512 + tid, ar = idx >> 1, blk = idx & 1;
-            *reinterpret_cast<uint4*>(&S.a[ar][blk][0]) = ra[p];
-        }
-        S.sc[tid] = rs;
+            for (int p = 0; p < 4; ++p) ldsdma16(acode[p] + size_t(u) * 16, a + p * 8192 + wave * 1024);
 #pragma unroll
-        for (int p = 0; p < 2 * NP; ++p) {
-            const int idx = p * 512 + tid, which = idx >> 10, rem = idx & 1023, j = rem >> 4, q = rem & 15;
-            *reinterpret_cast<uint4*>(&S.b[which][j][q * 8]) = rb[p];
+            for (int p = 0; p < 2; ++p) ldsdma4(ascale[p] + size_t(u) * 2, a + kSlotA + p * 2048 + wave * 256);
         }
+        uint8_t* b = sB + (u % kStages) * NP * kSlotB;
+        ldsdma16(bhi + boff + size_t(u) * kBlock, b + wave * 1024);
+        if constexpr (NP == 2) ldsdma16(blo + boff + size_t(u) * kBlock, b + kSlotB + wave * 1024);
     };
 
     floatx4 acc[4][4];
@@ -321,51 +368,105 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
     int art[4];   // this lane's A row in the tile for each of its 4 A tiles
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        art[i] = GATEUP ? ((i < 2 ? 0 : 256) + 32 * wave + 16 * (i & 1) + li) : (64 * wave + 16 * i + li);
+        art[i] = GATEUP ? ((i < 2 ? 0 : kRows / 2) + 32 * wave + 16 * (i & 1) + li) : (64 * wave + 16 * i + li);
+    const int ncol = (cnt + 15) / 16;   // token columns with at least one real token
+    const DqMagic mg = dq_magic();
 
-    const int nstage = Kd / kKC;
-    load(0);
-    store(st[0]);
-    __syncthreads();
+    // A stage's operands are read from LDS ahead of their use: the codes, scales and the first K-step's
+    // activation fragments one stage ahead (in flight while the stage before is multiplied), the
+    // second K-step's fragments at the start of the stage itself.
+    struct Ops {
+        uint32_t cw[4];
+        uint32_t sc[4];
+        half8 bv[4][NP];
+    };
+    auto read_b = [&](int st, int h, half8 (&bv)[4][NP]) {
+        const half8* sb = reinterpret_cast<const half8*>(sB + (st % kStages) * NP * kSlotB);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int j = c * 16 + li, kc = h * 4 + lg;
+#pragma unroll
+            for (int part = 0; part < NP; ++part) bv[c][part] = sb[part * (kSlotB / 16) + j * 8 + (kc ^ (j & 7))];
+        }
+    };
+    auto read_ops = [&](int st, Ops& o) {
+        const uint8_t* a = sA + ((st / kSuper) & 1) * (kSlotA + kSlotAs);
+        const uint32_t* sa = reinterpret_cast<const uint32_t*>(a);
+        const uint32_t* sas = reinterpret_cast<const uint32_t*>(a + kSlotA);
+        const int bq = st % kSuper;   // block within the super-stage
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = art[i];
+            o.cw[i] = sa[(r * 4 + (bq ^ ((r >> 2) & 3))) * 4 + lg];
+            o.sc[i] = sas[r * 2 + (bq >> 1)] >> (16 * (bq & 1));
+        }
+        read_b(st, 0, o.bv);
+    };
+    // loads issued after stage st's: later stages' B parts and the A super-stages among them
+    auto wait_stage = [&](int st, int issued_to) {
+        int later = 0;
+        for (int u = st + 1; u < issued_to; ++u) later += NP + (u % kSuper == 0 ? kDA : 0);
+        wait_vm_dyn(later);
+    };
+    auto mul = [&](const uint32_t (&cw)[4], const uint32_t (&sc)[4], int h, const half8 (&bv)[4][NP]) {
+        half8 av[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const _Float16 d = __builtin_bit_cast(_Float16, uint16_t(sc[i]));
+            av[i] = dequant8(h ? cw[i] >> 8 : cw[i], half2v{d, d}, mg);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            if (c == 0 || c < ncol) {   // a tile has at least one token
+#pragma unroll
+                for (int part = 0; part < NP; ++part)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[i][c] = mfma_acc(av[i], bv[c][part], acc[i][c]);
+            }
+        }
+    };
+
+    // B slot of stage u is refilled by stage u + kStages once every wave has read stage u (both
+    // K-steps), i.e. after the barrier of iteration u + 1
+    const int nstage = nbk;
+    int issued = min(kStages, nstage);   // stages issued so far (0 .. issued - 1)
+    for (int u = 0; u < issued; ++u) issue(u);
+    Ops cur;
+    wait_stage(0, issued);
+    ring_barrier();
+    read_ops(0, cur);
     for (int sI = 0; sI < nstage; ++sI) {
-        MmStage<NP>& S = st[sI & 1];
-        if (sI + 1 < nstage) load((sI + 1) * kKC);
-#pragma unroll
-        for (int bb = 0; bb < kKC / 64; ++bb) {
-            uint32_t cw[4];
-            _Float16 dw[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                cw[i] = S.a[art[i]][bb][lg];
-                dw[i] = __builtin_bit_cast(_Float16, uint16_t(S.sc[art[i]] >> (16 * bb)));
-            }
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                half8 av[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) av[i] = dequant8(cw[i], h, dw[i]);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    if (c * 16 >= cnt) break;   // token columns past the group's end (ragged tiles)
-                    const int col = c * 16 + li, off = bb * 64 + h * 32 + lg * 8;
-#pragma unroll
-                    for (int part = 0; part < NP; ++part) {
-                        const half8 bv = *reinterpret_cast<const half8*>(&S.b[part][col][off]);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[i][c] = mfma_acc(av[i], bv, acc[i][c]);
-                    }
-                }
-            }
-        }
+#ifdef FRT_PF_STAGE_PROBE
+        const int pk = (GATEUP && (sI == 12 || sI == 13)) ? sI - 10 : -1;
+#define SPROBE(i) do { if (pk >= 0) FRT_PROBE(pk, i); } while (0)
+#else
+#define SPROBE(i) do { } while (0)
+#endif
+        SPROBE(0);
+        half8 b1[4][NP];
+        read_b(sI, 1, b1);   // issued before the next stage's reads, so it completes first
+        Ops nxt;
         if (sI + 1 < nstage) {
-            store(st[(sI + 1) & 1]);
-            __syncthreads();
+            wait_stage(sI + 1, issued);   // stage sI + 1's loads are done
+            SPROBE(1);
+            ring_barrier();   // ... for every wave, and every wave's reads of stage sI - 1 are complete
+            SPROBE(2);
+            if (sI >= 1 && issued < nstage) issue(issued++);   // into stage sI - 1's slot
+            read_ops(sI + 1, nxt);
+            SPROBE(3);
         }
+        mul(cur.cw, cur.sc, 0, cur.bv);
+        SPROBE(4);
+        mul(cur.cw, cur.sc, 1, b1);
+        SPROBE(5);
+        cur = nxt;
+#undef SPROBE
     }
 
+    FRT_PROBE(GATEUP ? 0 : 1, 1);
     if constexpr (GATEUP) {
-        // lane: token col c*16 + li; ff rows f = rbase + 32 wave + 16 i + 4 lg + j (i = 0, 1) for gate
-        // (acc[i]) and up (acc[2 + i]). The 32 rows of the wave are one Q8_0 block of h.
+        // lane: token column c*16 + li; ff rows f = rbase + 32 wave + 16 i + 4 lg + q (i = 0, 1) for
+        // gate (acc[i]) and up (acc[2 + i]). The 32 rows of the wave are one Q8_0 block of h.
         const int fbase = rbase + 32 * wave;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -375,9 +476,9 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    hv[i][j] = silu_mul(acc[i][c][j], acc[2 + i][c][j]);
-                    am = fmaxf(am, fabsf(hv[i][j]));
+                for (int q = 0; q < 4; ++q) {
+                    hv[i][q] = silu_mul(acc[i][c][q], acc[2 + i][c][q]);
+                    am = fmaxf(am, fabsf(hv[i][q]));
                 }
             am = fmaxf(am, __builtin_bit_cast(float, lane_xor16(__builtin_bit_cast(int, am))));
             am = fmaxf(am, __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(int, am))));
@@ -389,11 +490,10 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int f = fbase + 16 * i + 4 * lg + j;
-                        const float a = float(q8_code(hv[i][j], id)) * dr;
-                        const size_t pos = row * ff + (f & ~63) + perm64_pos(f & 63);
-                        hout[pos] = _Float16(a);   // h for the down GEMM, one fp16 part
+                    for (int q = 0; q < 4; ++q) {
+                        const int f = fbase + 16 * i + 4 * lg + q;
+                        const float a = float(q8_code(hv[i][q], id)) * dr;
+                        hout[row * ff + (f & ~63) + perm64_pos(f & 63)] = _Float16(a);
                     }
             }
         }
@@ -410,6 +510,8 @@ __global__ void __launch_bounds__(512) k_pf_mm(const uint8_t* __restrict__ arena
             }
         }
     }
+    FRT_PROBE(GATEUP ? 0 : 1, 2);
+    FRT_PROBE_END();
 }
 
 // ---------------------------------------------------------------- combine
@@ -477,9 +579,8 @@ __global__ void k_to_bf16(const float* __restrict__ src, __hip_bfloat16* __restr
 struct PfWs {
     int32_t *cnt, *bounds, *tok_of, *slot_of, *n_tiles;
     int2* tiles;
-    _Float16* xhi;
-    _Float16* xlo;
-    _Float16* hhi;
+    _Float16 *xhi, *xlo;   // x = code * d as an exact fp16 pair, perm64 order [T][n]
+    _Float16* h16;         // h = code * d as fp16, perm64 order [S][ff]
     float* yd;   // fp32 per-slot outputs when the caller does not receive them as fp32
     size_t bytes;
 };
@@ -505,7 +606,7 @@ static PfWs pf_carve(void* base, int T, int K, int n, int ff, int E, bool shared
     w.tiles = reinterpret_cast<int2*>(take(size_t(pf_max_tiles(S, G)) * 8));
     w.xhi = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
     w.xlo = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
-    w.hhi = reinterpret_cast<_Float16*>(take(size_t(S) * ff * 2));
+    w.h16 = reinterpret_cast<_Float16*>(take(size_t(S) * ff * 2));
     w.yd = own_yd ? reinterpret_cast<float*>(take(size_t(S) * n * 4)) : nullptr;
     w.bytes = size_t(p - static_cast<uint8_t*>(base));
     return w;
@@ -520,36 +621,34 @@ int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16
 
 int pf_check(int T, int K, int n, int ff, int E) {
     if (T < 1 || K < 1 || K > 32 || E < 1 || E > 4096 || K > E) return set_error(kErrShape, "prefill: T=%d K=%d E=%d", T, K, E);
-    if (n % 256 || ff % 128 || n < 256 || ff < 128)
-        return set_error(kErrShape, "prefill: n=%d ff=%d (n a multiple of 256, ff of 128)", n, ff);
+    if (n % 256 || ff % 256 || n < 256 || ff < 256)   // whole A super-stages of 4 blocks
+        return set_error(kErrShape, "prefill: n=%d ff=%d (n and ff multiples of 256)", n, ff);
     return kOk;
 }
 
-template <bool GATEUP, int NP>
-static int pf_mm_attr() {
+template <bool GATEUP>
+static int pf_gemm_attr() {
     static bool done = false;   // per process; the attribute is a property of the kernel
     if (!done) {
-        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_mm<GATEUP, NP>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(2 * sizeof(MmStage<NP>))));
+        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<GATEUP>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, smem_bytes<GATEUP ? 2 : 1>()));
         done = true;
     }
     return kOk;
 }
 
-// The two grouped GEMMs. gate/up reads x as exact hi/lo pairs: h is requantized to Q8_0 after
-// SwiGLU, and an fp16 rounding of x (2^-12 relative) moves enough h values across a code boundary
-// to be seen at the output. down reads h as single fp16 values (2^-12 relative per element,
-// summed with no requantization after it).
+// The two grouped GEMMs (k_pf_gemm): gate/up on the exact x pairs, SwiGLU and Q8_0 of h in the
+// epilogue; down on h -> fp32 yd per slot.
 static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, int n, int ff,
                            const PfWs& w, int mt, float* ydf, hipStream_t stream) {
-    if (int rc = pf_mm_attr<true, 2>()) return rc;
-    if (int rc = pf_mm_attr<false, 1>()) return rc;
-    k_pf_mm<true, 2><<<dim3((ff + 255) / 256, mt), 512, 2 * sizeof(MmStage<2>), stream>>>(
-        arena, stride, E, shared_blob, n, ff, w.xhi, w.xlo, w.tok_of, w.bounds, w.tiles, w.n_tiles, w.hhi, nullptr,
+    if (int rc = pf_gemm_attr<true>()) return rc;
+    if (int rc = pf_gemm_attr<false>()) return rc;
+    k_pf_gemm<true><<<dim3((ff + kRows / 2 - 1) / (kRows / 2), mt), 512, smem_bytes<2>(), stream>>>(
+        arena, stride, E, shared_blob, n, ff, w.xhi, w.xlo, w.tok_of, w.bounds, w.tiles, w.n_tiles, w.h16, nullptr,
         nullptr);
     timing_mark(stream, "pf_gateup");
-    k_pf_mm<false, 1><<<dim3((n + 511) / 512, mt), 512, 2 * sizeof(MmStage<1>), stream>>>(
-        arena, stride, E, shared_blob, n, ff, w.hhi, nullptr, w.tok_of, w.bounds, w.tiles, w.n_tiles, nullptr, ydf,
+    k_pf_gemm<false><<<dim3((n + kRows - 1) / kRows, mt), 512, smem_bytes<1>(), stream>>>(
+        arena, stride, E, shared_blob, n, ff, w.h16, nullptr, w.tok_of, w.bounds, w.tiles, w.n_tiles, nullptr, ydf,
         w.slot_of);
     return kOk;
 }

@@ -136,8 +136,9 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, in
 }
 
 // ---- Q8_0 of activations: one wave per 2 blocks of 32 (quant/q2_0/q2_0.cpp:93-108).
-// xq int8 [rows][n] natural order, xd [rows][n/32]. With xq16: the same codes as fp16 in the
-// prefill GEMM's operand order (perm64 below), [rows][n].
+// xq int8 [rows][n] natural order, xd [rows][n/32]. With xhi (and xlo): the activations a = q * d as
+// fp16 in the prefill GEMM's operand order (perm64_pos), [rows][n]: xhi = fp16(a) and
+// xlo = fp16(a - xhi), an exact pair (a has at most 7 + 11 significant bits).
 __global__ void k_quant_q8(const float* __restrict__ x, int n_blocks, int8_t* __restrict__ xq, float* __restrict__ xd,
                            _Float16* __restrict__ xhi, _Float16* __restrict__ xlo, int n) {
     const int gw = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;   // global wave
@@ -156,17 +157,11 @@ __global__ void k_quant_q8(const float* __restrict__ x, int n_blocks, int8_t* __
     const float dr = f16_round(d);
     if (xd && j == 0) xd[blk] = dr;
     if (xhi) {
-        // the activation q * d as an exact fp16 pair, at its position in the perm64 order of the
-        // prefill GEMM (element 16 s + 4 g + c of a 64-block sits at 32 (s / 2) + 8 g + 4 (s % 2) + ci,
-        // ci = 0, 2, 1, 3 for c = 0, 1, 2, 3)
-        const int e = (blk & 1) * 32 + j;
-        const int s = e >> 4, g = (e >> 2) & 3, c = e & 3;
-        const int ci = c == 0 ? 0 : c == 1 ? 2 : c == 2 ? 1 : 3;
-        const size_t pos = size_t(blk >> 1) * kBlock + (s >> 1) * 32 + g * 8 + (s & 1) * 4 + ci;
+        const size_t pos = size_t(blk >> 1) * kBlock + perm64_pos((blk & 1) * 32 + j);
         const float a = float(q) * dr;
         const _Float16 hi = _Float16(a);
         xhi[pos] = hi;
-        xlo[pos] = _Float16(a - float(hi));
+        if (xlo) xlo[pos] = _Float16(a - float(hi));
     }
 }
 
