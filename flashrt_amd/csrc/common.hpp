@@ -22,13 +22,16 @@ constexpr int kWave = 64;
 __host__ __device__ inline size_t mat_bytes(int rows, int cols) { return size_t(rows) * (cols / kBlock) * 18; }
 __host__ __device__ inline size_t expert_bytes(int n, int ff) { return 2 * mat_bytes(ff, n) + mat_bytes(n, ff); }
 
-// K order of a 64-block in the prefill GEMM operands (perm64). Lane group g of an MFMA A operand
-// holds code dword g of its row's block: code k of that dword (bits 2k, 2k+1; element
-// 16 (k % 4) + 4 g + k / 4) is dequantized into K-step (k / 4) % 2, slot 2 (k % 4) + k / 8 of
-// the lane's 8 operand values. Position of element j (0..63) of the block in that order:
-__host__ __device__ inline int perm64_pos(int j) {
-    const int s = j >> 4, g = (j >> 2) & 3, b = j & 3;
-    return 32 * (b & 1) + 8 * g + 2 * s + (b >> 1);
+// K order of the prefill GEMM operands within each 256-element stretch (four Q2_0 blocks), perm256.
+// MFMA lane group g holds block g of the stretch as one 16-byte code chunk; K-step t (0..7, 32 deep)
+// takes from it code dword t / 2, codes 4 (t % 2) + m and 8 + 4 (t % 2) + m (m = 0..3), as operand
+// slots 2m and 2m + 1. Code k of dword d is element 16 (k % 4) + 4 d + k / 4 of the block. Position of
+// element K (0..255) of the stretch in that order:
+__host__ __device__ inline int perm256_pos(int K) {
+    const int g = K >> 6, j = K & 63;
+    const int k = 4 * (j & 3) + (j >> 4);   // code index within its dword
+    const int d = (j & 15) >> 2;            // dword
+    return 32 * (2 * d + ((k >> 2) & 1)) + 8 * g + 2 * (k & 3) + (k >> 3);
 }
 
 // C-ABI status codes
@@ -88,7 +91,8 @@ __device__ __forceinline__ unsigned long long* frt_probe_lds() {
     } while (0)
 #define FRT_PROBE_END()                                                                            \
     do {                                                                                           \
-        if (threadIdx.x < 32 && frt_probe_lds()[threadIdx.x])                                      \
+        if (threadIdx.x < 32 && frt_probe_lds()[threadIdx.x] &&                                    \
+            blockIdx.x + blockIdx.y * gridDim.x < 2048) /* rows of the table */                       \
             frt_probe[threadIdx.x / 8][blockIdx.x + blockIdx.y * gridDim.x][threadIdx.x % 8] =     \
                 frt_probe_lds()[threadIdx.x];                                                      \
     } while (0)

@@ -17,6 +17,8 @@
 
 #include <hip/hip_bf16.h>
 
+#include <type_traits>
+
 namespace frt {
 
 constexpr int kTN = 64;        // tokens per GEMM tile
@@ -174,43 +176,43 @@ __global__ void k_pf_place_shared(int T, int K, int32_t* __restrict__ tok_of, in
 //            (quant/q2_0/moe_cpu.cpp:43-61), h = code * d written as fp16 for the down GEMM.
 //   down:    A rows are output rows r0 + 0..511, wave w owns r0 + 64 w .. +63; yd[slot][row] fp32.
 //
-// Staging (direct global-to-LDS loads, global_load_lds: each lane's bytes land at the wave's LDS
-// base + lane * size, so the loads take no registers):
-//   A, per super-stage of 4 blocks (K = 256), double-buffered: 4 adjacent lanes load one row's 64
-//   contiguous code bytes (and 2 lanes its 8 scale bytes). A weight row is a separate 512-byte
-//   (gate/up) or 128-byte (down) stretch of HBM, so this is what keeps the loads coalesced: one lane
-//   per row and block makes every lane a separate cache-line request, and the request rate, not
-//   the bytes, then bounds the kernel.
-//     codes  [512 rows][4 chunks of 16 B], block b of row r at chunk b ^ ((r >> 2) & 3): the MFMA
-//            read (16 rows x dword g of one block) then hits 64 distinct banks
-//     scales [512 rows][2 dwords] (fp16 scales of the 4 blocks)
-//   B, per stage of one block (K = 64), in a ring of kStages slots, issued kStages - 1 stages before
-//   the stage's operands are read from LDS into registers (which happens while the stage before it
-//   is multiplied, so neither the loads nor the LDS reads wait in line with the MFMAs):
-//     [NP][64 tokens][8 chunks of 8 fp16], chunk kc of token j at j * 8 + (kc ^ (j & 7)), so that the
-//     8 lanes of a 128-bit read phase hit 8 distinct bank groups.
-//   A super-stage k is issued just before the B loads of stage 4k, so waiting for a stage's B loads
-//   (loads complete in issue order) also covers its A super-stage.
+// K order (perm256_pos): within each 256-element stretch, MFMA lane group g takes block g of the
+// stretch. So the weights go straight from HBM into registers: lane (row i, group g) loads the
+// 16-byte code chunk of block g of its row, and the 4 lanes of a row read 64 contiguous bytes (a
+// weight row is a separate 512-byte (gate/up) or 128-byte (down) stretch of HBM; one lane per row
+// and 16-byte chunk would make every lane a separate cache-line request). Each wave loads only
+// its own rows, one stretch ahead, into a second register set.
+//
+// Activations go through LDS: stages of 128 K (half a stretch) in a ring of kStages slots filled by
+// direct global-to-LDS loads (global_load_lds: each lane's 16 bytes land at the wave's LDS base +
+// 16 lane, no registers), issued two stages ahead; one workgroup barrier per stage. Slot layout:
+//   [NP][64 tokens][16 chunks of 8 fp16], chunk kc of token j at j * 16 + (kc ^ (j & 15)), so that
+//   the lanes of a 128-bit read phase (one chunk of 8 or 16 tokens) hit distinct bank groups.
 constexpr int kRows = 512;    // A rows per workgroup
-constexpr int kStages = 4;    // B ring slots
-constexpr int kSuper = 4;     // blocks per A super-stage
-constexpr int kSlotA = kRows * kSuper * 16, kSlotAs = kRows * kSuper * 2, kSlotB = kTN * kBlock * 2;
+constexpr int kStages = 3;    // activation ring slots (stages issued kStages - 1 ahead)
+constexpr int kStageK = 128;  // K per activation stage
+constexpr int kSlotB = kTN * kStageK * 2;   // bytes per part per slot
 template <int NP>
-constexpr int smem_bytes() { return 2 * (kSlotA + kSlotAs) + kStages * NP * kSlotB; }
+constexpr int smem_bytes() { return kStages * NP * kSlotB; }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
-// direct global -> LDS loads of 16 / 4 bytes per lane to lds_base + lane * size (lds_base uniform)
+// direct global -> LDS load of 16 bytes per lane to lds_base + 16 lane (lds_base uniform)
 __device__ __forceinline__ void ldsdma16(const void* g, void* lds_base) {
     __builtin_amdgcn_global_load_lds((gbl_ptr_t)g, (lds_ptr_t)lds_base, 16, 0, 0);
 }
-__device__ __forceinline__ void ldsdma4(const void* g, void* lds_base) {
-    __builtin_amdgcn_global_load_lds((gbl_ptr_t)g, (lds_ptr_t)lds_base, 4, 0, 0);
-}
 // A workgroup barrier that does not wait for outstanding global loads (__syncthreads' release fence
 // would wait for all of them, the ring's later stages included): this wave's LDS accesses complete,
-// then s_barrier; the memory clobber keeps the compiler from moving memory accesses across it.
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// then s_barrier. The wait is the builtin (so the compiler's own wait insertion knows the LDS reads
+// before it are complete); the empty asm statements keep memory accesses from moving across.
+__device__ __forceinline__ void ring_barrier() {
+    __builtin_amdgcn_sched_barrier(0);   // nothing is scheduled across (register math included)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt and expcnt not waited for
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
 // s_waitcnt with vmcnt = N (gfx9 encoding; expcnt and lgkmcnt not waited for)
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -290,7 +292,8 @@ __global__ void __launch_bounds__(512) k_pf_gemm(const uint8_t* __restrict__ are
                                                  _Float16* __restrict__ hout,
                                                  float* __restrict__ yd, const int32_t* __restrict__ slot_of) {
     constexpr int NP = GATEUP ? 2 : 1;
-    constexpr int kDA = kSlotA / 16 / 512 + kSlotAs / 4 / 512;   // A loads per lane per super-stage (4 + 2)
+    constexpr int kDB = 2 * NP;   // direct loads per lane per activation stage
+    constexpr int kDA = 8;        // weight loads per lane per stretch (4 code chunks + 4 scales)
     if (int(blockIdx.y) >= *n_tiles) return;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int sRow[kTN];
@@ -301,62 +304,70 @@ __global__ void __launch_bounds__(512) k_pf_gemm(const uint8_t* __restrict__ are
     const int row0 = bounds[grp] + tile.y;
     const int cnt = min(kTN, bounds[grp + 1] - row0);
     const uint8_t* blob = grp < E ? arena + size_t(grp) * stride : shared_blob;
-    const int Kd = GATEUP ? n : ff;            // contraction length
-    const int nbk = Kd / kBlock;               // weight blocks per A row (a multiple of kSuper)
+    const int Kd = GATEUP ? n : ff;            // contraction length (a multiple of 512)
+    const int nbk = Kd / kBlock;               // weight blocks per A row
     const int rows_total = GATEUP ? ff : n;    // rows of each A matrix
     const size_t mb = mat_bytes(ff, n);
     const int rbase = blockIdx.x * (GATEUP ? kRows / 2 : kRows);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int li = lane & 15, lg = lane >> 4;
     // B row of each tile token: x row = token (gate/up), h row = dispatched row (down); a token
     // past the group's end repeats the first (its columns are skipped and never written)
     if (tid < kTN) sRow[tid] = GATEUP ? tok_of[row0 + min(tid, cnt - 1)] : row0 + min(tid, cnt - 1);
     __syncthreads();
 
-    // A row t of the tile -> its matrix row (rows past the end load any row; never stored)
-    auto a_mat = [&](int t, const uint8_t*& m, int& r) {
-        m = GATEUP ? (t < kRows / 2 ? blob : blob + mb) : blob + 2 * mb;
-        r = min(rbase + (GATEUP ? (t & (kRows / 2 - 1)) : t), rows_total - 1);
-    };
-    // this thread's A loads of a super-stage: code chunks at LDS positions P = 512 p + tid (row P / 4,
-    // block (P % 4) ^ ((row / 4) % 4)), scale dwords at Q = 512 p + tid (row Q / 2, blocks 2 (Q % 2) + 0..1)
-    const uint8_t* acode[4];
-    const uint8_t* ascale[2];
+    // this lane's weight rows (one per A tile; rows past the end load any row and are never stored):
+    // the matrix base is wave-uniform (gate for tiles 0, 1 and up for tiles 2, 3; down), the row a
+    // 32-bit chunk index
+    const uint8_t* const mA = GATEUP ? blob : blob + 2 * mb;
+    const uint8_t* const mB = GATEUP ? blob + mb : mA;
+    const size_t scale_off = size_t(rows_total) * nbk * 16;
+    uint32_t aoff[4];   // (row * nbk + lg): the chunk / scale index of block lg of stretch 0
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const int P = 512 * p + tid, t = P >> 2, blk = (P & 3) ^ ((t >> 2) & 3);
-        const uint8_t* m;
-        int r;
-        a_mat(t, m, r);
-        acode[p] = m + (size_t(r) * nbk + blk) * 16;
+    for (int i = 0; i < 4; ++i) {
+        const int t = GATEUP ? ((i < 2 ? 0 : kRows / 2) + 32 * wave + 16 * (i & 1) + li) : (64 * wave + 16 * i + li);
+        const int r = min(rbase + (GATEUP ? (t & (kRows / 2 - 1)) : t), rows_total - 1);
+        aoff[i] = uint32_t(r) * nbk + lg;
     }
+    // weights of stretch q (blocks 4q + lg) into a register set
+    struct ARegs {
+        uint4 cw[4];
+        uint32_t sc[4];
+    };
+    auto load_a = [&](int q, ARegs& a) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint8_t* m = i < 2 ? mA : mB;
+            a.cw[i] = gld_u4(m + (size_t(aoff[i]) + 4 * q) * 16);
+            a.sc[i] = gld<uint16_t>(m + scale_off + (size_t(aoff[i]) + 4 * q) * 2);
+        }
+    };
+    // this thread's activation chunks of a stage: LDS positions P = 512 p + tid (token P / 16)
+    uint32_t boff[2];   // element offsets (rows * Kd stays below 2^31)
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-        const int Q = 512 * p + tid, t = Q >> 1;
-        const uint8_t* m;
-        int r;
-        a_mat(t, m, r);
-        ascale[p] = m + size_t(rows_total) * nbk * 16 + size_t(r) * nbk * 2 + (Q & 1) * 4;
+        const int P = 512 * p + tid, j = P >> 4, kc = (P & 15) ^ (j & 15);
+        boff[p] = uint32_t(sRow[j]) * Kd + kc * 8;
     }
-    size_t boff;
-    {
-        const int j = tid >> 3, kc = (tid & 7) ^ (j & 7);
-        boff = size_t(sRow[j]) * Kd + kc * 8;
-    }
-    uint8_t* const sA = smem;                                   // [2][kSlotA + kSlotAs]
-    uint8_t* const sB = smem + 2 * (kSlotA + kSlotAs);         // [kStages][NP][kSlotB]
-    // the loads of stage u: A super-stage u / 4 first when u % 4 == 0, then u's B parts
-    auto issue = [&](int u) {
-        if (u % kSuper == 0) {
-            const int k = u / kSuper;
-            uint8_t* a = sA + (k & 1) * (kSlotA + kSlotAs);
+    auto issue_b = [&](int st, int slot) {
+        uint8_t* b = smem + slot * NP * kSlotB;
 #pragma unroll
-            for (int p = 0; p < 4; ++p) ldsdma16(acode[p] + size_t(u) * 16, a + p * 8192 + wave * 1024);
-#pragma unroll
-            for (int p = 0; p < 2; ++p) ldsdma4(ascale[p] + size_t(u) * 2, a + kSlotA + p * 2048 + wave * 256);
+        for (int p = 0; p < 2; ++p) {
+            ldsdma16(bhi + boff[p] + size_t(st) * kStageK, b + p * 8192 + wave * 1024);
+            if constexpr (NP == 2) ldsdma16(blo + boff[p] + size_t(st) * kStageK, b + kSlotB + p * 8192 + wave * 1024);
         }
-        uint8_t* b = sB + (u % kStages) * NP * kSlotB;
-        ldsdma16(bhi + boff + size_t(u) * kBlock, b + wave * 1024);
-        if constexpr (NP == 2) ldsdma16(blo + boff + size_t(u) * kBlock, b + kSlotB + wave * 1024);
+    };
+    auto read_b = [&](auto nc, int st, int t, half8 (&bv)[4][NP]) {   // K-step t (0..3) of stage st
+        constexpr int NC = decltype(nc)::value;
+        const half8* sb = reinterpret_cast<const half8*>(smem + (st % kStages) * NP * kSlotB);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int j = c * 16 + li, kc = t * 4 + lg;
+#pragma unroll
+            for (int part = 0; part < NP; ++part) {
+                bv[c][part] = sb[part * (kSlotB / 16) + j * 16 + (kc ^ (j & 15))];
+            }
+        }
     };
 
     floatx4 acc[4][4];
@@ -364,103 +375,72 @@ __global__ void __launch_bounds__(512) k_pf_gemm(const uint8_t* __restrict__ are
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[i][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int li = lane & 15, lg = lane >> 4;
-    int art[4];   // this lane's A row in the tile for each of its 4 A tiles
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        art[i] = GATEUP ? ((i < 2 ? 0 : kRows / 2) + 32 * wave + 16 * (i & 1) + li) : (64 * wave + 16 * i + li);
-    const int ncol = (cnt + 15) / 16;   // token columns with at least one real token
     const DqMagic mg = dq_magic();
 
-    // A stage's operands are read from LDS ahead of their use: the codes, scales and the first K-step's
-    // activation fragments one stage ahead (in flight while the stage before is multiplied), the
-    // second K-step's fragments at the start of the stage itself.
-    struct Ops {
-        uint32_t cw[4];
-        uint32_t sc[4];
-        half8 bv[4][NP];
-    };
-    auto read_b = [&](int st, int h, half8 (&bv)[4][NP]) {
-        const half8* sb = reinterpret_cast<const half8*>(sB + (st % kStages) * NP * kSlotB);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int j = c * 16 + li, kc = h * 4 + lg;
-#pragma unroll
-            for (int part = 0; part < NP; ++part) bv[c][part] = sb[part * (kSlotB / 16) + j * 8 + (kc ^ (j & 7))];
-        }
-    };
-    auto read_ops = [&](int st, Ops& o) {
-        const uint8_t* a = sA + ((st / kSuper) & 1) * (kSlotA + kSlotAs);
-        const uint32_t* sa = reinterpret_cast<const uint32_t*>(a);
-        const uint32_t* sas = reinterpret_cast<const uint32_t*>(a + kSlotA);
-        const int bq = st % kSuper;   // block within the super-stage
+    // K-step tt (0..7) of a stretch: dequantize the 4 A fragments, NC columns x NP parts x 4 tiles
+    auto mul = [&](auto nc, const ARegs& a, int tt, const half8(&bv)[4][NP]) {
+        constexpr int NC = decltype(nc)::value;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int r = art[i];
-            o.cw[i] = sa[(r * 4 + (bq ^ ((r >> 2) & 3))) * 4 + lg];
-            o.sc[i] = sas[r * 2 + (bq >> 1)] >> (16 * (bq & 1));
-        }
-        read_b(st, 0, o.bv);
-    };
-    // loads issued after stage st's: later stages' B parts and the A super-stages among them
-    auto wait_stage = [&](int st, int issued_to) {
-        int later = 0;
-        for (int u = st + 1; u < issued_to; ++u) later += NP + (u % kSuper == 0 ? kDA : 0);
-        wait_vm_dyn(later);
-    };
-    auto mul = [&](const uint32_t (&cw)[4], const uint32_t (&sc)[4], int h, const half8 (&bv)[4][NP]) {
-        half8 av[4];
+            const uint4 w = a.cw[i];
+            const int d = tt >> 1;
+            const uint32_t cw = d == 0 ? w.x : d == 1 ? w.y : d == 2 ? w.z : w.w;
+            const _Float16 s = __builtin_bit_cast(_Float16, uint16_t(a.sc[i]));
+            const half8 av = dequant8((tt & 1) ? cw >> 8 : cw, half2v{s, s}, mg);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const _Float16 d = __builtin_bit_cast(_Float16, uint16_t(sc[i]));
-            av[i] = dequant8(h ? cw[i] >> 8 : cw[i], half2v{d, d}, mg);
-        }
+            for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            if (c == 0 || c < ncol) {   // a tile has at least one token
-#pragma unroll
-                for (int part = 0; part < NP; ++part)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[i][c] = mfma_acc(av[i], bv[c][part], acc[i][c]);
-            }
+                for (int part = 0; part < NP; ++part) {
+                    acc[i][c] = mfma_acc(av, bv[c][part], acc[i][c]);
+                }
         }
     };
 
-    // B slot of stage u is refilled by stage u + kStages once every wave has read stage u (both
-    // K-steps), i.e. after the barrier of iteration u + 1
-    const int nstage = nbk;
-    int issued = min(kStages, nstage);   // stages issued so far (0 .. issued - 1)
-    for (int u = 0; u < issued; ++u) issue(u);
-    Ops cur;
-    wait_stage(0, issued);
-    ring_barrier();
-    read_ops(0, cur);
-    for (int sI = 0; sI < nstage; ++sI) {
-#ifdef FRT_PF_STAGE_PROBE
-        const int pk = (GATEUP && (sI == 12 || sI == 13)) ? sI - 10 : -1;
-#define SPROBE(i) do { if (pk >= 0) FRT_PROBE(pk, i); } while (0)
-#else
-#define SPROBE(i) do { } while (0)
-#endif
-        SPROBE(0);
-        half8 b1[4][NP];
-        read_b(sI, 1, b1);   // issued before the next stage's reads, so it completes first
-        Ops nxt;
-        if (sI + 1 < nstage) {
-            wait_stage(sI + 1, issued);   // stage sI + 1's loads are done
-            SPROBE(1);
-            ring_barrier();   // ... for every wave, and every wave's reads of stage sI - 1 are complete
-            SPROBE(2);
-            if (sI >= 1 && issued < nstage) issue(issued++);   // into stage sI - 1's slot
-            read_ops(sI + 1, nxt);
-            SPROBE(3);
+    // Stage st (K = 128 st ..) is stretch st / 2, K-steps 4 (st % 2) .. + 3. Per stage st, after its
+    // barrier: A stretch st / 2 + 1 (st even), then B stage st + 2. Waiting for B stage st (vmcnt:
+    // later loads may stay outstanding) covers everything issued before it, A stretch st / 2
+    // included (issued two stages earlier, just before B stage st). The pattern is
+    // the same for every stage: past the end, the last stretch / stage is loaded again (into
+    // registers / a slot nothing reads any more), so the wait counts are constants and the
+    // compiler's own waits for the weight registers never see a path without later loads (at such a
+    // merge it would wait for every load in flight).
+    const int nst = Kd / kStageK;   // a multiple of 4
+    const int nq = nst / 2;         // stretches (even)
+    auto run = [&](auto nc) {
+        ARegs a0, a1;   // stretches of even / odd index (named, so they stay in registers)
+        // the loads of stages -2, -1 of the steady-state pattern below
+        load_a(0, a0);
+        issue_b(0, 0);
+        issue_b(min(1, nst - 1), 1);
+        // the two stages of stretch q, whose weights are in cur; the next stretch loads into nxt
+        auto stretch = [&](int q, const ARegs& cur, ARegs& nxt) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int st = 2 * q + h;
+                // loads issued after B stage st: B stage st + 1, and A stretch q + 1 when h = 1
+                if (h == 0) wait_vm<kDB>();
+                else wait_vm<kDB + kDA>();
+                ring_barrier();   // stage st is in LDS for every wave; every wave is done with stage st - 1
+                if (h == 0) load_a(min(q + 1, nq - 1), nxt);
+                issue_b(min(st + 2, nst - 1), (st + 2) % kStages);   // into stage st - 1's slot
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    half8 bv[4][NP];
+                    read_b(nc, st, t, bv);   // the NC columns the tile uses
+                    mul(nc, cur, 4 * h + t, bv);
+                }
+            }
+        };
+        for (int q = 0; q < nq; q += 2) {   // nq is even
+            stretch(q, a0, a1);
+            stretch(q + 1, a1, a0);
         }
-        mul(cur.cw, cur.sc, 0, cur.bv);
-        SPROBE(4);
-        mul(cur.cw, cur.sc, 1, b1);
-        SPROBE(5);
-        cur = nxt;
-#undef SPROBE
+    };
+    switch ((cnt + 15) / 16) {   // token columns with at least one real token
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        case 3: run(std::integral_constant<int, 3>{}); break;
+        default: run(std::integral_constant<int, 4>{}); break;
     }
 
     FRT_PROBE(GATEUP ? 0 : 1, 1);
@@ -493,7 +473,7 @@ __global__ void __launch_bounds__(512) k_pf_gemm(const uint8_t* __restrict__ are
                     for (int q = 0; q < 4; ++q) {
                         const int f = fbase + 16 * i + 4 * lg + q;
                         const float a = float(q8_code(hv[i][q], id)) * dr;
-                        hout[row * ff + (f & ~63) + perm64_pos(f & 63)] = _Float16(a);
+                        hout[row * ff + (f & ~255) + perm256_pos(f & 255)] = _Float16(a);
                     }
             }
         }
@@ -621,8 +601,8 @@ int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16
 
 int pf_check(int T, int K, int n, int ff, int E) {
     if (T < 1 || K < 1 || K > 32 || E < 1 || E > 4096 || K > E) return set_error(kErrShape, "prefill: T=%d K=%d E=%d", T, K, E);
-    if (n % 256 || ff % 256 || n < 256 || ff < 256)   // whole A super-stages of 4 blocks
-        return set_error(kErrShape, "prefill: n=%d ff=%d (n and ff multiples of 256)", n, ff);
+    if (n % 512 || ff % 512 || n < 512 || ff < 512)   // whole pairs of 256-element weight stretches
+        return set_error(kErrShape, "prefill: n=%d ff=%d (n and ff multiples of 512)", n, ff);
     return kOk;
 }
 

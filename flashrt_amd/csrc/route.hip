@@ -137,7 +137,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, in
 
 // ---- Q8_0 of activations: one wave per 2 blocks of 32 (quant/q2_0/q2_0.cpp:93-108).
 // xq int8 [rows][n] natural order, xd [rows][n/32]. With xhi (and xlo): the activations a = q * d as
-// fp16 in the prefill GEMM's operand order (perm64_pos), [rows][n]: xhi = fp16(a) and
+// fp16 in the prefill GEMM's operand order (perm256_pos), [rows][n]: xhi = fp16(a) and
 // xlo = fp16(a - xhi), an exact pair (a has at most 7 + 11 significant bits).
 __global__ void k_quant_q8(const float* __restrict__ x, int n_blocks, int8_t* __restrict__ xq, float* __restrict__ xd,
                            _Float16* __restrict__ xhi, _Float16* __restrict__ xlo, int n) {
@@ -157,7 +157,8 @@ __global__ void k_quant_q8(const float* __restrict__ x, int n_blocks, int8_t* __
     const float dr = f16_round(d);
     if (xd && j == 0) xd[blk] = dr;
     if (xhi) {
-        const size_t pos = size_t(blk >> 1) * kBlock + perm64_pos((blk & 1) * 32 + j);
+        const size_t e = size_t(blk) * kQ8 + j;   // element index in the row-major [rows][n]
+        const size_t pos = (e & ~size_t(255)) + perm256_pos(int(e & 255));
         const float a = float(q) * dr;
         const _Float16 hi = _Float16(a);
         xhi[pos] = hi;
