@@ -72,23 +72,66 @@ __device__ __forceinline__ int block_excl_scan(int v, int* total, int* ws) {
 }
 
 // 1024 threads. cnt [nchunk][E] becomes each chunk's first row per expert (absolute).
+// Tiles are listed longest first (4 token columns of 16, then 3, 2, 1; by expert within a class),
+// so that the grouped GEMMs start the long tiles first and finish on short ones.
+__device__ __forceinline__ int tile_class(int rows) { return (rows + 15) / 16; }   // 1..4
+
 __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int nchunk, int E, int T, int K, int shared,
                                                   int32_t* __restrict__ bounds, int2* __restrict__ tiles,
                                                   int32_t* __restrict__ n_tiles) {
     __shared__ int ws[17];
-    int run_rows = 0, run_tiles = 0;
+    // tiles of each class of group e (rows c): c / 64 full tiles (class 4) and one of class (c % 64)
+    auto count = [&](int c, int (&n)[5]) {
+        n[1] = n[2] = n[3] = n[4] = 0;
+        n[4] = c / kTN;
+        if (c % kTN) ++n[tile_class(c % kTN)];
+    };
+    auto group_rows = [&](int e) {
+        int c = 0;
+        for (int b = 0; b < nchunk; ++b) c += cnt[size_t(b) * E + e];
+        return c;
+    };
+    // pass 1: tiles per class over all groups (the shared group E included)
+    int total[5] = {0, 0, 0, 0, 0};
     for (int e0 = 0; e0 < E; e0 += blockDim.x) {
         const int e = e0 + threadIdx.x;
-        int c = 0;
-        if (e < E)
-            for (int b = 0; b < nchunk; ++b) c += cnt[size_t(b) * E + e];
-        int tot_rows, tot_tiles;
+        int n[5];
+        count(e < E ? group_rows(e) : 0, n);
+        for (int k = 1; k <= 4; ++k) {
+            int tot;
+            block_excl_scan(n[k], &tot, ws);
+            total[k] += tot;
+        }
+    }
+    int sh[5] = {0, 0, 0, 0, 0};
+    if (shared) {
+        count(T, sh);
+        for (int k = 1; k <= 4; ++k) total[k] += sh[k];
+    }
+    int base[5];   // first tile of each class
+    base[4] = 0;
+    for (int k = 3; k >= 1; --k) base[k] = base[k + 1] + total[k + 1];
+    // pass 2: bounds, chunk offsets for k_pf_place, and the tiles
+    int run_rows = 0;
+    for (int e0 = 0; e0 < E; e0 += blockDim.x) {
+        const int e = e0 + threadIdx.x;
+        const int c = e < E ? group_rows(e) : 0;
+        int tot_rows;
         const int off = block_excl_scan(c, &tot_rows, ws) + run_rows;
-        const int nt = (c + kTN - 1) / kTN;
-        const int toff = block_excl_scan(nt, &tot_tiles, ws) + run_tiles;
+        int n[5], at[5];
+        count(c, n);
+        for (int k = 1; k <= 4; ++k) {
+            int tot;
+            at[k] = block_excl_scan(n[k], &tot, ws) + base[k];
+            base[k] += tot;
+        }
         if (e < E) {
             bounds[e] = off;
-            for (int i = 0; i < nt; ++i) tiles[toff + i] = make_int2(e, i * kTN);
+            for (int i = 0; i < c / kTN; ++i) tiles[at[4] + i] = make_int2(e, i * kTN);
+            if (c % kTN) {
+                const int k = tile_class(c % kTN);
+                tiles[at[k] + (k == 4 ? n[4] - 1 : 0)] = make_int2(e, (c / kTN) * kTN);
+            }
             int run = off;
             for (int b = 0; b < nchunk; ++b) {
                 const int x = cnt[size_t(b) * E + e];
@@ -97,16 +140,18 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
             }
         }
         run_rows += tot_rows;
-        run_tiles += tot_tiles;
     }
     if (threadIdx.x == 0) {
         bounds[E] = run_rows;   // = T * K
-        int nt = run_tiles;
         if (shared) {
             bounds[E + 1] = run_rows + T;
-            for (int j = 0; j < T; j += kTN) tiles[nt++] = make_int2(E, j);
+            for (int i = 0; i < T / kTN; ++i) tiles[base[4] + i] = make_int2(E, i * kTN);
+            if (T % kTN) {
+                const int k = tile_class(T % kTN);
+                tiles[base[k] + (k == 4 ? sh[4] - 1 : 0)] = make_int2(E, (T / kTN) * kTN);
+            }
         }
-        *n_tiles = nt;
+        *n_tiles = total[1] + total[2] + total[3] + total[4];
     }
 }
 
@@ -494,6 +539,138 @@ __global__ void __launch_bounds__(512) k_pf_gemm(const uint8_t* __restrict__ are
     FRT_PROBE_END();
 }
 
+// k_pf_down: the down GEMM, one workgroup per tile. The tile's activations (h of 64 dispatched rows,
+// all of K = ff, perm256 order) are loaded into LDS once (64 tokens x ff fp16; chunk kc of token j
+// at j * ff / 8 + (kc ^ (j & 15))), then the workgroup walks all n output rows in blocks of 512
+// (wave w: rows 64 w + 16 i + li of the block), streaming the weights straight into registers with
+// three stretches of lookahead (four register sets). No barrier after the activation load: each
+// wave reads only its own weights. NQ = ff / 256 stretches per row block.
+template <int NQ>
+__global__ void __launch_bounds__(512) k_pf_down(const uint8_t* __restrict__ arena, size_t stride, int E,
+                                                 const uint8_t* __restrict__ shared_blob, int n,
+                                                 const _Float16* __restrict__ h, const int32_t* __restrict__ bounds,
+                                                 const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
+                                                 float* __restrict__ yd, const int32_t* __restrict__ slot_of) {
+    constexpr int ff = NQ * 256;
+    constexpr int nbk = ff / kBlock;   // weight blocks per row
+    constexpr int cpt = ff / 8;        // 16-byte activation chunks per token
+    constexpr int kDB = kTN * cpt / 512;   // activation loads per lane
+    if (int(blockIdx.y) >= *n_tiles) return;
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int sRow[kTN];
+    FRT_PROBE_BEGIN();
+    FRT_PROBE(1, 0);
+    const int2 tile = tiles[blockIdx.y];
+    const int grp = tile.x;
+    const int row0 = bounds[grp] + tile.y;
+    const int cnt = min(kTN, bounds[grp + 1] - row0);
+    const uint8_t* blob = grp < E ? arena + size_t(grp) * stride : shared_blob;
+    const uint8_t* const md = blob + 2 * mat_bytes(ff, n);   // down [n][ff]
+    const size_t scale_off = size_t(n) * nbk * 16;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int li = lane & 15, lg = lane >> 4;
+    if (tid < kTN) sRow[tid] = row0 + min(tid, cnt - 1);   // past the group's end: repeat a row
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < kDB; ++p) {
+        const int P = 512 * p + tid, j = P / cpt, kc = (P % cpt) ^ (j & 15);
+        ldsdma16(h + size_t(sRow[j]) * ff + kc * 8, smem + P * 16 - lane * 16);
+    }
+
+    uint32_t aoff[4];   // chunk index of block lg of stretch 0 of row block 0 for tile i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) aoff[i] = uint32_t(64 * wave + 16 * i + li) * nbk + lg;
+    struct ARegs {
+        uint4 cw[4];
+        uint32_t sc[4];
+    };
+    const int nsx = (n / 512) * NQ;   // stretches in all (a multiple of 4: n % 1024 == 0)
+    auto load_a = [&](int s, ARegs& a) {   // stretch s: row block s / NQ, blocks 4 (s % NQ) + lg
+        const size_t base = size_t(s / NQ) * 512 * nbk + 4 * (s % NQ);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a.cw[i] = gld_u4(md + (base + aoff[i]) * 16);
+            a.sc[i] = gld<uint16_t>(md + scale_off + (base + aoff[i]) * 2);
+        }
+    };
+    const DqMagic mg = dq_magic();
+
+    size_t yslot[4];   // yd row of this lane's token column c (loaded before the weight stream)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) yslot[c] = size_t(slot_of[row0 + min(c * 16 + li, cnt - 1)]) * n;
+    auto run = [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+        ARegs a0, a1, a2, a3;
+        floatx4 acc[4][NC];
+        load_a(0, a0);
+        load_a(min(1, nsx - 1), a1);
+        load_a(min(2, nsx - 1), a2);
+        wait_vm<3 * 8>();   // the activations (issued first) are in LDS for this wave ...
+        __syncthreads();    // ... and for every wave
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc[i][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        const half8* sb = reinterpret_cast<const half8*>(smem);
+        // stretch s with weights in cur; the stretch three ahead loads into nxt (the last one again
+        // past the end, so every stretch has the same loads in flight)
+        auto step = [&](int s, int q, const ARegs& cur, ARegs& nxt) {
+            load_a(min(s + 3, nsx - 1), nxt);
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) {
+                half8 bv[4];
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const int j = c * 16 + li, kc = (q * 8 + tt) * 4 + lg;
+                    bv[c] = sb[j * cpt + (kc ^ (j & 15))];
+                }
+                const int d = tt >> 1;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint4 w = cur.cw[i];
+                    const uint32_t cw = d == 0 ? w.x : d == 1 ? w.y : d == 2 ? w.z : w.w;
+                    const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(cur.sc[i]));
+                    const half8 av = dequant8((tt & 1) ? cw >> 8 : cw, half2v{sc, sc}, mg);
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) acc[i][c] = mfma_acc(av, bv[c], acc[i][c]);
+                }
+                __builtin_amdgcn_sched_barrier(0);   // one K-step of operands live at a time
+            }
+            if (q == NQ - 1) {   // row block s / NQ done: yd[slot][row], then a fresh block
+                const int rb = s / NQ;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    if (c * 16 + li < cnt) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int r = rb * 512 + 64 * wave + 16 * i + 4 * lg;
+                            *reinterpret_cast<float4*>(yd + yslot[c] + r) =
+                                make_float4(acc[i][c][0], acc[i][c][1], acc[i][c][2], acc[i][c][3]);
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[i][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
+        };
+        for (int s = 0; s < nsx; s += 4) {
+            step(s, 0 % NQ, a0, a3);
+            step(s + 1, 1 % NQ, a1, a0);
+            step(s + 2, 2 % NQ, a2, a1);
+            step(s + 3, 3 % NQ, a3, a2);
+        }
+    };
+    switch ((cnt + 15) / 16) {   // token columns with at least one real token
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        case 3: run(std::integral_constant<int, 3>{}); break;
+        default: run(std::integral_constant<int, 4>{}); break;
+    }
+    FRT_PROBE(1, 1);
+    FRT_PROBE(1, 2);
+    FRT_PROBE_END();
+}
+
 // ---------------------------------------------------------------- combine
 
 // out[t][i] = sum over the token's K slots in ascending expert id of w * yd (+ shared * sigmoid(g));
@@ -601,8 +778,10 @@ int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16
 
 int pf_check(int T, int K, int n, int ff, int E) {
     if (T < 1 || K < 1 || K > 32 || E < 1 || E > 4096 || K > E) return set_error(kErrShape, "prefill: T=%d K=%d E=%d", T, K, E);
-    if (n % 512 || ff % 512 || n < 512 || ff < 512)   // whole pairs of 256-element weight stretches
-        return set_error(kErrShape, "prefill: n=%d ff=%d (n and ff multiples of 512)", n, ff);
+    // gate/up: whole pairs of 256-element weight stretches; down: the tile's h in LDS (ff <= 1024),
+    // weight stretches in fours
+    if (n % 1024 || n < 1024 || (ff != 512 && ff != 1024))
+        return set_error(kErrShape, "prefill: n=%d ff=%d (n a multiple of 1024; ff 512 or 1024)", n, ff);
     return kOk;
 }
 
@@ -617,19 +796,36 @@ static int pf_gemm_attr() {
     return kOk;
 }
 
-// The two grouped GEMMs (k_pf_gemm): gate/up on the exact x pairs, SwiGLU and Q8_0 of h in the
-// epilogue; down on h -> fp32 yd per slot.
+template <int NQ>
+static int pf_down_attr(size_t lds) {
+    static bool done = false;
+    if (!done) {
+        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_down<NQ>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+        done = true;
+    }
+    return kOk;
+}
+
+// The two grouped GEMMs: gate/up (k_pf_gemm) on the exact x pairs, SwiGLU and Q8_0 of h in the
+// epilogue; down (k_pf_down) on h -> fp32 yd per slot.
 static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, int n, int ff,
                            const PfWs& w, int mt, float* ydf, hipStream_t stream) {
     if (int rc = pf_gemm_attr<true>()) return rc;
-    if (int rc = pf_gemm_attr<false>()) return rc;
     k_pf_gemm<true><<<dim3((ff + kRows / 2 - 1) / (kRows / 2), mt), 512, smem_bytes<2>(), stream>>>(
         arena, stride, E, shared_blob, n, ff, w.xhi, w.xlo, w.tok_of, w.bounds, w.tiles, w.n_tiles, w.h16, nullptr,
         nullptr);
     timing_mark(stream, "pf_gateup");
-    k_pf_gemm<false><<<dim3((n + kRows - 1) / kRows, mt), 512, smem_bytes<1>(), stream>>>(
-        arena, stride, E, shared_blob, n, ff, w.h16, nullptr, w.tok_of, w.bounds, w.tiles, w.n_tiles, nullptr, ydf,
-        w.slot_of);
+    const size_t down_lds = size_t(kTN) * ff * 2;   // the tile's activations
+    if (ff == 512) {
+        if (int rc = pf_down_attr<2>(down_lds)) return rc;
+        k_pf_down<2><<<dim3(1, mt), 512, down_lds, stream>>>(arena, stride, E, shared_blob, n, w.h16, w.bounds,
+                                                            w.tiles, w.n_tiles, ydf, w.slot_of);
+    } else {
+        if (int rc = pf_down_attr<4>(down_lds)) return rc;
+        k_pf_down<4><<<dim3(1, mt), 512, down_lds, stream>>>(arena, stride, E, shared_blob, n, w.h16, w.bounds,
+                                                            w.tiles, w.n_tiles, ydf, w.slot_of);
+    }
     return kOk;
 }
 
