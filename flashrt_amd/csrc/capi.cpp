@@ -28,21 +28,36 @@ namespace {
 struct Timing {
     bool on = false;
     std::vector<hipEvent_t> pool;
+    size_t used = 0;   // events of the pool handed out since frt_timing_begin
     std::vector<std::pair<std::string, hipEvent_t>> marks;
+    std::vector<std::pair<std::string, std::pair<hipEvent_t, hipEvent_t>>> kernels;   // start / stop at the kernel
+    hipEvent_t take() {
+        if (used == pool.size()) {
+            hipEvent_t e;
+            if (hipEventCreate(&e) != hipSuccess) return nullptr;
+            pool.push_back(e);
+        }
+        return pool[used++];
+    }
 };
 Timing g_timing;
 }  // namespace
 
+bool timing_events(const char* kernel, hipEvent_t* start, hipEvent_t* stop) {
+    Timing& t = g_timing;
+    if (!t.on) return false;
+    *start = t.take();
+    *stop = t.take();
+    if (!*start || !*stop) return false;
+    t.kernels.push_back({kernel, {*start, *stop}});
+    return true;
+}
+
 void timing_mark(hipStream_t stream, const char* kernel) {
     Timing& t = g_timing;
     if (!t.on) return;
-    if (t.marks.size() == t.pool.size()) {
-        hipEvent_t e;
-        if (hipEventCreate(&e) != hipSuccess) return;
-        t.pool.push_back(e);
-    }
-    hipEvent_t e = t.pool[t.marks.size()];
-    if (hipEventRecord(e, stream) != hipSuccess) return;
+    hipEvent_t e = t.take();
+    if (!e || hipEventRecord(e, stream) != hipSuccess) return;
     t.marks.emplace_back(kernel, e);
 }
 
@@ -147,10 +162,13 @@ const char* frt_last_error(void) { return g_err; }
 void frt_timing_begin(void) {
     g_timing.on = true;
     g_timing.marks.clear();
+    g_timing.kernels.clear();
+    g_timing.used = 0;
 }
 
 // Durations between consecutive marks of one stream's launches, summed per kernel name (a mark
-// named "begin" opens each call). Writes up to max entries; returns the number of kernel names.
+// named "begin" opens each call); kernels launched with their own start / stop events report those
+// instead. Writes up to max entries; returns the number of kernel names.
 int frt_timing_end(char* names, int name_len, double* total_ms, int* launches, int max) {
     Timing& t = g_timing;
     t.on = false;
@@ -166,6 +184,17 @@ int frt_timing_end(char* names, int name_len, double* total_ms, int* launches, i
         acc[k].first += ms;
         acc[k].second += 1;
     }
+    // kernels with events of their own: their start-to-stop times replace the intervals
+    std::map<std::string, std::pair<double, int>> own;
+    for (const auto& ke : t.kernels) {
+        FRT_HIP(hipEventSynchronize(ke.second.second));
+        float ms = 0.0f;
+        FRT_HIP(hipEventElapsedTime(&ms, ke.second.first, ke.second.second));
+        own[ke.first].first += ms;
+        own[ke.first].second += 1;
+        if (!acc.count(ke.first)) order.push_back(ke.first);
+    }
+    for (const auto& o : own) acc[o.first] = o.second;
     int n = 0;
     for (const auto& k : order) {
         if (n >= max) break;
@@ -175,6 +204,8 @@ int frt_timing_end(char* names, int name_len, double* total_ms, int* launches, i
         ++n;
     }
     t.marks.clear();
+    t.kernels.clear();
+    t.used = 0;
     return n;
 }
 const char* frt_version(void) { return "flashrt-mi355x 0.1 (gfx950)"; }

@@ -7,6 +7,7 @@
 // gate [ff][n] | up [ff][n] | down [n][ff].
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -62,6 +63,19 @@ int set_error(int code, const char* fmt, ...);
 // launch stream; frt_timing_end() turns consecutive events into per-kernel durations. Not for use
 // under graph capture.
 void timing_mark(hipStream_t stream, const char* kernel);
+// Kernels launched through launch_timed() also get start/stop events recorded at the kernel itself
+// (hipExtLaunchKernelGGL) while timing is on; frt_timing_end() reports those for the kernel's name,
+// which excludes the dispatch gap that an interval between two recorded events also contains.
+bool timing_events(const char* kernel, hipEvent_t* start, hipEvent_t* stop);
+template <typename K, typename... Args>
+inline void launch_timed(const char* name, K kernel, dim3 grid, dim3 block, size_t shm, hipStream_t stream,
+                         Args... args) {
+    hipEvent_t s, e;
+    if (timing_events(name, &s, &e))
+        hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(shm), stream, s, e, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, uint32_t(shm), stream, args...);
+}
 
 inline size_t up256(size_t x) { return (x + 255) & ~size_t(255); }
 

@@ -740,11 +740,11 @@ static int dec_down(const DecScratch& s, int n, int ff, int T, int K, const floa
 #define FRT_DN(NBFV)                                                                                           \
     case NBFV:                                                                                                 \
         if (yh)                                                                                                \
-            k_dec_down<NBFV, true><<<n / 8, 256, smem, stream>>>(s.ent, s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid,  \
-                                                                 out, yh, U_max, S, pf, pf_rows);               \
+            launch_timed("dec_down", k_dec_down<NBFV, true>, dim3(n / 8), dim3(256), smem, stream, s.ent, s.n_ent, \
+                         s.comb, s.hq, s.hd, n, ff, T, K, resid, out, yh, U_max, S, pf, pf_rows);                   \
         else                                                                                                   \
-            k_dec_down<NBFV, false><<<n / 8, 256, smem, stream>>>(s.ent, s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid, \
-                                                                  out, yh, U_max, S, pf, pf_rows);              \
+            launch_timed("dec_down", k_dec_down<NBFV, false>, dim3(n / 8), dim3(256), smem, stream, s.ent,       \
+                         s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid, out, yh, U_max, S, pf, pf_rows);          \
         break;
     switch (nbf) {
         FRT_DN(4) FRT_DN(8) FRT_DN(10) FRT_DN(16)
@@ -774,10 +774,14 @@ int dec_moe(const float* logits, const float* gate, int T, int E, int K, const u
     const int nb = n / kBlock;
     dim3 g1(ff / 32, T * K + 1);
 #define FRT_RG(NBV, VV)                                                                                         \
-    if (T == 1) k_dec_route_gateup<NBV, VV, 1><<<g1, 1024, 0, stream>>>(logits, gate, T, E, K, arena, stride, shared_blob, xq, xd, \
-                                                        n, ff, s.hq, s.hd, s.ent, s.n_ent, s.comb, ids, wts, counts); \
-    else k_dec_route_gateup<NBV, VV, kDecMaxT><<<g1, 1024, 0, stream>>>(logits, gate, T, E, K, arena, stride, shared_blob, xq, xd, \
-                                                        n, ff, s.hq, s.hd, s.ent, s.n_ent, s.comb, ids, wts, counts)
+    if (T == 1)                                                                                                 \
+        launch_timed("dec_route_gateup", k_dec_route_gateup<NBV, VV, 1>, g1, dim3(1024), 0, stream, logits, gate, T, \
+                     E, K, arena, stride, shared_blob, xq, xd, n, ff, s.hq, s.hd, s.ent, s.n_ent, s.comb, ids, wts,    \
+                     counts);                                                                                   \
+    else                                                                                                        \
+        launch_timed("dec_route_gateup", k_dec_route_gateup<NBV, VV, kDecMaxT>, g1, dim3(1024), 0, stream, logits,  \
+                     gate, T, E, K, arena, stride, shared_blob, xq, xd, n, ff, s.hq, s.hd, s.ent, s.n_ent, s.comb, ids, \
+                     wts, counts)
 #define FRT_RGN(NBV)                       \
     case NBV:                              \
         if (E <= 512) FRT_RG(NBV, 8);      \

@@ -812,19 +812,22 @@ static int pf_down_attr(size_t lds) {
 static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, int n, int ff,
                            const PfWs& w, int mt, float* ydf, hipStream_t stream) {
     if (int rc = pf_gemm_attr<true>()) return rc;
-    k_pf_gemm<true><<<dim3((ff + kRows / 2 - 1) / (kRows / 2), mt), 512, smem_bytes<2>(), stream>>>(
-        arena, stride, E, shared_blob, n, ff, w.xhi, w.xlo, w.tok_of, w.bounds, w.tiles, w.n_tiles, w.h16, nullptr,
-        nullptr);
+    launch_timed("pf_gateup", k_pf_gemm<true>, dim3((ff + kRows / 2 - 1) / (kRows / 2), mt), dim3(512),
+                 smem_bytes<2>(), stream, arena, stride, E, shared_blob, n, ff, (const _Float16*)w.xhi,
+                 (const _Float16*)w.xlo, (const int32_t*)w.tok_of, (const int32_t*)w.bounds, (const int2*)w.tiles,
+                 (const int32_t*)w.n_tiles, w.h16, (float*)nullptr, (const int32_t*)nullptr);
     timing_mark(stream, "pf_gateup");
     const size_t down_lds = size_t(kTN) * ff * 2;   // the tile's activations
     if (ff == 512) {
         if (int rc = pf_down_attr<2>(down_lds)) return rc;
-        k_pf_down<2><<<dim3(1, mt), 512, down_lds, stream>>>(arena, stride, E, shared_blob, n, w.h16, w.bounds,
-                                                            w.tiles, w.n_tiles, ydf, w.slot_of);
+        launch_timed("pf_down", k_pf_down<2>, dim3(1, mt), dim3(512), down_lds, stream, arena, stride, E, shared_blob,
+                     n, (const _Float16*)w.h16, (const int32_t*)w.bounds, (const int2*)w.tiles,
+                     (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of);
     } else {
         if (int rc = pf_down_attr<4>(down_lds)) return rc;
-        k_pf_down<4><<<dim3(1, mt), 512, down_lds, stream>>>(arena, stride, E, shared_blob, n, w.h16, w.bounds,
-                                                            w.tiles, w.n_tiles, ydf, w.slot_of);
+        launch_timed("pf_down", k_pf_down<4>, dim3(1, mt), dim3(512), down_lds, stream, arena, stride, E, shared_blob,
+                     n, (const _Float16*)w.h16, (const int32_t*)w.bounds, (const int2*)w.tiles,
+                     (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of);
     }
     return kOk;
 }
@@ -878,7 +881,8 @@ int pf_moe(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blo
     const PfWs w = pf_carve(ws, T, K, n, ff, E, true, true);
     if (w.bytes > ws_bytes) return set_error(kErrWorkspace, "prefill: workspace %zu < %zu", ws_bytes, w.bytes);
     if (int rc = pf_experts(arena, stride, E, shared_blob, n, ff, x, ids, T, K, w.yd, 0, w, stream)) return rc;
-    k_pf_combine<float><<<dim3((n + 1023) / 1024, T), 256, 0, stream>>>(w.yd, ids, wts, gate, T, K, n, 1, resid, out);
+    launch_timed("pf_combine", k_pf_combine<float>, dim3((n + 1023) / 1024, T), dim3(256), 0, stream,
+                 (const float*)w.yd, ids, wts, gate, T, K, n, 1, resid, out);
     timing_mark(stream, "pf_combine");
     FRT_LAUNCHED("prefill combine");
     return kOk;

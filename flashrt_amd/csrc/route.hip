@@ -212,7 +212,8 @@ int router_logits(const float* x, int T, const float* W, const float* bias, cons
         if (smem > 65536)                                                                                        \
             FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_router<LL>),                            \
                                         hipFuncAttributeMaxDynamicSharedMemorySize, int(smem)));                 \
-        k_router<LL><<<grid, 64 * wg_rows, smem, stream>>>(x, T, W, bias, gate_w, E, logits, gate, TT, tok_per_wg, norm, xq, xd); \
+        launch_timed("router_quant", k_router<LL>, grid, dim3(64 * wg_rows), smem, stream, x, T, W, bias, gate_w, E, \
+                     logits, gate, TT, tok_per_wg, norm, xq, xd);                                                    \
         break;
     switch (L) {
         FRT_ROUTER_L(8) FRT_ROUTER_L(16) FRT_ROUTER_L(24) FRT_ROUTER_L(32) FRT_ROUTER_L(40) FRT_ROUTER_L(48)
@@ -243,7 +244,7 @@ int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16
     if (rows < 1 || n % 64) return set_error(kErrShape, "quantize_q8: n=%d not a multiple of 64", n);
     const int nb = rows * (n / kQ8);
     const int waves = (nb + 1) / 2;
-    k_quant_q8<<<(waves + 3) / 4, 256, 0, stream>>>(x, nb, xq, xd, xhi, xlo, n);
+    launch_timed("pf_quant_x", k_quant_q8, dim3((waves + 3) / 4), dim3(256), 0, stream, x, nb, xq, xd, xhi, xlo, n);
     FRT_LAUNCHED("quantize_q8");
     return kOk;
 }
