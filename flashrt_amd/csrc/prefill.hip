@@ -151,7 +151,8 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
                 tiles[base[k] + (k == 4 ? sh[4] - 1 : 0)] = make_int2(E, (T / kTN) * kTN);
             }
         }
-        *n_tiles = total[1] + total[2] + total[3] + total[4];
+        n_tiles[0] = total[1] + total[2] + total[3] + total[4];
+        n_tiles[1] = total[2] + total[3] + total[4];   // the one-column tiles come last
     }
 }
 
@@ -213,32 +214,47 @@ __global__ void k_pf_place_shared(int T, int K, int32_t* __restrict__ tok_of, in
 // Codes 4..7 of each half are shifted down by 8 first. Per pair of weights: one v_and_or_b32,
 // one v_pk_add_f16 and one v_pk_mul_f16 (plus one shift per 16 weights).
 //
-// Workgroup: 512 threads (8 waves), 64 tokens x 512 A rows; each wave owns 4 A tiles of 16 rows
-// and all 4 token columns of 16, so every activation fragment read from LDS feeds 4 MFMAs and
-// every dequantized weight fragment up to 4 NP.
-//   gate+up: A rows 0..255 are gate rows f0 + 0..255, A rows 256..511 the same up rows; wave w owns
-//            ff rows f0 + 32 w .. +31 (gate and up). Epilogue: SwiGLU, Q8_0 of the 32-row block of h
-//            (quant/q2_0/moe_cpu.cpp:43-61), h = code * d written as fp16 for the down GEMM.
-//   down:    A rows are output rows r0 + 0..511, wave w owns r0 + 64 w .. +63; yd[slot][row] fp32.
+// k_pf_gemm<SMALL>: the gate/up GEMM. A tile's A rows are ff rows f0 .. of gate and the same rows of
+// up; wave w owns 32 of them (2 gate + 2 up tiles of 16), so SwiGLU and the Q8_0 of a 32-row block
+// of h (quant/q2_0/moe_cpu.cpp:43-61) are lane-local; h = code * d is written as fp16 for the down
+// GEMM. Two shapes:
+//   SMALL = false: 256 threads (4 waves), 64 tokens x 128 ff rows, activation stages of K = 64 (a
+//                  48 KB ring), so two workgroups share a CU and one computes while the other waits
+//                  for its loads; the tile classes of 2-4 token columns (one branch-free variant per
+//                  column count).
+//   SMALL = true:  256 threads, 16 tokens x 128 ff rows, stages of K = 128, for the tiles of one
+//                  token column (half of them under skewed routing): a quarter of the LDS and of the
+//                  registers, so 4 workgroups share a CU.
+// Every activation fragment read from LDS feeds 4 MFMAs, every dequantized weight fragment NC NP.
 //
 // K order (perm256_pos): within each 256-element stretch, MFMA lane group g takes block g of the
 // stretch. So the weights go straight from HBM into registers: lane (row i, group g) loads the
 // 16-byte code chunk of block g of its row, and the 4 lanes of a row read 64 contiguous bytes (a
-// weight row is a separate 512-byte (gate/up) or 128-byte (down) stretch of HBM; one lane per row
-// and 16-byte chunk would make every lane a separate cache-line request). Each wave loads only
-// its own rows, one stretch ahead, into a second register set.
+// weight row is a separate 512-byte stretch of HBM; one lane per row and 16-byte chunk would make
+// every lane a separate cache-line request). Each wave loads only its own rows, one stretch ahead,
+// into a second register set.
 //
-// Activations go through LDS: stages of 128 K (half a stretch) in a ring of kStages slots filled by
+// Activations go through LDS: stages of 64 or 128 K in a ring of kStages slots filled by
 // direct global-to-LDS loads (global_load_lds: each lane's 16 bytes land at the wave's LDS base +
 // 16 lane, no registers), issued two stages ahead; one workgroup barrier per stage. Slot layout:
-//   [NP][64 tokens][16 chunks of 8 fp16], chunk kc of token j at j * 16 + (kc ^ (j & 15)), so that
-//   the lanes of a 128-bit read phase (one chunk of 8 or 16 tokens) hit distinct bank groups.
-constexpr int kRows = 512;    // A rows per workgroup
+//   [NP][tokens][cpt chunks of 8 fp16], chunk kc of token j at j * cpt + (kc ^ (j % cpt)), so that the
+//   lanes of a 128-bit read phase (one chunk of 8 tokens) hit distinct bank groups.
 constexpr int kStages = 3;    // activation ring slots (stages issued kStages - 1 ahead)
-constexpr int kStageK = 128;  // K per activation stage
-constexpr int kSlotB = kTN * kStageK * 2;   // bytes per part per slot
-template <int NP>
-constexpr int smem_bytes() { return kStages * NP * kSlotB; }
+template <bool SMALL>
+struct GuShape {
+    static constexpr int threads = 256;
+    static constexpr int tokens = SMALL ? 16 : kTN;       // activation rows in LDS
+    static constexpr int ff_rows = threads / 2;           // ff rows per workgroup (32 per wave)
+    static constexpr int stage_k = SMALL ? 128 : 64;      // K per activation stage
+    static constexpr int sps = 256 / stage_k;             // stages per weight stretch
+    static constexpr int ksps = stage_k / 32;             // MFMA K-steps per stage
+    static constexpr int cpt = stage_k / 8;               // 16-byte chunks per token per stage
+    static constexpr int slot_b = tokens * stage_k * 2;   // bytes per part per slot
+    static constexpr int smem = kStages * 2 * slot_b;
+    static constexpr int dma = tokens * cpt / threads;    // activation loads per lane per part
+    static constexpr int min_waves = SMALL ? 4 : 2;       // per SIMD (SMALL: 4 workgroups per CU)
+};
+
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
@@ -328,90 +344,90 @@ __device__ __forceinline__ floatx4 mfma_acc(half8 a, half8 b, floatx4 c) {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-template <bool GATEUP>
-__global__ void __launch_bounds__(512) k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E,
-                                                 const uint8_t* __restrict__ shared_blob, int n, int ff,
-                                                 const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
-                                                 const int32_t* __restrict__ tok_of, const int32_t* __restrict__ bounds,
-                                                 const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-                                                 _Float16* __restrict__ hout,
-                                                 float* __restrict__ yd, const int32_t* __restrict__ slot_of) {
-    constexpr int NP = GATEUP ? 2 : 1;
-    constexpr int kDB = 2 * NP;   // direct loads per lane per activation stage
-    constexpr int kDA = 8;        // weight loads per lane per stretch (4 code chunks + 4 scales)
-    if (int(blockIdx.y) >= *n_tiles) return;
+template <bool SMALL>
+__global__ void __launch_bounds__(GuShape<SMALL>::threads, GuShape<SMALL>::min_waves)
+k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t* __restrict__ shared_blob, int n,
+          int ff, const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
+          const int32_t* __restrict__ tok_of, const int32_t* __restrict__ bounds, const int2* __restrict__ tiles,
+          const int32_t* __restrict__ n_tiles, _Float16* __restrict__ hout) {
+    using Sh = GuShape<SMALL>;
+    constexpr int NP = 2;
+    constexpr int kDB = Sh::dma * NP;   // activation loads per lane per stage
+    constexpr int kDA = 8;              // weight loads per lane per stretch (4 code chunks + 4 scales)
+    // A 1-D grid of gx ff-slices x tiles (tiles rounded up to a multiple of 8). Workgroup L runs on
+    // XCD L % 8, so the slices of a tile are placed 8 apart: they run on the same XCD at about the same
+    // time, and the tile's activations come into that XCD's L2 once.
+    const int gx = ff / Sh::ff_rows;
+    const int L = blockIdx.x, r8 = L >> 3;
+    const int slice = r8 % gx, t = (L & 7) + 8 * (r8 / gx);
+    // n_tiles[0]: tiles in all; n_tiles[1]: the first tile of one token column (the list is ordered
+    // longest first). The small shape takes those, the other the rest.
+    const int ti = SMALL ? n_tiles[1] + t : t;
+    if (ti >= (SMALL ? n_tiles[0] : n_tiles[1])) return;
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int sRow[kTN];
+    __shared__ int sRow[Sh::tokens];
     FRT_PROBE_BEGIN();
-    FRT_PROBE(GATEUP ? 0 : 1, 0);
-    const int2 tile = tiles[blockIdx.y];
+    FRT_PROBE(0, 0);
+    const int2 tile = tiles[ti];
     const int grp = tile.x;
     const int row0 = bounds[grp] + tile.y;
-    const int cnt = min(kTN, bounds[grp + 1] - row0);
+    const int cnt = min(Sh::tokens, bounds[grp + 1] - row0);
     const uint8_t* blob = grp < E ? arena + size_t(grp) * stride : shared_blob;
-    const int Kd = GATEUP ? n : ff;            // contraction length (a multiple of 512)
-    const int nbk = Kd / kBlock;               // weight blocks per A row
-    const int rows_total = GATEUP ? ff : n;    // rows of each A matrix
+    const int nbk = n / kBlock;   // weight blocks per row
     const size_t mb = mat_bytes(ff, n);
-    const int rbase = blockIdx.x * (GATEUP ? kRows / 2 : kRows);
+    const int rbase = slice * Sh::ff_rows;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lg = lane >> 4;
-    // B row of each tile token: x row = token (gate/up), h row = dispatched row (down); a token
-    // past the group's end repeats the first (its columns are skipped and never written)
-    if (tid < kTN) sRow[tid] = GATEUP ? tok_of[row0 + min(tid, cnt - 1)] : row0 + min(tid, cnt - 1);
+    // activation row of each tile token; past the group's end the first repeats (never written)
+    if (tid < Sh::tokens) sRow[tid] = tok_of[row0 + min(tid, cnt - 1)];
     __syncthreads();
 
-    // this lane's weight rows (one per A tile; rows past the end load any row and are never stored):
-    // the matrix base is wave-uniform (gate for tiles 0, 1 and up for tiles 2, 3; down), the row a
-    // 32-bit chunk index
-    const uint8_t* const mA = GATEUP ? blob : blob + 2 * mb;
-    const uint8_t* const mB = GATEUP ? blob + mb : mA;
-    const size_t scale_off = size_t(rows_total) * nbk * 16;
-    uint32_t aoff[4];   // (row * nbk + lg): the chunk / scale index of block lg of stretch 0
+    // this lane's weight rows: ff row rbase + 32 wave + 16 (i & 1) + li of gate (i < 2) and up;
+    // rows past the end load any row and are never stored. aoff = row * nbk + lg: the chunk and
+    // scale index of block lg of stretch 0.
+    const uint8_t* const mG = blob;
+    const uint8_t* const mU = blob + mb;
+    const size_t scale_off = size_t(ff) * nbk * 16;
+    uint32_t aoff[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int t = GATEUP ? ((i < 2 ? 0 : kRows / 2) + 32 * wave + 16 * (i & 1) + li) : (64 * wave + 16 * i + li);
-        const int r = min(rbase + (GATEUP ? (t & (kRows / 2 - 1)) : t), rows_total - 1);
-        aoff[i] = uint32_t(r) * nbk + lg;
-    }
-    // weights of stretch q (blocks 4q + lg) into a register set
+    for (int i = 0; i < 2; ++i) aoff[i] = uint32_t(min(rbase + 32 * wave + 16 * i + li, ff - 1)) * nbk + lg;
     struct ARegs {
         uint4 cw[4];
         uint32_t sc[4];
     };
-    auto load_a = [&](int q, ARegs& a) {
+    auto load_a = [&](int q, ARegs& a) {   // stretch q (blocks 4q + lg)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint8_t* m = i < 2 ? mA : mB;
-            a.cw[i] = gld_u4(m + (size_t(aoff[i]) + 4 * q) * 16);
-            a.sc[i] = gld<uint16_t>(m + scale_off + (size_t(aoff[i]) + 4 * q) * 2);
+            const uint8_t* m = i < 2 ? mG : mU;
+            const size_t o = size_t(aoff[i & 1]) + 4 * q;
+            a.cw[i] = gld_u4(m + o * 16);
+            a.sc[i] = gld<uint16_t>(m + scale_off + o * 2);
         }
     };
-    // this thread's activation chunks of a stage: LDS positions P = 512 p + tid (token P / 16)
-    uint32_t boff[2];   // element offsets (rows * Kd stays below 2^31)
+    // this thread's activation chunks of a stage: LDS positions P = threads p + tid (token P / 16)
+    uint32_t boff[Sh::dma];   // element offsets (rows * n stays below 2^31)
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int P = 512 * p + tid, j = P >> 4, kc = (P & 15) ^ (j & 15);
-        boff[p] = uint32_t(sRow[j]) * Kd + kc * 8;
+    for (int p = 0; p < Sh::dma; ++p) {
+        const int P = Sh::threads * p + tid, j = P / Sh::cpt, kc = (P % Sh::cpt) ^ (j & (Sh::cpt - 1));
+        boff[p] = uint32_t(sRow[j]) * n + kc * 8;
     }
     auto issue_b = [&](int st, int slot) {
-        uint8_t* b = smem + slot * NP * kSlotB;
+        uint8_t* b = smem + slot * NP * Sh::slot_b;
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            ldsdma16(bhi + boff[p] + size_t(st) * kStageK, b + p * 8192 + wave * 1024);
-            if constexpr (NP == 2) ldsdma16(blo + boff[p] + size_t(st) * kStageK, b + kSlotB + p * 8192 + wave * 1024);
+        for (int p = 0; p < Sh::dma; ++p) {
+            ldsdma16(bhi + boff[p] + size_t(st) * Sh::stage_k, b + p * Sh::threads * 16 + wave * 1024);
+            ldsdma16(blo + boff[p] + size_t(st) * Sh::stage_k, b + Sh::slot_b + p * Sh::threads * 16 + wave * 1024);
         }
     };
-    auto read_b = [&](auto nc, int st, int t, half8 (&bv)[4][NP]) {   // K-step t (0..3) of stage st
+    auto read_b = [&](auto nc, int st, int t, half8(&bv)[4][NP]) {   // K-step t of stage st
         constexpr int NC = decltype(nc)::value;
-        const half8* sb = reinterpret_cast<const half8*>(smem + (st % kStages) * NP * kSlotB);
+        const half8* sb = reinterpret_cast<const half8*>(smem + (st % kStages) * NP * Sh::slot_b);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const int j = c * 16 + li, kc = t * 4 + lg;
 #pragma unroll
-            for (int part = 0; part < NP; ++part) {
-                bv[c][part] = sb[part * (kSlotB / 16) + j * 16 + (kc ^ (j & 15))];
-            }
+            for (int part = 0; part < NP; ++part)
+                bv[c][part] = sb[part * (Sh::slot_b / 16) + j * Sh::cpt + (kc ^ (j & (Sh::cpt - 1)))];
         }
     };
 
@@ -435,22 +451,20 @@ __global__ void __launch_bounds__(512) k_pf_gemm(const uint8_t* __restrict__ are
 #pragma unroll
             for (int c = 0; c < NC; ++c)
 #pragma unroll
-                for (int part = 0; part < NP; ++part) {
-                    acc[i][c] = mfma_acc(av, bv[c][part], acc[i][c]);
-                }
+                for (int part = 0; part < NP; ++part) acc[i][c] = mfma_acc(av, bv[c][part], acc[i][c]);
         }
     };
 
-    // Stage st (K = 128 st ..) is stretch st / 2, K-steps 4 (st % 2) .. + 3. Per stage st, after its
-    // barrier: A stretch st / 2 + 1 (st even), then B stage st + 2. Waiting for B stage st (vmcnt:
+    // Stage st (K = stage_k st ..) is part st % sps of stretch st / sps. Per stage st, after its
+    // barrier: A stretch st / sps + 1 (first stage of a stretch), then B stage st + 2. Waiting for B stage st (vmcnt:
     // later loads may stay outstanding) covers everything issued before it, A stretch st / 2
-    // included (issued two stages earlier, just before B stage st). The pattern is
-    // the same for every stage: past the end, the last stretch / stage is loaded again (into
-    // registers / a slot nothing reads any more), so the wait counts are constants and the
-    // compiler's own waits for the weight registers never see a path without later loads (at such a
-    // merge it would wait for every load in flight).
-    const int nst = Kd / kStageK;   // a multiple of 4
-    const int nq = nst / 2;         // stretches (even)
+    // included (issued sps stages earlier, just before B stage st - sps + 2). The pattern is the same for
+    // every stage: past the end, the last stretch / stage is loaded again (into registers / a slot
+    // nothing reads any more), so the wait counts are constants and the compiler's own waits for the
+    // weight registers never see a path without later loads (at such a merge it would wait for
+    // every load in flight).
+    const int nst = n / Sh::stage_k;   // stages
+    const int nq = n / 256;            // stretches (even)
     auto run = [&](auto nc) {
         ARegs a0, a1;   // stretches of even / odd index (named, so they stay in registers)
         // the loads of stages -2, -1 of the steady-state pattern below
@@ -460,19 +474,20 @@ __global__ void __launch_bounds__(512) k_pf_gemm(const uint8_t* __restrict__ are
         // the two stages of stretch q, whose weights are in cur; the next stretch loads into nxt
         auto stretch = [&](int q, const ARegs& cur, ARegs& nxt) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int st = 2 * q + h;
-                // loads issued after B stage st: B stage st + 1, and A stretch q + 1 when h = 1
+            for (int h = 0; h < Sh::sps; ++h) {
+                const int st = Sh::sps * q + h;
+                // loads issued after B stage st: B stage st + 1, and A stretch q + 1 when h = 1 (issued at
+                // stage st - 1, the stretch's first)
                 if (h == 0) wait_vm<kDB>();
                 else wait_vm<kDB + kDA>();
                 ring_barrier();   // stage st is in LDS for every wave; every wave is done with stage st - 1
                 if (h == 0) load_a(min(q + 1, nq - 1), nxt);
                 issue_b(min(st + 2, nst - 1), (st + 2) % kStages);   // into stage st - 1's slot
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
+                for (int t = 0; t < Sh::ksps; ++t) {
                     half8 bv[4][NP];
                     read_b(nc, st, t, bv);   // the NC columns the tile uses
-                    mul(nc, cur, 4 * h + t, bv);
+                    mul(nc, cur, Sh::ksps * h + t, bv);
                 }
             }
         };
@@ -481,61 +496,50 @@ __global__ void __launch_bounds__(512) k_pf_gemm(const uint8_t* __restrict__ are
             stretch(q + 1, a1, a0);
         }
     };
-    switch ((cnt + 15) / 16) {   // token columns with at least one real token
-        case 1: run(std::integral_constant<int, 1>{}); break;
-        case 2: run(std::integral_constant<int, 2>{}); break;
-        case 3: run(std::integral_constant<int, 3>{}); break;
-        default: run(std::integral_constant<int, 4>{}); break;
+    if constexpr (SMALL) {
+        run(std::integral_constant<int, 1>{});
+    } else {
+        switch ((cnt + 15) / 16) {   // token columns with at least one real token (2..4 here)
+            case 2: run(std::integral_constant<int, 2>{}); break;
+            case 3: run(std::integral_constant<int, 3>{}); break;
+            default: run(std::integral_constant<int, 4>{}); break;
+        }
     }
 
-    FRT_PROBE(GATEUP ? 0 : 1, 1);
-    if constexpr (GATEUP) {
-        // lane: token column c*16 + li; ff rows f = rbase + 32 wave + 16 i + 4 lg + q (i = 0, 1) for
-        // gate (acc[i]) and up (acc[2 + i]). The 32 rows of the wave are one Q8_0 block of h.
-        const int fbase = rbase + 32 * wave;
+    FRT_PROBE(0, 1);
+    // lane: token column c*16 + li; ff rows f = rbase + 32 wave + 16 i + 4 lg + r (i = 0, 1) for gate
+    // (acc[i]) and up (acc[2 + i]). The 32 rows of the wave are one Q8_0 block of h.
+    const int fbase = rbase + 32 * wave;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int col = c * 16 + li;
-            float hv[2][4];
-            float am = 0.0f;
+    for (int c = 0; c < (SMALL ? 1 : 4); ++c) {
+        const int col = c * 16 + li;
+        float hv[2][4];
+        float am = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                hv[i][r] = silu_mul(acc[i][c][r], acc[2 + i][c][r]);
+                am = fmaxf(am, fabsf(hv[i][r]));
+            }
+        am = fmaxf(am, __builtin_bit_cast(float, lane_xor16(__builtin_bit_cast(int, am))));
+        am = fmaxf(am, __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(int, am))));
+        const float d = q8_scale(am);
+        const float id = q8_inv(d);
+        const float dr = f16_round(d);
+        if (col < cnt && fbase < ff) {
+            const size_t row = size_t(row0 + col);
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    hv[i][q] = silu_mul(acc[i][c][q], acc[2 + i][c][q]);
-                    am = fmaxf(am, fabsf(hv[i][q]));
+                for (int r = 0; r < 4; ++r) {
+                    const int f = fbase + 16 * i + 4 * lg + r;
+                    const float a = float(q8_code(hv[i][r], id)) * dr;
+                    hout[row * ff + (f & ~255) + perm256_pos(f & 255)] = _Float16(a);
                 }
-            am = fmaxf(am, __builtin_bit_cast(float, lane_xor16(__builtin_bit_cast(int, am))));
-            am = fmaxf(am, __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(int, am))));
-            const float d = q8_scale(am);
-            const float id = q8_inv(d);
-            const float dr = f16_round(d);
-            if (col < cnt && fbase < ff) {
-                const size_t row = size_t(row0 + col);
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int f = fbase + 16 * i + 4 * lg + q;
-                        const float a = float(q8_code(hv[i][q], id)) * dr;
-                        hout[row * ff + (f & ~255) + perm256_pos(f & 255)] = _Float16(a);
-                    }
-            }
-        }
-    } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int col = c * 16 + li;
-            if (col >= cnt) continue;
-            const size_t slot = size_t(slot_of[row0 + col]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = rbase + 64 * wave + 16 * i + 4 * lg;
-                if (r < n) *reinterpret_cast<float4*>(yd + slot * n + r) = make_float4(acc[i][c][0], acc[i][c][1], acc[i][c][2], acc[i][c][3]);
-            }
         }
     }
-    FRT_PROBE(GATEUP ? 0 : 1, 2);
+    FRT_PROBE(0, 2);
     FRT_PROBE_END();
 }
 
@@ -759,7 +763,7 @@ static PfWs pf_carve(void* base, int T, int K, int n, int ff, int E, bool shared
     w.bounds = reinterpret_cast<int32_t*>(take(size_t(E + 2) * 4));
     w.tok_of = reinterpret_cast<int32_t*>(take(size_t(S) * 4));
     w.slot_of = reinterpret_cast<int32_t*>(take(size_t(S) * 4));
-    w.n_tiles = reinterpret_cast<int32_t*>(take(4));
+    w.n_tiles = reinterpret_cast<int32_t*>(take(8));   // [0] tiles, [1] first tile of one column
     w.tiles = reinterpret_cast<int2*>(take(size_t(pf_max_tiles(S, G)) * 8));
     w.xhi = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
     w.xlo = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
@@ -785,12 +789,12 @@ int pf_check(int T, int K, int n, int ff, int E) {
     return kOk;
 }
 
-template <bool GATEUP>
+template <bool SMALL>
 static int pf_gemm_attr() {
     static bool done = false;   // per process; the attribute is a property of the kernel
     if (!done) {
-        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<GATEUP>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, smem_bytes<GATEUP ? 2 : 1>()));
+        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<SMALL>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, GuShape<SMALL>::smem));
         done = true;
     }
     return kOk;
@@ -811,11 +815,18 @@ static int pf_down_attr(size_t lds) {
 // epilogue; down (k_pf_down) on h -> fp32 yd per slot.
 static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, int n, int ff,
                            const PfWs& w, int mt, float* ydf, hipStream_t stream) {
+    if (int rc = pf_gemm_attr<false>()) return rc;
     if (int rc = pf_gemm_attr<true>()) return rc;
-    launch_timed("pf_gateup", k_pf_gemm<true>, dim3((ff + kRows / 2 - 1) / (kRows / 2), mt), dim3(512),
-                 smem_bytes<2>(), stream, arena, stride, E, shared_blob, n, ff, (const _Float16*)w.xhi,
+    // tiles of 2-4 token columns, then those of one (the tile list is ordered longest first)
+    const int mt8 = (mt + 7) / 8 * 8;
+    launch_timed("pf_gateup", k_pf_gemm<false>, dim3(ff / GuShape<false>::ff_rows * mt8), dim3(GuShape<false>::threads),
+                 GuShape<false>::smem, stream, arena, stride, E, shared_blob, n, ff, (const _Float16*)w.xhi,
                  (const _Float16*)w.xlo, (const int32_t*)w.tok_of, (const int32_t*)w.bounds, (const int2*)w.tiles,
-                 (const int32_t*)w.n_tiles, w.h16, (float*)nullptr, (const int32_t*)nullptr);
+                 (const int32_t*)w.n_tiles, w.h16);
+    launch_timed("pf_gateup1", k_pf_gemm<true>, dim3(ff / GuShape<true>::ff_rows * mt8), dim3(GuShape<true>::threads),
+                 GuShape<true>::smem, stream, arena, stride, E, shared_blob, n, ff, (const _Float16*)w.xhi,
+                 (const _Float16*)w.xlo, (const int32_t*)w.tok_of, (const int32_t*)w.bounds, (const int2*)w.tiles,
+                 (const int32_t*)w.n_tiles, w.h16);
     timing_mark(stream, "pf_gateup");
     const size_t down_lds = size_t(kTN) * ff * 2;   // the tile's activations
     if (ff == 512) {
