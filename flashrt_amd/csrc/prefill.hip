@@ -543,14 +543,16 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
     FRT_PROBE_END();
 }
 
-// k_pf_down: the down GEMM, one workgroup per tile. The tile's activations (h of 64 dispatched rows,
-// all of K = ff, perm256 order) are loaded into LDS once (64 tokens x ff fp16; chunk kc of token j
-// at j * ff / 8 + (kc ^ (j & 15))), then the workgroup walks all n output rows in blocks of 512
-// (wave w: rows 64 w + 16 i + li of the block), streaming the weights straight into registers with
-// three stretches of lookahead (four register sets). No barrier after the activation load: each
-// wave reads only its own weights. NQ = ff / 256 stretches per row block.
+// k_pf_down: the down GEMM, one workgroup (256 threads) per tile. The tile's activations (h of 64
+// dispatched rows, all of K = ff, perm256 order) are loaded into LDS once (64 tokens x ff fp16; chunk
+// kc of token j at j * ff / 8 + (kc ^ (j & 15))), then the workgroup walks all n output rows in blocks
+// of 256 (wave w: rows 64 w + 16 i + li of the block), streaming the weights straight into
+// registers with three stretches of lookahead (four register sets). No barrier after the
+// activation load: each wave reads only its own weights. Two workgroups share a CU (64 KB of LDS
+// each for ff = 512), so one computes while the other waits for loads. NQ = ff / 256 stretches per
+// row block.
 template <int NQ>
-__global__ void __launch_bounds__(512) k_pf_down(const uint8_t* __restrict__ arena, size_t stride, int E,
+__global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ arena, size_t stride, int E,
                                                  const uint8_t* __restrict__ shared_blob, int n,
                                                  const _Float16* __restrict__ h, const int32_t* __restrict__ bounds,
                                                  const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
@@ -558,7 +560,7 @@ __global__ void __launch_bounds__(512) k_pf_down(const uint8_t* __restrict__ are
     constexpr int ff = NQ * 256;
     constexpr int nbk = ff / kBlock;   // weight blocks per row
     constexpr int cpt = ff / 8;        // 16-byte activation chunks per token
-    constexpr int kDB = kTN * cpt / 512;   // activation loads per lane
+    constexpr int kDB = kTN * cpt / 256;   // activation loads per lane
     if (int(blockIdx.y) >= *n_tiles) return;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int sRow[kTN];
@@ -577,7 +579,7 @@ __global__ void __launch_bounds__(512) k_pf_down(const uint8_t* __restrict__ are
     __syncthreads();
 #pragma unroll
     for (int p = 0; p < kDB; ++p) {
-        const int P = 512 * p + tid, j = P / cpt, kc = (P % cpt) ^ (j & 15);
+        const int P = 256 * p + tid, j = P / cpt, kc = (P % cpt) ^ (j & 15);
         ldsdma16(h + size_t(sRow[j]) * ff + kc * 8, smem + P * 16 - lane * 16);
     }
 
@@ -588,9 +590,9 @@ __global__ void __launch_bounds__(512) k_pf_down(const uint8_t* __restrict__ are
         uint4 cw[4];
         uint32_t sc[4];
     };
-    const int nsx = (n / 512) * NQ;   // stretches in all (a multiple of 4: n % 1024 == 0)
+    const int nsx = (n / 256) * NQ;   // stretches in all (a multiple of 4: n % 1024 == 0)
     auto load_a = [&](int s, ARegs& a) {   // stretch s: row block s / NQ, blocks 4 (s % NQ) + lg
-        const size_t base = size_t(s / NQ) * 512 * nbk + 4 * (s % NQ);
+        const size_t base = size_t(s / NQ) * 256 * nbk + 4 * (s % NQ);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             a.cw[i] = gld_u4(md + (base + aoff[i]) * 16);
@@ -647,7 +649,7 @@ __global__ void __launch_bounds__(512) k_pf_down(const uint8_t* __restrict__ are
                     if (c * 16 + li < cnt) {
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            const int r = rb * 512 + 64 * wave + 16 * i + 4 * lg;
+                            const int r = rb * 256 + 64 * wave + 16 * i + 4 * lg;
                             *reinterpret_cast<float4*>(yd + yslot[c] + r) =
                                 make_float4(acc[i][c][0], acc[i][c][1], acc[i][c][2], acc[i][c][3]);
                         }
@@ -831,12 +833,12 @@ static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uin
     const size_t down_lds = size_t(kTN) * ff * 2;   // the tile's activations
     if (ff == 512) {
         if (int rc = pf_down_attr<2>(down_lds)) return rc;
-        launch_timed("pf_down", k_pf_down<2>, dim3(1, mt), dim3(512), down_lds, stream, arena, stride, E, shared_blob,
+        launch_timed("pf_down", k_pf_down<2>, dim3(1, mt), dim3(256), down_lds, stream, arena, stride, E, shared_blob,
                      n, (const _Float16*)w.h16, (const int32_t*)w.bounds, (const int2*)w.tiles,
                      (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of);
     } else {
         if (int rc = pf_down_attr<4>(down_lds)) return rc;
-        launch_timed("pf_down", k_pf_down<4>, dim3(1, mt), dim3(512), down_lds, stream, arena, stride, E, shared_blob,
+        launch_timed("pf_down", k_pf_down<4>, dim3(1, mt), dim3(256), down_lds, stream, arena, stride, E, shared_blob,
                      n, (const _Float16*)w.h16, (const int32_t*)w.bounds, (const int2*)w.tiles,
                      (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of);
     }
