@@ -199,11 +199,13 @@ def run_prefill(args, F, torch):
     gu_flops = 2.0 * S * 2 * N * FF
     dn_flops = 2.0 * S * N * FF
     util = {}
-    for name, fl in (("pf_gateup", gu_flops), ("pf_down", dn_flops)):
-        if name in kt:
-            avg_ms = kt[name][0] / kt[name][1]
+    # gate/up runs as two kernels per layer (tiles of 2-4 token columns, then those of one)
+    for name, parts, fl in (("pf_gateup", ("pf_gateup", "pf_gateup1"), gu_flops), ("pf_down", ("pf_down",), dn_flops)):
+        if all(p in kt for p in parts):
+            avg_ms = sum(kt[p][0] / kt[p][1] for p in parts)
             util[name] = dict(avg_us=avg_ms * 1e3, tflops=fl / (avg_ms * 1e-3) / 1e12,
-                              mfma_frac=fl / (avg_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS)
+                              mfma_frac=fl / (avg_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS,
+                              kernels=list(parts))
     flops = gu_flops + dn_flops
     log(f"prefill 2K: {ms:.3f} ms/layer, {T / ms * 1e3:.0f} tok/s, experts {flops / 1e9:.1f} GFLOP")
     return SimpleNamespace(ms=ms, tokens_per_s=T / ms * 1e3, kernels=kt, util=util, flops=flops)

@@ -2,7 +2,7 @@
 // (kernels/cuda/moe_q2.cu:514-548 is the reference's int8 counterpart).
 //
 // Dispatch (moe_q2.cu:83-168 semantics: a stable sort of slots s = t*K + k by ids[s]):
-//   k_pf_hist   per chunk of 1024 slots, an LDS histogram of experts (integer atomics only)
+//   k_pf_hist   per chunk of 256 slots, an LDS histogram of experts (integer atomics only)
 //   k_pf_scan   one workgroup: per-expert column prefix over chunks, bounds, the tile list
 //   k_pf_place  one wave per chunk walks its slots in order, 64 at a time; each lane's rank among
 //               equal experts in the batch comes from ballots (a wave64 match-any), so the
@@ -22,7 +22,7 @@
 namespace frt {
 
 constexpr int kTN = 64;        // tokens per GEMM tile
-constexpr int kChunk = 1024;   // slots per dispatch chunk
+constexpr int kChunk = 256;    // slots per dispatch chunk (one wave of k_pf_place walks one)
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
@@ -88,7 +88,8 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
     };
     auto group_rows = [&](int e) {
         int c = 0;
-        for (int b = 0; b < nchunk; ++b) c += cnt[size_t(b) * E + e];
+#pragma unroll 8
+        for (int b = 0; b < nchunk; ++b) c += cnt[size_t(b) * E + e];   // independent loads, 8 in flight
         return c;
     };
     // pass 1: tiles per class over all groups (the shared group E included)
@@ -133,10 +134,16 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
                 tiles[at[k] + (k == 4 ? n[4] - 1 : 0)] = make_int2(e, (c / kTN) * kTN);
             }
             int run = off;
-            for (int b = 0; b < nchunk; ++b) {
-                const int x = cnt[size_t(b) * E + e];
-                cnt[size_t(b) * E + e] = run;
-                run += x;
+            for (int b0 = 0; b0 < nchunk; b0 += 8) {   // 8 loads in flight, then their prefix
+                int xv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) xv[u] = b0 + u < nchunk ? cnt[size_t(b0 + u) * E + e] : 0;
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (b0 + u < nchunk) {
+                        cnt[size_t(b0 + u) * E + e] = run;
+                        run += xv[u];
+                    }
             }
         }
         run_rows += tot_rows;

@@ -166,6 +166,41 @@ __global__ void k_quant_q8(const float* __restrict__ x, int n_blocks, int8_t* __
     }
 }
 
+// ---- Q8_0 of activations into the prefill GEMM's exact (hi, lo) fp16 pairs, perm256_pos order: one
+// wave per 256-element stretch, 4 consecutive elements per lane (8 lanes per Q8_0 block of 32). The
+// pairs go through LDS so that each lane then writes 4 consecutive positions (8 bytes) of each.
+// Same values as k_quant_q8 with xhi / xlo.
+__global__ void __launch_bounds__(256) k_quant_pairs(const float* __restrict__ x, int n_stretch,
+                                                     _Float16* __restrict__ xhi, _Float16* __restrict__ xlo) {
+    __shared__ _Float16 sp[4][2][256];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int st = blockIdx.x * 4 + wave;
+    if (st >= n_stretch) return;   // whole waves; no workgroup barrier below
+    const float4 v4 = *reinterpret_cast<const float4*>(x + size_t(st) * 256 + lane * 4);
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    am = fmaxf(am, __shfl_xor(am, 1));
+    am = fmaxf(am, __shfl_xor(am, 2));
+    am = fmaxf(am, __shfl_xor(am, 4));   // the 8 lanes of the block
+    const float d = q8_scale(am);
+    const float id = q8_inv(d);
+    const float dr = f16_round(d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = float(q8_code(v[i], id)) * dr;
+        const _Float16 hi = _Float16(a);
+        const int p = perm256_pos(lane * 4 + i);
+        sp[wave][0][p] = hi;
+        sp[wave][1][p] = _Float16(a - float(hi));
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's LDS writes are done (lgkmcnt(0))
+    __builtin_amdgcn_wave_barrier();
+    const uint2 h = *reinterpret_cast<const uint2*>(&sp[wave][0][lane * 4]);
+    const uint2 l = *reinterpret_cast<const uint2*>(&sp[wave][1][lane * 4]);
+    *reinterpret_cast<uint2*>(xhi + size_t(st) * 256 + lane * 4) = h;
+    *reinterpret_cast<uint2*>(xlo + size_t(st) * 256 + lane * 4) = l;
+}
+
 // wave per token
 template <int V>
 __global__ void __launch_bounds__(256) k_route_topk(const float* __restrict__ logits, int T, int E, int K,
@@ -243,6 +278,12 @@ int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16
                 hipStream_t stream) {
     if (rows < 1 || n % 64) return set_error(kErrShape, "quantize_q8: n=%d not a multiple of 64", n);
     const int nb = rows * (n / kQ8);
+    if (xhi && xlo && !xq && !xd && n % 256 == 0) {   // the prefill GEMM's pairs alone
+        const int ns = rows * (n / 256);
+        launch_timed("pf_quant_x", k_quant_pairs, dim3((ns + 3) / 4), dim3(256), 0, stream, x, ns, xhi, xlo);
+        FRT_LAUNCHED("quantize_q8");
+        return kOk;
+    }
     const int waves = (nb + 1) / 2;
     launch_timed("pf_quant_x", k_quant_q8, dim3((waves + 3) / 4), dim3(256), 0, stream, x, nb, xq, xd, xhi, xlo, n);
     FRT_LAUNCHED("quantize_q8");
