@@ -277,6 +277,44 @@ def test_moe_q2_run(F, w0, yd_bf16):
         F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, nb, None, True)
 
 
+@pytest.mark.parametrize("n,ff,T,K,E", [(1024, 1024, 40, 4, 6), (2048, 512, 8, 2, 8), (1024, 512, 200, 3, 4)])
+def test_moe_q2_run_shapes(F, n, ff, T, K, E):
+    """moe_q2::run at other shapes and tile mixes, every slot against the oracle's expert_ffn:
+    ff = 1024 (four weight stretches per down row block, a 128 KB tile in LDS) with n = 1024 and about
+    27 rows per expert (two-column tiles); only one-column tiles (T = 8, K = 2 over 8 experts); full
+    64-row tiles next to partial ones (T = 200, K = 3 over 4 experts)."""
+    w = H.World(cfg=0, n=n, ff=ff, E=E, K=K)
+    rng = np.random.default_rng(n + ff + T)
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    ids = np.stack([rng.choice(E, size=K, replace=False) for _ in range(T)]).astype(np.int32)
+    nb = F.moe_q2.workspace_bytes(T, K, n, ff, E)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    yd = torch.full((T * K, n), float("nan"), dtype=torch.float32, device="cuda")
+    F.moe_q2.run(w.arena.data_ptr(), w.stride, E, n, ff, dev(x), dev(ids), T, K, yd, ws, nb)
+    torch.cuda.synchronize()
+    y = yd.cpu().numpy().reshape(T, K, n)
+    for t in range(T):
+        for k in range(K):
+            ref = O.expert_ffn(w.blob(int(ids[t, k])), n, ff, x[t])
+            err = H.out_rel(y[t, k][None], ref)
+            assert err <= H.OUT_REL, (t, k, err)
+
+
+def test_moe_q2_run_shape_errors(F, w0):
+    """The grouped GEMMs' shape limits (n a multiple of 1024, ff 512 or 1024) fail loudly."""
+    T, K = 4, 2
+    x = torch.zeros((T, 2048), dtype=torch.float32, device="cuda")
+    ids = torch.zeros((T, K), dtype=torch.int32, device="cuda")
+    ids[:, 1] = 1
+    yd = torch.empty((T * K, 2048), dtype=torch.float32, device="cuda")
+    for n, ff in ((2048, 768), (1536, 512)):
+        nb = F.moe_q2.workspace_bytes(T, K, n, ff, 8)
+        ws = torch.empty(max(nb, 1 << 20), dtype=torch.uint8, device="cuda")
+        with pytest.raises(F.FrtError) as e:
+            F.moe_q2.run(w0.arena.data_ptr(), w0.stride, 8, n, ff, x, ids, T, K, yd, ws, ws.numel())
+        assert e.value.code == -1
+
+
 def test_layer_prefill_config3(F):
     """Config 3: 2048 bf16 tokens, Zipf(1.2) routing prior. Every token's ids are bit-exact; the
     outputs of 48 sampled tokens are checked against the oracle (a token's output depends only on
@@ -329,6 +367,21 @@ def test_layer_mixed_config4(F):
     assert np.array_equal(sid, ids[sel])
     assert H.out_rel(out[sel], ref) <= H.OUT_REL
     assert np.isfinite(out).all()
+
+
+def test_next_router_warming_keeps_results(F, w0):
+    """A decode call that also loads the next layer's router rows into the caches
+    (frt_moe_layer.next_router_w) returns exactly what it returns without."""
+    x = np.random.default_rng(5).standard_normal((1, H.N)).astype(np.float32)
+    out0, ids0, wts0 = w0.gpu_forward(x)
+    w0.layer_obj.set_next_router(w0.router_w)
+    try:
+        out1, ids1, wts1 = w0.gpu_forward(x)
+    finally:
+        w0.layer_obj.set_next_router(None)
+    assert np.array_equal(ids0, ids1)
+    assert np.array_equal(wts0, wts1)
+    assert np.array_equal(out0, out1)
 
 
 def test_layer_errors(F, w0):
