@@ -406,7 +406,8 @@ def main():
                               "mfma_frac_layer": round(pf.flops / (pf.ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
                               "kernels": {k: dict(avg_us=round(v[0] / v[1] * 1e3, 2), launches=v[1])
                                           for k, v in pf.kernels.items()},
-                              "mfma": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in pf.util.items()}}
+                              "mfma": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                                       for k, v in pf.util.items()}}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args, F, torch, st)
     print(json.dumps(line), flush=True)
