@@ -246,6 +246,36 @@ __global__ void k_pf_place_shared(int T, int K, int32_t* __restrict__ tok_of, in
 // 16 lane, no registers), issued two stages ahead; one workgroup barrier per stage. Slot layout:
 //   [NP][tokens][cpt chunks of 8 fp16], chunk kc of token j at j * cpt + (kc ^ (j % cpt)), so that the
 //   lanes of a 128-bit read phase (one chunk of 8 tokens) hit distinct bank groups.
+// The vmcnt of stage st's wait in k_pf_gemm: the loads it may leave outstanding, B stage st + 1 and,
+// when stage st - 1 was a stretch's first (h = 1), the A stretch issued just before it.
+constexpr int gu_wait(int h, int kDB, int kDA) { return h == 1 ? kDB + kDA : kDB; }
+// The same count from the issue order itself: prologue A 0, B 0, B 1; stage s issues A (when s % sps
+// == 0), then B s + 2. Counts the loads issued after B stage st and before stage st's wait.
+constexpr int gu_after_b(int st, int sps, int kDB, int kDA) {
+    int seq[64] = {};   // 1 = an A stretch, 2 + s = B stage s
+    int n = 0;
+    seq[n++] = 1;
+    seq[n++] = 2;
+    seq[n++] = 3;
+    int end = n;   // issues before stage st's wait
+    for (int s = 0; s < st; ++s) {
+        if (s % sps == 0) seq[n++] = 1;
+        seq[n++] = 2 + s + 2;
+        end = n;
+    }
+    int after = 0;
+    bool seen = false;
+    for (int i = 0; i < end; ++i) {
+        if (seen) after += seq[i] == 1 ? kDA : kDB;
+        if (seq[i] == 2 + st) seen = true;
+    }
+    return after;
+}
+constexpr bool gu_waits_ok(int sps, int kDB, int kDA) {
+    for (int st = 0; st < 12; ++st)
+        if (gu_after_b(st, sps, kDB, kDA) != gu_wait(st % sps, kDB, kDA)) return false;
+    return true;
+}
 constexpr int kStages = 3;    // activation ring slots (stages issued kStages - 1 ahead)
 template <bool SMALL>
 struct GuShape {
@@ -260,6 +290,7 @@ struct GuShape {
     static constexpr int smem = kStages * 2 * slot_b;
     static constexpr int dma = tokens * cpt / threads;    // activation loads per lane per part
     static constexpr int min_waves = SMALL ? 4 : 2;       // per SIMD (SMALL: 4 workgroups per CU)
+    static_assert(sps >= 2 && gu_waits_ok(sps, dma * 2, 8), "the wait counts of k_pf_gemm");
 };
 
 
@@ -350,6 +381,7 @@ __device__ __forceinline__ floatx4 mfma_acc(half8 a, half8 b, floatx4 c) {
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 
 template <bool SMALL>
 __global__ void __launch_bounds__(GuShape<SMALL>::threads, GuShape<SMALL>::min_waves)
@@ -462,10 +494,12 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
         }
     };
 
-    // Stage st (K = stage_k st ..) is part st % sps of stretch st / sps. Per stage st, after its
-    // barrier: A stretch st / sps + 1 (first stage of a stretch), then B stage st + 2. Waiting for B stage st (vmcnt:
-    // later loads may stay outstanding) covers everything issued before it, A stretch st / 2
-    // included (issued sps stages earlier, just before B stage st - sps + 2). The pattern is the same for
+    // Stage st (K = stage_k st ..) is part h = st % sps of stretch st / sps. Per stage st, after its
+    // barrier: A stretch st / sps + 1 (first stage of a stretch, h = 0), then B stage st + 2. At the
+    // wait of stage st, the loads issued after B stage st are those of stage st - 1: B stage st + 1,
+    // preceded by an A stretch only when stage st - 1 was a stretch's first (h = 1). Waiting for B
+    // stage st (vmcnt: those later loads may stay outstanding) covers everything issued before it,
+    // A stretch st / sps included (issued at the stretch before's first stage). The pattern is the same for
     // every stage: past the end, the last stretch / stage is loaded again (into registers / a slot
     // nothing reads any more), so the wait counts are constants and the compiler's own waits for the
     // weight registers never see a path without later loads (at such a merge it would wait for
@@ -484,9 +518,9 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
             for (int h = 0; h < Sh::sps; ++h) {
                 const int st = Sh::sps * q + h;
                 // loads issued after B stage st: B stage st + 1, and A stretch q + 1 when h = 1 (issued at
-                // stage st - 1, the stretch's first)
-                if (h == 0) wait_vm<kDB>();
-                else wait_vm<kDB + kDA>();
+                // stage st - 1, the stretch's first); none other may stay outstanding
+                if (h == 1) wait_vm<gu_wait(1, kDB, kDA)>();
+                else wait_vm<gu_wait(0, kDB, kDA)>();
                 ring_barrier();   // stage st is in LDS for every wave; every wave is done with stage st - 1
                 if (h == 0) load_a(min(q + 1, nq - 1), nxt);
                 issue_b(min(st + 2, nst - 1), (st + 2) % kStages);   // into stage st - 1's slot

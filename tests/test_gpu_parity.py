@@ -338,6 +338,29 @@ def test_layer_prefill_config3(F):
     assert np.isfinite(out).all()
 
 
+def test_layer_prefill_repeatable(F):
+    """The prefill kernels sum without atomics, so one input gives the same bits on every call: 8
+    calls of the config 3 layer agree exactly on all 2048 tokens (a load that an LDS ring reads
+    before it lands, or a missing barrier, shows up as differences between calls)."""
+    T = 2048
+    bias = O.gen_zipf_bias(3, 0, H.E, H.ZIPF_S_PREFILL, H.PREFILL_ALPHA)
+    w3 = H.World(cfg=3, bias=bias)
+    xt = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    F.gen.normal(xt, 3, 0, O.X_TENSOR, 1.0, round_bf16=True)
+    out = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    ws = w3.layer_obj.workspace(T)
+    first = None
+    for i in range(8):
+        out.fill_(float("nan"))
+        w3.layer_obj.forward(xt, out, T=T, ws=ws)
+        cur = out.clone()
+        if first is None:
+            first = cur
+            assert torch.isfinite(first).all()
+        else:
+            assert torch.equal(cur, first), i
+
+
 def test_layer_mixed_config4(F):
     """Config 4: an 8192-token bf16 prefill chunk plus 16 uncorrelated fp32 decode tokens in one
     launch (T = 8208), with adversarial popularity: +2.8 on the logits of 16 seeded hot experts puts
@@ -382,6 +405,50 @@ def test_next_router_warming_keeps_results(F, w0):
     assert np.array_equal(ids0, ids1)
     assert np.array_equal(wts0, wts1)
     assert np.array_equal(out0, out1)
+
+
+def _edge_bias(case: str) -> np.ndarray:
+    rng = np.random.default_rng(11)
+    E = H.E
+    pos = rng.permutation(E)
+    if case == "all_equal":
+        return np.zeros(E, np.float32)
+    if case == "coarse":
+        return (np.round(rng.standard_normal(E) * 2.0) / 2.0).astype(np.float32)
+    b = (-1.0 - np.abs(rng.standard_normal(E))).astype(np.float32)
+    if case == "tie10":          # 5 distinct leaders, then 12 equal values across the 10th place
+        b[pos[:5]] = [10.0, 9.0, 8.0, 7.0, 6.0]
+        b[pos[5:17]] = 5.0
+    elif case in ("c64", "c65"):   # 3 leaders and 61 / 62 equal: 64 / 65 candidates
+        b[pos[:3]] = [10.0, 9.0, 8.0]
+        b[pos[3:3 + (61 if case == "c64" else 62)]] = 4.0
+    elif case == "neg_inf":      # 6 finite logits; 4 of the selection are -inf (weight 0)
+        b[:] = -np.inf
+        b[pos[:6]] = [3.0, 1.0, 0.5, -2.0, -2.0, 7.0]
+    elif case == "signed_zero":  # +0 and -0 leaders, equal as logits
+        b[pos[:14]] = np.where(np.arange(14) % 2 == 0, 0.0, -0.0).astype(np.float32)
+    return b
+
+
+@pytest.mark.parametrize("case", ["tie10", "c64", "c65", "all_equal", "neg_inf", "signed_zero", "coarse"])
+def test_decode_routing_edge_logits(F, case):
+    """Decode routing on chosen logits: with the router matrix zero the logits are the bias
+    exactly. Ties across the 10th place go to the lowest ids; 64 candidates stay on the one-wave
+    selection of a single token, 65 and more (all equal) take the four-wave path; -inf logits get
+    weight 0. T = 1 (one-wave path) and T = 2 (four-wave path) against the oracle."""
+    w = H.World(cfg=0, bias=_edge_bias(case))
+    w.router_w.zero_()
+    w.router_h[:] = 0.0
+    torch.cuda.synchronize()
+    for T in (1, 2):
+        x = O.gen_normal(0, 0, O.X_TENSOR + 9, T * H.N).reshape(T, H.N)
+        out, ids, wts = w.gpu_forward(x)
+        ref, rid, rw, _ = w.oracle_forward(x)
+        assert np.array_equal(ids, rid), (case, T, ids, rid)
+        nz = rw != 0
+        assert np.array_equal(wts[~nz], rw[~nz]), (case, T)
+        assert H.w_rel(wts[nz], rw[nz]) <= H.W_REL, (case, T)
+        assert H.out_rel(out, ref) <= H.OUT_REL, (case, T)
 
 
 def test_layer_errors(F, w0):
