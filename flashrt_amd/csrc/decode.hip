@@ -52,12 +52,106 @@ struct DecComb {
 
 struct WinLds {
     DecEntry ent[64];
+    int32_t many;   // the one-wave selection of a single token found more than 64 candidates
     int32_t ids[kDecMaxT][32];
     float w[kDecMaxT][32];
     DecComb comb;
     TopkLds tk[kDecMaxT];
     int32_t n_ent;
 };
+
+// The routing and entry list of a single token by one wave, the same selection, weights and
+// entries as topk_group4 followed by the single-token entry code below, with ballots in place of
+// sorts and barriers:
+//   1. lane l holds experts V l .. V l + V - 1; a lower bound on the K-th largest lane maximum (a
+//      search over the keys' upper 16 bits by ballot counts) bounds the K-th largest logit from
+//      below, so every member of the top K is a candidate; candidates are compacted into LDS in
+//      ascending id;
+//   2. one candidate per lane: its rank by logit counts the candidates ahead of it (higher key, or
+//      equal and lower id); the selection is rank < K, and the entry index is the selection's lane
+//      order (ascending id);
+//   3. e = exp(l - max) in rank order through LDS, w = e / (sum of e in rank order).
+// More than 64 candidates (heavily tied logits) sets L.many and writes nothing else; the caller
+// then runs the four-wave path. gl is the shared gate logit in lane 0.
+template <int V>
+__device__ __forceinline__ void route1_wave(const float (&v)[V], int E, int K, float gl,
+                                            const uint8_t* __restrict__ arena, size_t stride,
+                                            const uint8_t* __restrict__ shared_blob, WinLds& L) {
+    const int lane = threadIdx.x & 63;
+    TopkLds& S = L.tk[0];
+    uint32_t key[V], mk = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        key[i] = V * lane + i < E ? logit_key(v[i]) : 0u;
+        mk = max(mk, key[i]);
+    }
+    const uint32_t t1 = wave_kth_key_hi(mk, K) << 16;
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) c += int(key[i] != 0u && key[i] >= t1);
+    int C;
+    int pos = wave_excl_scan(c, &C);
+    if (C > 64) {
+        if (lane == 0) L.many = 1;
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {   // branch-free compaction: a non-candidate goes to junk slot 64 + lane
+        const bool is_c = key[i] != 0u && key[i] >= t1;
+        const int slot = is_c ? pos : 64 + lane;
+        S.cand_v[slot] = v[i];
+        S.cand_id[slot] = V * lane + i;
+        pos += int(is_c);
+    }
+    const bool cl = lane < C;
+    const float cv = cl ? S.cand_v[lane] : 0.0f;
+    const int ci = cl ? S.cand_id[lane] : 0x7fffffff;
+    const uint32_t ck = cl ? logit_key(cv) : 0u;
+    int rank = 0;
+    for (int j = 0; j < C; ++j) {
+        const uint32_t kj = uint32_t(__builtin_amdgcn_readlane(int(ck), j));
+        rank += int(kj > ck || (kj == ck && j < lane));
+    }
+    const bool sel = cl && rank < K;
+    const int u = lanes_below(__ballot(sel));   // entry index: ascending expert id
+    const int top = __builtin_ctzll(__ballot(sel && rank == 0));
+    const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), top));
+    const float e = sel ? expf(cv - mx) : 0.0f;
+    if (sel) S.e[rank] = e;
+    float ws = 0.0f;
+    for (int k = 0; k < K; ++k) ws += S.e[k];
+    const float w = e / ws;
+    if (sel) {
+        L.ids[0][rank] = ci;
+        L.w[0][rank] = w;
+        DecEntry& d = L.ent[u];
+        d.blob = arena + size_t(ci) * stride;
+        d.ntok = 1;
+        d.base = u;
+        d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
+        d.slot[0] = rank;
+        d.slot[1] = d.slot[2] = d.slot[3] = -1;
+        d.w[0] = w;
+        d.w[1] = d.w[2] = d.w[3] = 0.0f;
+        L.comb.slot[0][u] = u;
+        L.comb.w[0][u] = w;
+    }
+    const float sw = sigmoidf_(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gl), 0)));
+    if (lane == 63) {
+        DecEntry& d = L.ent[K];
+        d.blob = shared_blob;
+        d.ntok = 1;
+        d.base = K;
+        d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
+        d.slot[0] = d.slot[1] = d.slot[2] = d.slot[3] = -1;
+        d.w[0] = sw;
+        d.w[1] = d.w[2] = d.w[3] = 0.0f;
+        L.comb.slot[0][K] = K;
+        L.comb.w[0][K] = sw;
+        L.n_ent = K + 1;
+        L.many = 0;
+    }
+}
 
 template <int V>
 __device__ __forceinline__ int window_entries(const float* __restrict__ logits, const float* __restrict__ gate, int T,
@@ -66,10 +160,35 @@ __device__ __forceinline__ int window_entries(const float* __restrict__ logits, 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g = wave >> 2, q = wave & 3;
     const bool active = g < T;
-    // shared gate logits, loaded here (a volatile load stays where it is issued: the compiler would
-    // otherwise sink it to its use, after the top-k, and wait out a whole round trip there)
-    const float gl = (wave == 0 && lane < T) ? *reinterpret_cast<const volatile float*>(gate + lane) : 0.0f;
+    // shared gate logits, issued with the logits (a plain load: a volatile one is waited for where it
+    // is issued); every lane loads (a clamped index, no branch, so no wait is placed at a branch merge)
+    const float gl = gate[min(lane, T - 1)];
     float mx;
+    if (T == 1) {   // one wave selects; the rest of the workgroup waits at the barrier
+        if (wave == 0) {
+            float v[V];
+            if (E == 64 * V) {
+                const float4* l4 = reinterpret_cast<const float4*>(logits + V * lane);
+#pragma unroll
+                for (int i = 0; i < V / 4; ++i) {
+                    const float4 f = l4[i];
+                    v[4 * i] = f.x;
+                    v[4 * i + 1] = f.y;
+                    v[4 * i + 2] = f.z;
+                    v[4 * i + 3] = f.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < V; ++i) v[i] = logits[min(V * lane + i, E - 1)];
+            }
+            route1_wave<V>(v, E, K, gl, arena, stride, shared_blob, L);
+        }
+        __syncthreads();
+        if (!L.many) {
+            FRT_PROBE(3, 6);
+            return K + 1;
+        }
+    }
     topk_group4<V>(logits + size_t(active ? g : 0) * E, E, K, q, active, L.tk[active ? g : 0], mx);
     if (T == 1) {   // one token: entries are its K experts by ascending id (slot = entry), then the shared expert
         if (wave == 0) {

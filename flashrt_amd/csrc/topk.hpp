@@ -102,6 +102,36 @@ __device__ __forceinline__ int wave_excl_scan(int c, int* total) {
     return x - c;
 }
 
+// Order key of a logit: unsigned comparison of keys is float comparison of logits, with -0 and +0
+// equal (for finite and infinite values; NaN is not a logit). Key 0 is below every logit and marks
+// an empty lane.
+__device__ __forceinline__ uint32_t logit_key(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    u = u == 0x80000000u ? 0u : u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// The largest t < 2^16 with at least K lanes holding key >= t << 16 (K >= 1; 0 when fewer than K
+// lanes hold a nonzero key): a lower bound on the K-th largest key, found two bits at a time from
+// the top by ballot counts over the keys' upper halves; uniform.
+__device__ __forceinline__ uint32_t wave_kth_key_hi(uint32_t key, int K) {
+    const uint32_t kh = key >> 16;
+    uint32_t t = 0;
+#pragma unroll
+    for (int b = 14; b >= 0; b -= 2) {
+        const uint32_t c1 = t | (1u << b), c2 = t | (2u << b), c3 = t | (3u << b);
+        const int n1 = __popcll(__ballot(kh >= c1)), n2 = __popcll(__ballot(kh >= c2)),
+                  n3 = __popcll(__ballot(kh >= c3));
+        t = n3 >= K ? c3 : n2 >= K ? c2 : n1 >= K ? c1 : t;
+    }
+    return t;
+}
+
+// Number of lanes below this one whose bit is set in m.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0));
+}
+
 // Top-K (K <= 64) of one token's E <= 64 V logits by one wave. cand: 64 floats + 64 ints of LDS
 // scratch for this wave. On return lane k < K holds the k-th selection (sel_id, sel_l) in rank
 // order; mx is the largest logit and se this lane's share of sum_e exp(l_e - mx).
