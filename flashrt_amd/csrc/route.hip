@@ -50,29 +50,47 @@ __global__ void __launch_bounds__(256) k_router(const float* __restrict__ x, int
     const float* w = is_gate ? gate_w : W + size_t(row < E ? row : 0) * n;
     float wr[L];
     {   // this lane's chain of the router row: L contiguous floats as L/4 16-byte loads
+        // (loaded unconditionally, row 0 standing in for a row that is not live, whose wave skips the
+        // dot product: a conditional load would be waited for where the branches meet)
         const float4* w4 = reinterpret_cast<const float4*>(w + lane * L);
 #pragma unroll
         for (int i = 0; i < L / 4; ++i) {
-            const float4 v = live ? w4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 v = w4[i];
             wr[4 * i] = v.x;
             wr[4 * i + 1] = v.y;
             wr[4 * i + 2] = v.z;
             wr[4 * i + 3] = v.w;
         }
     }
-    const float b = (live && !is_gate && bias) ? bias[row] : 0.0f;
+    const float b = bias ? bias[min(row, E - 1)] : 0.0f;   // used for rows < E only
     const int t_begin = blockIdx.y * tok_per_wg, t_end = min(T, t_begin + tok_per_wg);
     for (int t0 = t_begin; t0 < t_end; t0 += TT) {
         const int tn = min(TT, t_end - t0);
-        __syncthreads();
-        for (int i = threadIdx.x; i < tn * (n / 4); i += blockDim.x) {
-            const int t = i / (n / 4), k = (i % (n / 4)) * 4;
-            const float4 v = *reinterpret_cast<const float4*>(x + size_t(t0 + t) * n + k);
-            float* dst = xs + (t * 64 + k / L) * (L + 1) + k % L;   // L % 4 == 0: one chain
-            dst[0] = v.x;
-            dst[1] = v.y;
-            dst[2] = v.z;
-            dst[3] = v.w;
+        // the previous tile's LDS reads are done (none before the first tile: its x loads then
+        // issue right behind the row loads, without a fence waiting for those)
+        if (t0 != t_begin) __syncthreads();
+        // x tile into LDS, 4 loads per thread in flight before their LDS writes (clamped indices, no
+        // branches, which would let the compiler sink each load to its write: past the end a thread
+        // rewrites the last element with its own value)
+        const int nx = tn * (n / 4);
+        for (int i0 = threadIdx.x; i0 < nx; i0 += 4 * int(blockDim.x)) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = min(i0 + u * int(blockDim.x), nx - 1);
+                const int t = i / (n / 4), k = (i % (n / 4)) * 4;
+                v[u] = *reinterpret_cast<const float4*>(x + size_t(t0 + t) * n + k);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = min(i0 + u * int(blockDim.x), nx - 1);
+                const int t = i / (n / 4), k = (i % (n / 4)) * 4;
+                float* dst = xs + (t * 64 + k / L) * (L + 1) + k % L;   // L % 4 == 0: one chain
+                dst[0] = v[u].x;
+                dst[1] = v[u].y;
+                dst[2] = v[u].z;
+                dst[3] = v[u].w;
+            }
         }
         __syncthreads();
         FRT_PROBE(0, 1);
