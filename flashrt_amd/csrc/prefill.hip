@@ -241,42 +241,46 @@ __global__ void k_pf_place_shared(int T, int K, int32_t* __restrict__ tok_of, in
 // every lane a separate cache-line request). Each wave loads only its own rows, one stretch ahead,
 // into a second register set.
 //
-// Activations go through LDS: stages of 64 or 128 K in a ring of kStages slots filled by
-// direct global-to-LDS loads (global_load_lds: each lane's 16 bytes land at the wave's LDS base +
-// 16 lane, no registers), issued two stages ahead; one workgroup barrier per stage. Slot layout:
+// Activations go through LDS: stages of 64 or 128 K in a ring of 3 slots
+// filled by direct global-to-LDS loads (global_load_lds: each lane's 16 bytes land at the wave's LDS
+// base + 16 lane, no registers), issued 2 stages ahead; one workgroup barrier per stage. Slot layout:
 //   [NP][tokens][cpt chunks of 8 fp16], chunk kc of token j at j * cpt + (kc ^ (j % cpt)), so that the
 //   lanes of a 128-bit read phase (one chunk of 8 tokens) hit distinct bank groups.
-// The vmcnt of stage st's wait in k_pf_gemm: the loads it may leave outstanding, B stage st + 1 and,
-// when stage st - 1 was a stretch's first (h = 1), the A stretch issued just before it.
-constexpr int gu_wait(int h, int kDB, int kDA) { return h == 1 ? kDB + kDA : kDB; }
-// The same count from the issue order itself: prologue A 0, B 0, B 1; stage s issues A (when s % sps
-// == 0), then B s + 2. Counts the loads issued after B stage st and before stage st's wait.
-constexpr int gu_after_b(int st, int sps, int kDB, int kDA) {
-    int seq[64] = {};   // 1 = an A stretch, 2 + s = B stage s
+// Issue order of k_pf_gemm's loads, as stages s of the same pattern: stage s issues the weights of
+// stretch s / sps + 1 when s is a stretch's first (s % sps == 0: "A"), then the activations of stage
+// s + ahead ("B"). The prologue is the stages s = -max(ahead, sps) .. -1 of that pattern (A of
+// stretch 0 at s = -sps; B stage s + ahead for s >= -ahead), so every stage's wait counts the same.
+constexpr int gu_mod(int a, int m) { return ((a % m) + m) % m; }
+// The vmcnt of stage st's wait: the loads issued after B stage st (at stage st - ahead), by stages
+// st - ahead + 1 .. st - 1: ahead - 1 B stages and the A of each stretch's first among them.
+constexpr int gu_wait(int h, int ahead, int sps, int kDB, int kDA) {
+    int c = (ahead - 1) * kDB;
+    for (int d = 1; d < ahead; ++d) c += gu_mod(h - d, sps) == 0 ? kDA : 0;
+    return c;
+}
+// The same count by listing the issues of the prologue and stages 0 .. st - 1 (1 = an A, 2 + s = B
+// stage s) and counting what follows B stage st.
+constexpr int gu_after_b(int st, int ahead, int sps, int kDB, int kDA) {
+    int seq[96] = {};
     int n = 0;
-    seq[n++] = 1;
-    seq[n++] = 2;
-    seq[n++] = 3;
-    int end = n;   // issues before stage st's wait
-    for (int s = 0; s < st; ++s) {
-        if (s % sps == 0) seq[n++] = 1;
-        seq[n++] = 2 + s + 2;
-        end = n;
+    const int first = -(ahead > sps ? ahead : sps);
+    for (int s = first; s < st; ++s) {
+        if (gu_mod(s, sps) == 0 && s / sps + 1 >= 0 && s >= -sps) seq[n++] = 1;
+        if (s >= -ahead) seq[n++] = 2 + s + ahead;
     }
     int after = 0;
     bool seen = false;
-    for (int i = 0; i < end; ++i) {
+    for (int i = 0; i < n; ++i) {
         if (seen) after += seq[i] == 1 ? kDA : kDB;
         if (seq[i] == 2 + st) seen = true;
     }
     return after;
 }
-constexpr bool gu_waits_ok(int sps, int kDB, int kDA) {
-    for (int st = 0; st < 12; ++st)
-        if (gu_after_b(st, sps, kDB, kDA) != gu_wait(st % sps, kDB, kDA)) return false;
+constexpr bool gu_waits_ok(int ahead, int sps, int kDB, int kDA) {
+    for (int st = 0; st < 16; ++st)
+        if (gu_after_b(st, ahead, sps, kDB, kDA) != gu_wait(gu_mod(st, sps), ahead, sps, kDB, kDA)) return false;
     return true;
 }
-constexpr int kStages = 3;    // activation ring slots (stages issued kStages - 1 ahead)
 template <bool SMALL>
 struct GuShape {
     static constexpr int threads = 256;
@@ -287,10 +291,12 @@ struct GuShape {
     static constexpr int ksps = stage_k / 32;             // MFMA K-steps per stage
     static constexpr int cpt = stage_k / 8;               // 16-byte chunks per token per stage
     static constexpr int slot_b = tokens * stage_k * 2;   // bytes per part per slot
-    static constexpr int smem = kStages * 2 * slot_b;
+    static constexpr int stages = 3;                      // activation ring slots
+    static constexpr int ahead = stages - 1;              // stages issued ahead
+    static constexpr int smem = stages * 2 * slot_b;
     static constexpr int dma = tokens * cpt / threads;    // activation loads per lane per part
     static constexpr int min_waves = SMALL ? 4 : 2;       // per SIMD (SMALL: 4 workgroups per CU)
-    static_assert(sps >= 2 && gu_waits_ok(sps, dma * 2, 8), "the wait counts of k_pf_gemm");
+    static_assert(sps <= 4 && gu_waits_ok(ahead, sps, dma * 2, 8), "the wait counts of k_pf_gemm");
 };
 
 
@@ -460,7 +466,7 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
     };
     auto read_b = [&](auto nc, int st, int t, half8(&bv)[4][NP]) {   // K-step t of stage st
         constexpr int NC = decltype(nc)::value;
-        const half8* sb = reinterpret_cast<const half8*>(smem + (st % kStages) * NP * Sh::slot_b);
+        const half8* sb = reinterpret_cast<const half8*>(smem + (st % Sh::stages) * NP * Sh::slot_b);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const int j = c * 16 + li, kc = t * 4 + lg;
@@ -495,35 +501,38 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
     };
 
     // Stage st (K = stage_k st ..) is part h = st % sps of stretch st / sps. Per stage st, after its
-    // barrier: A stretch st / sps + 1 (first stage of a stretch, h = 0), then B stage st + 2. At the
-    // wait of stage st, the loads issued after B stage st are those of stage st - 1: B stage st + 1,
-    // preceded by an A stretch only when stage st - 1 was a stretch's first (h = 1). Waiting for B
-    // stage st (vmcnt: those later loads may stay outstanding) covers everything issued before it,
-    // A stretch st / sps included (issued at the stretch before's first stage). The pattern is the same for
-    // every stage: past the end, the last stretch / stage is loaded again (into registers / a slot
-    // nothing reads any more), so the wait counts are constants and the compiler's own waits for the
-    // weight registers never see a path without later loads (at such a merge it would wait for
-    // every load in flight).
+    // barrier: A stretch st / sps + 1 (first stage of a stretch, h = 0), then B stage st + ahead (the
+    // issue pattern of gu_wait). Waiting for B stage st (vmcnt: the loads issued after it may stay
+    // outstanding) covers everything issued before it, A stretch st / sps included. The pattern is
+    // the same for every stage: past the end, the last stretch / stage is loaded again (into
+    // registers / a slot nothing reads any more), so the wait counts are constants and the
+    // compiler's own waits for the weight registers never see a path without later loads (at such
+    // a merge it would wait for every load in flight).
     const int nst = n / Sh::stage_k;   // stages
     const int nq = n / 256;            // stretches (even)
     auto run = [&](auto nc) {
         ARegs a0, a1;   // stretches of even / odd index (named, so they stay in registers)
-        // the loads of stages -2, -1 of the steady-state pattern below
-        load_a(0, a0);
-        issue_b(0, 0);
-        issue_b(min(1, nst - 1), 1);
+        // the loads of stages -max(ahead, sps) .. -1 of the steady-state pattern below
+#pragma unroll
+        for (int s = -(Sh::ahead > Sh::sps ? Sh::ahead : Sh::sps); s < 0; ++s) {
+            if (gu_mod(s, Sh::sps) == 0 && s >= -Sh::sps) load_a(0, a0);
+            if (s >= -Sh::ahead) issue_b(min(s + Sh::ahead, nst - 1), s + Sh::ahead);
+        }
         // the two stages of stretch q, whose weights are in cur; the next stretch loads into nxt
         auto stretch = [&](int q, const ARegs& cur, ARegs& nxt) {
 #pragma unroll
             for (int h = 0; h < Sh::sps; ++h) {
                 const int st = Sh::sps * q + h;
-                // loads issued after B stage st: B stage st + 1, and A stretch q + 1 when h = 1 (issued at
-                // stage st - 1, the stretch's first); none other may stay outstanding
-                if (h == 1) wait_vm<gu_wait(1, kDB, kDA)>();
-                else wait_vm<gu_wait(0, kDB, kDA)>();
+                // loads issued after B stage st (by stages st - ahead + 1 .. st - 1) may stay outstanding
+                switch (h) {
+                    case 0: wait_vm<gu_wait(0, Sh::ahead, Sh::sps, kDB, kDA)>(); break;
+                    case 1: wait_vm<gu_wait(1, Sh::ahead, Sh::sps, kDB, kDA)>(); break;
+                    case 2: wait_vm<gu_wait(2, Sh::ahead, Sh::sps, kDB, kDA)>(); break;
+                    default: wait_vm<gu_wait(3, Sh::ahead, Sh::sps, kDB, kDA)>(); break;
+                }
                 ring_barrier();   // stage st is in LDS for every wave; every wave is done with stage st - 1
                 if (h == 0) load_a(min(q + 1, nq - 1), nxt);
-                issue_b(min(st + 2, nst - 1), (st + 2) % kStages);   // into stage st - 1's slot
+                issue_b(min(st + Sh::ahead, nst - 1), (st + Sh::ahead) % Sh::stages);   // into stage st - 1's slot
 #pragma unroll
                 for (int t = 0; t < Sh::ksps; ++t) {
                     half8 bv[4][NP];
