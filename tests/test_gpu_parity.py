@@ -361,6 +361,35 @@ def test_layer_prefill_repeatable(F):
             assert torch.equal(cur, first), i
 
 
+def test_layer_prefill_graph_replays(F):
+    """The prefill layer (router GEMM, top-k, dispatch, grouped GEMMs, combine) captured in a HIP
+    graph replays to the eager result, bit for bit, on three replays with eager work and
+    synchronizations between them (no fill node of the library's own in the graph)."""
+    T = 2048
+    bias = O.gen_zipf_bias(3, 0, H.E, H.ZIPF_S_PREFILL, H.PREFILL_ALPHA)
+    w3 = H.World(cfg=3, bias=bias)
+    xt = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    F.gen.normal(xt, 3, 0, O.X_TENSOR, 1.0, round_bf16=True)
+    ws = w3.layer_obj.workspace(T)
+    ref = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    w3.layer_obj.forward(xt, ref, T=T, ws=ws)
+    torch.cuda.synchronize()
+    out = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        w3.layer_obj.forward(xt, out, T=T, ws=ws, stream=s)
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), i
+        w3.layer_obj.forward(xt, ref, T=T, ws=ws)   # eager work between the replays
+        torch.cuda.synchronize()
+
+
 def test_layer_mixed_config4(F):
     """Config 4: an 8192-token bf16 prefill chunk plus 16 uncorrelated fp32 decode tokens in one
     launch (T = 8208), with adversarial popularity: +2.8 on the logits of 16 seeded hot experts puts
