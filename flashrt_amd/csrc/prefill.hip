@@ -323,19 +323,6 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
-// s_waitcnt vmcnt(n) for a run-time n in 0..31
-__device__ __forceinline__ void wait_vm_dyn(int n) {
-    switch (n) {
-#define FRT_WAIT_CASE(k) \
-    case k: wait_vm<k>(); break;
-        FRT_WAIT_CASE(0) FRT_WAIT_CASE(1) FRT_WAIT_CASE(2) FRT_WAIT_CASE(3) FRT_WAIT_CASE(4) FRT_WAIT_CASE(5)
-        FRT_WAIT_CASE(6) FRT_WAIT_CASE(7) FRT_WAIT_CASE(8) FRT_WAIT_CASE(9) FRT_WAIT_CASE(10) FRT_WAIT_CASE(11)
-        FRT_WAIT_CASE(12) FRT_WAIT_CASE(13) FRT_WAIT_CASE(14) FRT_WAIT_CASE(15)
-#undef FRT_WAIT_CASE
-        default: wait_vm<0>(); break;
-    }
-}
-
 // (x & mask) | bits as one v_and_or_b32 (with literal operands the compiler splits it in two)
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
     uint32_t r;
@@ -403,6 +390,7 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
     // XCD L % 8, so the slices of a tile are placed 8 apart: they run on the same XCD at about the same
     // time, and the tile's activations come into that XCD's L2 once.
     const int gx = ff / Sh::ff_rows;
+    const int ffp = (ff + 255) & ~255;   // h row length
     const int L = blockIdx.x, r8 = L >> 3;
     const int slice = r8 % gx, t = (L & 7) + 8 * (r8 / gx);
     // n_tiles[0]: tiles in all; n_tiles[1]: the first tile of one token column (the list is ordered
@@ -585,8 +573,18 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
                 for (int r = 0; r < 4; ++r) {
                     const int f = fbase + 16 * i + 4 * lg + r;
                     const float a = float(q8_code(hv[i][r], id)) * dr;
-                    hout[row * ff + (f & ~255) + perm256_pos(f & 255)] = _Float16(a);
+                    hout[row * ffp + (f & ~255) + perm256_pos(f & 255)] = _Float16(a);
                 }
+        }
+    }
+    // h rows are ffp = ff rounded up to 256 long (whole perm256 stretches for the down GEMM); the
+    // slice holding the last rows also writes zeros at the pad's positions, so that the down GEMM's
+    // products there are 0 (its weights for the pad are any finite values of the row)
+    if (ffp > ff && rbase + Sh::ff_rows >= ff) {
+        const int np = ffp - ff;   // pad elements per row: f = ff .. ffp - 1
+        for (int i = tid; i < cnt * np; i += Sh::threads) {
+            const int col = i / np, f = ff + i % np;
+            hout[size_t(row0 + col) * ffp + (f & ~255) + perm256_pos(f & 255)] = _Float16(0.0f);
         }
     }
     FRT_PROBE(0, 2);
@@ -594,22 +592,25 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
 }
 
 // k_pf_down: the down GEMM, one workgroup (256 threads) per tile. The tile's activations (h of 64
-// dispatched rows, all of K = ff, perm256 order) are loaded into LDS once (64 tokens x ff fp16; chunk
-// kc of token j at j * ff / 8 + (kc ^ (j & 15))), then the workgroup walks all n output rows in blocks
+// dispatched rows, all of K = ffp = ff rounded up to 256, perm256 order, zeros in the pad) are loaded
+// into LDS once (64 tokens x ffp fp16; chunk kc of token j at j * ffp / 8 + (kc ^ (j & 15))), then
+// the workgroup walks all n output rows in blocks
 // of 256 (wave w: rows 64 w + 16 i + li of the block), streaming the weights straight into
 // registers with three stretches of lookahead (four register sets). No barrier after the
 // activation load: each wave reads only its own weights. Two workgroups share a CU (64 KB of LDS
-// each for ff = 512), so one computes while the other waits for loads. NQ = ff / 256 stretches per
-// row block.
-template <int NQ>
+// each for ff = 512), so one computes while the other waits for loads. NQ = ffp / 256 stretches per
+// row block; a weight block past the row's last (the pad) is read as the row's last block, whose
+// finite products with the pad's zeros are 0. TAIL: the stretch count is not a multiple of 4, and
+// the last round of 4 steps has steps past the end (loads repeated, no products).
+template <int NQ, bool TAIL>
 __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ arena, size_t stride, int E,
-                                                 const uint8_t* __restrict__ shared_blob, int n,
+                                                 const uint8_t* __restrict__ shared_blob, int n, int ff,
                                                  const _Float16* __restrict__ h, const int32_t* __restrict__ bounds,
                                                  const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
                                                  float* __restrict__ yd, const int32_t* __restrict__ slot_of) {
-    constexpr int ff = NQ * 256;
-    constexpr int nbk = ff / kBlock;   // weight blocks per row
-    constexpr int cpt = ff / 8;        // 16-byte activation chunks per token
+    constexpr int ffp = NQ * 256;      // h row length
+    const int nbk = ff / kBlock;       // weight blocks per row
+    constexpr int cpt = ffp / 8;       // 16-byte activation chunks per token
     constexpr int kDB = kTN * cpt / 256;   // activation loads per lane
     if (int(blockIdx.y) >= *n_tiles) return;
     extern __shared__ __align__(16) uint8_t smem[];
@@ -630,19 +631,19 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
 #pragma unroll
     for (int p = 0; p < kDB; ++p) {
         const int P = 256 * p + tid, j = P / cpt, kc = (P % cpt) ^ (j & 15);
-        ldsdma16(h + size_t(sRow[j]) * ff + kc * 8, smem + P * 16 - lane * 16);
+        ldsdma16(h + size_t(sRow[j]) * ffp + kc * 8, smem + P * 16 - lane * 16);
     }
 
-    uint32_t aoff[4];   // chunk index of block lg of stretch 0 of row block 0 for tile i
+    uint32_t aoff[4];   // chunk index of block 0 of this lane's row in row block 0, for tile i
 #pragma unroll
-    for (int i = 0; i < 4; ++i) aoff[i] = uint32_t(64 * wave + 16 * i + li) * nbk + lg;
+    for (int i = 0; i < 4; ++i) aoff[i] = uint32_t(64 * wave + 16 * i + li) * nbk;
     struct ARegs {
         uint4 cw[4];
         uint32_t sc[4];
     };
-    const int nsx = (n / 256) * NQ;   // stretches in all (a multiple of 4: n % 1024 == 0)
+    const int nsx = (n / 256) * NQ;   // stretches in all (a multiple of 4 unless TAIL)
     auto load_a = [&](int s, ARegs& a) {   // stretch s: row block s / NQ, blocks 4 (s % NQ) + lg
-        const size_t base = size_t(s / NQ) * 256 * nbk + 4 * (s % NQ);
+        const size_t base = size_t(s / NQ) * 256 * nbk + min(4 * (s % NQ) + lg, nbk - 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             a.cw[i] = gld_u4(md + (base + aoff[i]) * 16);
@@ -672,6 +673,7 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
         // past the end, so every stretch has the same loads in flight)
         auto step = [&](int s, int q, const ARegs& cur, ARegs& nxt) {
             load_a(min(s + 3, nsx - 1), nxt);
+            if (TAIL && s >= nsx) return;   // past the end (uniform)
 #pragma unroll
             for (int tt = 0; tt < 8; ++tt) {
                 half8 bv[4];
@@ -709,11 +711,13 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
                 }
             }
         };
+        // the stretch's place in its row block: a constant per unrolled step when NQ divides 4
+        auto qof = [&](int s, int i) { return 4 % NQ == 0 ? i % NQ : s % NQ; };
         for (int s = 0; s < nsx; s += 4) {
-            step(s, 0 % NQ, a0, a3);
-            step(s + 1, 1 % NQ, a1, a0);
-            step(s + 2, 2 % NQ, a2, a1);
-            step(s + 3, 3 % NQ, a3, a2);
+            step(s, qof(s, 0), a0, a3);
+            step(s + 1, qof(s + 1, 1), a1, a0);
+            step(s + 2, qof(s + 2, 2), a2, a1);
+            step(s + 3, qof(s + 3, 3), a3, a2);
         }
     };
     switch ((cnt + 15) / 16) {   // token columns with at least one real token
@@ -792,8 +796,8 @@ __global__ void k_to_bf16(const float* __restrict__ src, __hip_bfloat16* __restr
 struct PfWs {
     int32_t *cnt, *bounds, *tok_of, *slot_of, *n_tiles;
     int2* tiles;
-    _Float16 *xhi, *xlo;   // x = code * d as an exact fp16 pair, perm64 order [T][n]
-    _Float16* h16;         // h = code * d as fp16, perm64 order [S][ff]
+    _Float16 *xhi, *xlo;   // x = code * d as an exact fp16 pair, perm256 order [T][n]
+    _Float16* h16;         // h = code * d as fp16, perm256 order [S][ffp], ffp = ff rounded up to 256
     float* yd;   // fp32 per-slot outputs when the caller does not receive them as fp32
     size_t bytes;
 };
@@ -819,7 +823,7 @@ static PfWs pf_carve(void* base, int T, int K, int n, int ff, int E, bool shared
     w.tiles = reinterpret_cast<int2*>(take(size_t(pf_max_tiles(S, G)) * 8));
     w.xhi = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
     w.xlo = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
-    w.h16 = reinterpret_cast<_Float16*>(take(size_t(S) * ff * 2));
+    w.h16 = reinterpret_cast<_Float16*>(take(size_t(S) * ((ff + 255) & ~255) * 2));
     w.yd = own_yd ? reinterpret_cast<float*>(take(size_t(S) * n * 4)) : nullptr;
     w.bytes = size_t(p - static_cast<uint8_t*>(base));
     return w;
@@ -834,10 +838,11 @@ int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16
 
 int pf_check(int T, int K, int n, int ff, int E) {
     if (T < 1 || K < 1 || K > 32 || E < 1 || E > 4096 || K > E) return set_error(kErrShape, "prefill: T=%d K=%d E=%d", T, K, E);
-    // gate/up: whole pairs of 256-element weight stretches; down: the tile's h in LDS (ff <= 1024),
-    // weight stretches in fours
-    if (n % 1024 || n < 1024 || (ff != 512 && ff != 1024))
-        return set_error(kErrShape, "prefill: n=%d ff=%d (n a multiple of 1024; ff 512 or 1024)", n, ff);
+    // gate/up: whole pairs of 256-element weight stretches along n, slices of 128 ff rows; down: the
+    // tile's h (ff rounded up to 256) in LDS, at most 1024
+    if (n % 512 || n < 512 || ff % 128 || ff < 128 || ff > 1024)
+        return set_error(kErrShape, "prefill: n=%d ff=%d (n a multiple of 512; ff a multiple of 128 up to 1024)", n,
+                         ff);
     return kOk;
 }
 
@@ -852,11 +857,11 @@ static int pf_gemm_attr() {
     return kOk;
 }
 
-template <int NQ>
+template <int NQ, bool TAIL>
 static int pf_down_attr(size_t lds) {
     static bool done = false;
     if (!done) {
-        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_down<NQ>),
+        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_down<NQ, TAIL>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
         done = true;
     }
@@ -880,18 +885,19 @@ static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uin
                  (const _Float16*)w.xlo, (const int32_t*)w.tok_of, (const int32_t*)w.bounds, (const int2*)w.tiles,
                  (const int32_t*)w.n_tiles, w.h16);
     timing_mark(stream, "pf_gateup");
-    const size_t down_lds = size_t(kTN) * ff * 2;   // the tile's activations
-    if (ff == 512) {
-        if (int rc = pf_down_attr<2>(down_lds)) return rc;
-        launch_timed("pf_down", k_pf_down<2>, dim3(1, mt), dim3(256), down_lds, stream, arena, stride, E, shared_blob,
-                     n, (const _Float16*)w.h16, (const int32_t*)w.bounds, (const int2*)w.tiles,
-                     (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of);
-    } else {
-        if (int rc = pf_down_attr<4>(down_lds)) return rc;
-        launch_timed("pf_down", k_pf_down<4>, dim3(1, mt), dim3(256), down_lds, stream, arena, stride, E, shared_blob,
-                     n, (const _Float16*)w.h16, (const int32_t*)w.bounds, (const int2*)w.tiles,
-                     (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of);
+    const int nq = (ff + 255) / 256;                     // stretches per h row
+    const size_t down_lds = size_t(kTN) * nq * 256 * 2;  // the tile's activations
+    const bool tail = (n / 256) * nq % 4 != 0;
+#define FRT_PF_DOWN(NQV, TL)                                                                                 \
+    if (nq == NQV && tail == TL) {                                                                           \
+        if (int rc = pf_down_attr<NQV, TL>(down_lds)) return rc;                                             \
+        launch_timed("pf_down", k_pf_down<NQV, TL>, dim3(1, mt), dim3(256), down_lds, stream, arena, stride, E, \
+                     shared_blob, n, ff, (const _Float16*)w.h16, (const int32_t*)w.bounds, (const int2*)w.tiles, \
+                     (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of);                             \
     }
+    FRT_PF_DOWN(1, false) FRT_PF_DOWN(1, true) FRT_PF_DOWN(2, false) FRT_PF_DOWN(2, true)
+    FRT_PF_DOWN(3, false) FRT_PF_DOWN(3, true) FRT_PF_DOWN(4, false) FRT_PF_DOWN(4, true)
+#undef FRT_PF_DOWN
     return kOk;
 }
 

@@ -190,6 +190,21 @@ def test_layer_decode_config0(F, w0):
     assert H.out_rel(out, ref) <= H.OUT_REL
 
 
+def test_layer_reference_test_shape(F):
+    """The reference tests' shape, d_model 2560 and expert ff 640 (tests/test_moe_q2.cpp:68-153),
+    through the whole layer: decode at T = 1 and 3 and prefill at T = 128, every token's ids,
+    weights and outputs against the oracle."""
+    w = H.World(cfg=0, n=2560, ff=640)
+    rng = np.random.default_rng(2560)
+    for T in (1, 3, 128):
+        x = rng.standard_normal((T, 2560)).astype(np.float32)
+        out, ids, wts = w.gpu_forward(x)
+        ref, rid, rw, _ = w.oracle_forward(x)
+        assert np.array_equal(ids, rid), T
+        assert H.w_rel(wts, rw) <= H.W_REL, T
+        assert H.out_rel(out, ref) <= H.OUT_REL, T
+
+
 def test_layer_decode_config1_window(F):
     w1 = H.World(cfg=1)
     xc = torch.empty((3, H.N), dtype=torch.float32, device="cuda")
@@ -277,12 +292,15 @@ def test_moe_q2_run(F, w0, yd_bf16):
         F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, nb, None, True)
 
 
-@pytest.mark.parametrize("n,ff,T,K,E", [(1024, 1024, 40, 4, 6), (2048, 512, 8, 2, 8), (1024, 512, 200, 3, 4)])
+@pytest.mark.parametrize("n,ff,T,K,E", [(1024, 1024, 40, 4, 6), (2048, 512, 8, 2, 8), (1024, 512, 200, 3, 4),
+                                         (2560, 640, 90, 4, 6), (512, 128, 70, 2, 3), (1536, 384, 50, 3, 5)])
 def test_moe_q2_run_shapes(F, n, ff, T, K, E):
     """moe_q2::run at other shapes and tile mixes, every slot against the oracle's expert_ffn:
     ff = 1024 (four weight stretches per down row block, a 128 KB tile in LDS) with n = 1024 and about
     27 rows per expert (two-column tiles); only one-column tiles (T = 8, K = 2 over 8 experts); full
-    64-row tiles next to partial ones (T = 200, K = 3 over 4 experts)."""
+    64-row tiles next to partial ones (T = 200, K = 3 over 4 experts); ff not a multiple of 256 (the
+    h rows padded to whole stretches: 640 = the reference tests' 2560 / 640 shape, with a stretch
+    count that is not a multiple of 4; 128; 384) and n = 512 and 1536."""
     w = H.World(cfg=0, n=n, ff=ff, E=E, K=K)
     rng = np.random.default_rng(n + ff + T)
     x = rng.standard_normal((T, n)).astype(np.float32)
@@ -301,13 +319,14 @@ def test_moe_q2_run_shapes(F, n, ff, T, K, E):
 
 
 def test_moe_q2_run_shape_errors(F, w0):
-    """The grouped GEMMs' shape limits (n a multiple of 1024, ff 512 or 1024) fail loudly."""
+    """The grouped GEMMs' shape limits (n a multiple of 512; ff a multiple of 128 up to 1024) fail
+    loudly."""
     T, K = 4, 2
     x = torch.zeros((T, 2048), dtype=torch.float32, device="cuda")
     ids = torch.zeros((T, K), dtype=torch.int32, device="cuda")
     ids[:, 1] = 1
     yd = torch.empty((T * K, 2048), dtype=torch.float32, device="cuda")
-    for n, ff in ((2048, 768), (1536, 512)):
+    for n, ff in ((2048, 704), (1280, 512), (2048, 1152), (256, 512)):
         nb = F.moe_q2.workspace_bytes(T, K, n, ff, 8)
         ws = torch.empty(max(nb, 1 << 20), dtype=torch.uint8, device="cuda")
         with pytest.raises(F.FrtError) as e:
