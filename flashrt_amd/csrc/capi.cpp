@@ -103,9 +103,16 @@ void gen_zipf_bias(uint64_t seed, int cfg, int layer, int E, float s, float alph
 
 constexpr int kDecodeMaxT = 4;
 
-// decode-side scratch for moe_hits: x quantized (T rows) ahead of dec scratch
+// moe_hits runs a window in chunks of at most hits_chunk(T, K) tokens (the grouped decode kernels
+// take T <= 4 and T * K <= 63); each chunk reads each of its distinct blobs once
+static int hits_chunk(int T, int K) {
+    int c = 63 / (K > 0 ? K : 1);
+    if (c > kDecodeMaxT) c = kDecodeMaxT;
+    return T < c ? T : c;
+}
+// decode-side scratch for moe_hits: x quantized (T rows) ahead of the dec scratch of one chunk
 static size_t hits_bytes(int K, int ff, int T, int n) {
-    return up256(size_t(T) * n) + up256(size_t(T) * (n / kQ8) * 4) + dec_scratch_bytes(T, K, ff);
+    return up256(size_t(T) * n) + up256(size_t(T) * (n / kQ8) * 4) + dec_scratch_bytes(hits_chunk(T, K), K, ff);
 }
 
 struct LayerWs {
@@ -279,7 +286,9 @@ size_t frt_moe_hits_scratch_bytes(int K, int ff, int T, int n) { return hits_byt
 int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const float* x, int n, int ff,
                  void* scratch, float* yh, void* stream, int T) {
     if (!hit_ptr || !hit_n || !x || !scratch || !yh) return set_error(kErrNull, "moe_hits: null pointer");
-    if (int rc = dec_check(T, K, n, ff)) return rc;
+    if (T < 1 || K < 1 || K > 32) return set_error(kErrShape, "moe_hits: T=%d K=%d", T, K);
+    const int tc = hits_chunk(T, K);
+    if (int rc = dec_check(tc, K, n, ff)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint8_t* p = static_cast<uint8_t*>(scratch);
     int8_t* xq = reinterpret_cast<int8_t*>(p);
@@ -287,7 +296,13 @@ int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, con
     float* xd = reinterpret_cast<float*>(p);
     p += up256(size_t(T) * (n / kQ8) * 4);
     if (int rc = quantize_q8(x, T, n, xq, xd, nullptr, nullptr, s)) return rc;
-    return dec_hits(hit_ptr, hit_n, K, xq, xd, n, ff, p, yh, s, T);
+    for (int t0 = 0; t0 < T; t0 += tc) {   // chunks in stream order share the dec scratch
+        const int tn = T - t0 < tc ? T - t0 : tc;
+        if (int rc = dec_hits(hit_ptr + size_t(t0) * K, hit_n + t0, K, xq + size_t(t0) * n, xd + size_t(t0) * (n / kQ8),
+                              n, ff, p, yh + size_t(t0) * K * n, s, tn))
+            return rc;
+    }
+    return kOk;
 }
 
 size_t frt_moe_layer_workspace_bytes(const frt_moe_layer* L, int T) {

@@ -100,7 +100,8 @@ int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, 
 /* ---- decode expert GEMVs (arch/qwen4exp/moe_fast.hpp:134-142 moe_hits_scratch_bytes, moe_hits).
  * yh [T][K][n]: entry (t, k) for k < hit_n[t] = down(silu(gate x) * up x) of the blob at
  * hit_ptr[t*K + k] (device array of device pointers); entries k >= hit_n[t] are not written.
- * x [T][n] fp32, T <= 4 (each distinct blob read once for the window, moe_fast.cu:195-355).
+ * x [T][n] fp32, any T >= 1: windows of up to min(4, 63 / K) tokens read each distinct blob once
+ * (moe_fast.cu:195-355); a longer window runs in such chunks, one after the other on the stream.
  * Activations are quantized to Q8_0 per 32 (the reference quantizes per 64 here). */
 size_t frt_moe_hits_scratch_bytes(int K, int ff, int T, int n);
 int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const float* x, int n, int ff,

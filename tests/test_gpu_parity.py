@@ -263,6 +263,34 @@ def test_moe_hits(F, w0):
         assert np.array_equal(a, y[t, :hit_n[t]])
 
 
+@pytest.mark.parametrize("T,K", [(8, 10), (5, 32)])
+def test_moe_hits_long_windows(F, w0, T, K):
+    """Windows longer than one grouped launch takes (T = 8 = the reference's kMaxWindow,
+    moe_fast.cu:38; with K = 32 a chunk holds one token) run in chunks: every slot against the
+    oracle, pad slots untouched, and each token equal to its one-token call bit for bit."""
+    rng = np.random.default_rng(T * K)
+    x = rng.standard_normal((T, H.N)).astype(np.float32)
+    hit_n = rng.integers(1, K + 1, size=T).astype(np.int32)
+    experts = rng.choice(512, size=(T, K), replace=True).astype(np.int64)
+    experts[1:, :3] = experts[0, :3]   # shared across the window's chunks
+    base = w0.arena.data_ptr()
+    ptr = torch.tensor((base + experts * w0.stride).reshape(-1), dtype=torch.int64, device="cuda")
+    yh = torch.full((T, K, H.N), float("nan"), dtype=torch.float32, device="cuda")
+    scratch = torch.empty(F.moe_hits_scratch_bytes(K, H.FF, T, H.N), dtype=torch.uint8, device="cuda")
+    F.moe_hits(ptr, dev(hit_n), K, dev(x), H.N, H.FF, scratch, yh, T=T)
+    torch.cuda.synchronize()
+    y = yh.cpu().numpy()
+    for t in range(T):
+        assert np.isnan(y[t, hit_n[t]:]).all()
+        for k in range(hit_n[t]):
+            ref = O.expert_ffn(w0.blob(int(experts[t, k])), H.N, H.FF, x[t])
+            assert H.out_rel(y[t, k][None], ref) <= H.OUT_REL, (t, k)
+        y1 = torch.full((1, K, H.N), float("nan"), dtype=torch.float32, device="cuda")
+        F.moe_hits(ptr[t * K:(t + 1) * K], dev(hit_n[t:t + 1]), K, dev(x[t:t + 1]), H.N, H.FF, scratch, y1, T=1)
+        torch.cuda.synchronize()
+        assert np.array_equal(y1.cpu().numpy()[0, :hit_n[t]], y[t, :hit_n[t]]), t
+
+
 # ---------------------------------------------------------------- prefill path
 
 @pytest.mark.parametrize("yd_bf16", [False, True])
