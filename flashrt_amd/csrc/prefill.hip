@@ -7,7 +7,8 @@
 //   k_pf_place  one wave per chunk walks its slots in order, 64 at a time; each lane's rank among
 //               equal experts in the batch comes from ballots (a wave64 match-any), so the
 //               placement is stable and needs no atomics.
-//   The shared expert, when present, is group E holding every token in order (rows T*K + t).
+//   The shared expert, when present, is group E holding every token in order (rows T*K + t, written
+//   by the workgroups of k_pf_place past the chunks).
 //
 // GEMMs (k_pf_gemm, below): Q2_0 weights dequantized exactly to fp16 in registers, activations
 // as exact fp16 (hi, lo) pairs (gate/up) or fp16 (down), fp32 accumulation on MFMA; tiles of 64
@@ -166,9 +167,18 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
 // one wave per chunk; stable ranks from a ballot match-any over the expert id bits
 __global__ void __launch_bounds__(64) k_pf_place(const int32_t* __restrict__ ids, int S, int K, int E, int id_bits,
                                                  const int32_t* __restrict__ cnt, int32_t* __restrict__ tok_of,
-                                                 int32_t* __restrict__ slot_of) {
+                                                 int32_t* __restrict__ slot_of, int shared_T) {
     extern __shared__ int32_t next[];
     const int lane = threadIdx.x;
+    const int nchunk = (S + kChunk - 1) / kChunk;
+    if (int(blockIdx.x) >= nchunk) {   // the workgroups past the chunks: the shared group's rows S + t
+        const int t = (int(blockIdx.x) - nchunk) * 64 + lane;
+        if (t < shared_T) {
+            tok_of[S + t] = t;
+            slot_of[S + t] = S + t;
+        }
+        return;
+    }
     for (int e = lane; e < E; e += 64) next[e] = cnt[size_t(blockIdx.x) * E + e];
     __syncthreads();
     const int s0 = blockIdx.x * kChunk, s1 = min(S, s0 + kChunk);
@@ -192,14 +202,6 @@ __global__ void __launch_bounds__(64) k_pf_place(const int32_t* __restrict__ ids
             if (rank == 0) next[e] += __popcll(peers);   // the first lane of each expert
         }
         __syncthreads();
-    }
-}
-
-__global__ void k_pf_place_shared(int T, int K, int32_t* __restrict__ tok_of, int32_t* __restrict__ slot_of) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t < T) {
-        tok_of[T * K + t] = t;
-        slot_of[T * K + t] = T * K + t;
     }
 }
 
@@ -914,10 +916,11 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
     while ((1 << id_bits) < E) ++id_bits;
     if (int rc = quantize_q8(x, T, n, nullptr, nullptr, w.xhi, w.xlo, stream)) return rc;
     timing_mark(stream, "pf_quant_x");
-    k_pf_hist<<<nchunk, 256, size_t(E) * 4, stream>>>(ids, T * K, E, w.cnt);
-    k_pf_scan<<<1, 1024, 0, stream>>>(w.cnt, nchunk, E, T, K, shared ? 1 : 0, w.bounds, w.tiles, w.n_tiles);
-    k_pf_place<<<nchunk, 64, size_t(E) * 4, stream>>>(ids, T * K, K, E, id_bits, w.cnt, w.tok_of, w.slot_of);
-    if (shared) k_pf_place_shared<<<(T + 255) / 256, 256, 0, stream>>>(T, K, w.tok_of, w.slot_of);
+    launch_timed("pf_hist", k_pf_hist, dim3(nchunk), dim3(256), size_t(E) * 4, stream, ids, T * K, E, w.cnt);
+    launch_timed("pf_scan", k_pf_scan, dim3(1), dim3(1024), 0, stream, w.cnt, nchunk, E, T, K, shared ? 1 : 0, w.bounds,
+                 w.tiles, w.n_tiles);
+    launch_timed("pf_place", k_pf_place, dim3(nchunk + (shared ? (T + 63) / 64 : 0)), dim3(64), size_t(E) * 4, stream,
+                 ids, T * K, K, E, id_bits, w.cnt, w.tok_of, w.slot_of, shared ? T : 0);
     timing_mark(stream, "pf_dispatch");
     const int mt = pf_max_tiles(S, G);
     float* ydf = yd_kind == 1 ? w.yd : static_cast<float*>(yd);
@@ -974,7 +977,7 @@ int pf_dispatch(const int32_t* ids, int T, int K, int E, int32_t* bounds, int32_
     while ((1 << id_bits) < E) ++id_bits;
     k_pf_hist<<<nchunk, 256, size_t(E) * 4, stream>>>(ids, T * K, E, cnt);
     k_pf_scan<<<1, 1024, 0, stream>>>(cnt, nchunk, E, T, K, 0, bounds, tiles, n_tiles);
-    k_pf_place<<<nchunk, 64, size_t(E) * 4, stream>>>(ids, T * K, K, E, id_bits, cnt, tok_of, slot_of);
+    k_pf_place<<<nchunk, 64, size_t(E) * 4, stream>>>(ids, T * K, K, E, id_bits, cnt, tok_of, slot_of, 0);
     FRT_LAUNCHED("dispatch");
     return kOk;
 }
