@@ -46,30 +46,46 @@ __global__ void __launch_bounds__(256) k_pf_hist(const int32_t* __restrict__ ids
     for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[size_t(blockIdx.x) * E + e] = h[e];
 }
 
-__device__ __forceinline__ int block_excl_scan(int v, int* total, int* ws) {
+// Exclusive prefix sums over the workgroup of N ints per thread at once (and the totals): a shuffle
+// scan within each wave, then wave 0 scans the wave totals in parallel. ws: (nwaves + 1) * N ints.
+template <int N>
+__device__ __forceinline__ void block_excl_scan_v(const int (&v)[N], int (&r)[N], int (&total)[N], int* ws) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    int incl = v;
+    int incl[N];
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-    }
-    if (lane == 63) ws[wave] = incl;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int w = 0; w < nw; ++w) {
-            const int x = ws[w];
-            ws[w] = run;
-            run += x;
+    for (int i = 0; i < N; ++i) incl[i] = v[i];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1)
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int y = __shfl_up(incl[i], o, 64);
+            if (lane >= o) incl[i] += y;
         }
-        ws[nw] = run;
+    if (lane == 63)
+#pragma unroll
+        for (int i = 0; i < N; ++i) ws[wave * N + i] = incl[i];
+    __syncthreads();
+    if (wave == 0) {   // the wave totals: lane w < nw holds wave w's, scanned across the lanes
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int x = lane < nw ? ws[lane * N + i] : 0;
+            int c = x;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const int y = __shfl_up(c, o, 64);
+                if (lane >= o) c += y;
+            }
+            if (lane < nw) ws[lane * N + i] = c - x;
+            if (lane == nw - 1) ws[nw * N + i] = c;
+        }
     }
     __syncthreads();
-    const int r = ws[wave] + incl - v;
-    *total = ws[nw];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        r[i] = ws[wave * N + i] + incl[i] - v[i];
+        total[i] = ws[nw * N + i];
+    }
     __syncthreads();
-    return r;
 }
 
 // 1024 threads. cnt [nchunk][E] becomes each chunk's first row per expert (absolute).
@@ -80,7 +96,8 @@ __device__ __forceinline__ int tile_class(int rows) { return (rows + 15) / 16; }
 __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int nchunk, int E, int T, int K, int shared,
                                                   int32_t* __restrict__ bounds, int2* __restrict__ tiles,
                                                   int32_t* __restrict__ n_tiles) {
-    __shared__ int ws[17];
+    __shared__ int ws[17 * 5];
+    static_assert(1024 / 64 <= 16, "the wave-total scan covers 16 waves");
     // tiles of each class of group e (rows c): c / 64 full tiles (class 4) and one of class (c % 64)
     auto count = [&](int c, int (&n)[5]) {
         n[1] = n[2] = n[3] = n[4] = 0;
@@ -99,11 +116,10 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
         const int e = e0 + threadIdx.x;
         int n[5];
         count(e < E ? group_rows(e) : 0, n);
-        for (int k = 1; k <= 4; ++k) {
-            int tot;
-            block_excl_scan(n[k], &tot, ws);
-            total[k] += tot;
-        }
+        const int v[4] = {n[1], n[2], n[3], n[4]};
+        int r[4], tot[4];
+        block_excl_scan_v<4>(v, r, tot, ws);
+        for (int k = 1; k <= 4; ++k) total[k] += tot[k - 1];
     }
     int sh[5] = {0, 0, 0, 0, 0};
     if (shared) {
@@ -118,14 +134,15 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
     for (int e0 = 0; e0 < E; e0 += blockDim.x) {
         const int e = e0 + threadIdx.x;
         const int c = e < E ? group_rows(e) : 0;
-        int tot_rows;
-        const int off = block_excl_scan(c, &tot_rows, ws) + run_rows;
         int n[5], at[5];
         count(c, n);
+        const int v[5] = {c, n[1], n[2], n[3], n[4]};
+        int r[5], tot[5];
+        block_excl_scan_v<5>(v, r, tot, ws);
+        const int off = r[0] + run_rows, tot_rows = tot[0];
         for (int k = 1; k <= 4; ++k) {
-            int tot;
-            at[k] = block_excl_scan(n[k], &tot, ws) + base[k];
-            base[k] += tot;
+            at[k] = r[k] + base[k];
+            base[k] += tot[k];
         }
         if (e < E) {
             bounds[e] = off;
