@@ -97,6 +97,7 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
                                                   int32_t* __restrict__ bounds, int2* __restrict__ tiles,
                                                   int32_t* __restrict__ n_tiles) {
     __shared__ int ws[17 * 5];
+    __shared__ int s_rows[4096];   // each group's rows from pass 1 (E <= 4096)
     static_assert(1024 / 64 <= 16, "the wave-total scan covers 16 waves");
     // tiles of each class of group e (rows c): c / 64 full tiles (class 4) and one of class (c % 64)
     auto count = [&](int c, int (&n)[5]) {
@@ -115,7 +116,9 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
     for (int e0 = 0; e0 < E; e0 += blockDim.x) {
         const int e = e0 + threadIdx.x;
         int n[5];
-        count(e < E ? group_rows(e) : 0, n);
+        const int c = e < E ? group_rows(e) : 0;
+        if (e < E) s_rows[e] = c;
+        count(c, n);
         const int v[4] = {n[1], n[2], n[3], n[4]};
         int r[4], tot[4];
         block_excl_scan_v<4>(v, r, tot, ws);
@@ -133,7 +136,7 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
     int run_rows = 0;
     for (int e0 = 0; e0 < E; e0 += blockDim.x) {
         const int e = e0 + threadIdx.x;
-        const int c = e < E ? group_rows(e) : 0;
+        const int c = e < E ? s_rows[e] : 0;   // (written by this thread in pass 1)
         int n[5], at[5];
         count(c, n);
         const int v[5] = {c, n[1], n[2], n[3], n[4]};
