@@ -722,7 +722,10 @@ __device__ __forceinline__ float combine_list(const DecComb& C, int K, int t, in
 
 // ---- down for 8 output rows x every entry, then the combine. NBF = ff / 64 (8 lanes per row
 // when ff = 512). 256 threads; wave w takes entries w, w + 4, ...
-template <int NBF, bool MAYBE_EMPTY>
+// ONE: a single token's layer (T = 1, no per-slot outputs): its combine list is the entry list itself
+// (entry u = compact slot u, ascending expert id, the shared expert last, weight w[0]), so the list
+// is not staged and the sum reads the entries.
+template <int NBF, bool MAYBE_EMPTY, bool ONE>
 __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent_g, const int32_t* __restrict__ n_ent,
                                                   const DecComb* __restrict__ comb,
                                                   const int8_t* __restrict__ hq, const float* __restrict__ hd, int n,
@@ -756,14 +759,14 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent_g, const i
     Stage<int4, 3, 256> st_q;
     Stage<float, 2, 256> st_d;
     st_e.load(reinterpret_cast<const int4*>(ent_g), n_e);
-    st_c.load(reinterpret_cast<const int32_t*>(comb), n_c);
+    if (!ONE) st_c.load(reinterpret_cast<const int32_t*>(comb), n_c);
     st_q.load(reinterpret_cast<const int4*>(hq), n_q);
     st_d.load(hd, n_d);
     DownRegs<NBF, 4> R;
     down_load<NBF, 4>(ent_g, U, wave, r0, n, ff, R);   // global entry list (down_load reads it as global)
     __builtin_amdgcn_sched_barrier(0);
     st_e.store(reinterpret_cast<int4*>(s_ent), reinterpret_cast<const int4*>(ent_g), n_e);
-    if (!yh) st_c.store(reinterpret_cast<int32_t*>(&s_comb), reinterpret_cast<const int32_t*>(comb), n_c);
+    if (!ONE && !yh) st_c.store(reinterpret_cast<int32_t*>(&s_comb), reinterpret_cast<const int32_t*>(comb), n_c);
     st_q.store(reinterpret_cast<int4*>(sh_q), reinterpret_cast<const int4*>(hq), n_q);
     st_d.store(sh_d, hd, n_d);
     __syncthreads();
@@ -799,7 +802,17 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent_g, const i
         return;
     }
     if (ti < T) {
-        float o = combine_list(s_comb, K, ti, rli, sh_y);
+        float o;
+        if (ONE) {   // the combine_list order: the K routed entries from 0, then the shared one
+            float acc = 0.0f;
+            for (int u = 0; u < K; ++u) {
+                const float p = ent[u].w[0] * sh_y[u * RD + rli];
+                acc = acc + p;
+            }
+            o = acc + sh_y[K * RD + rli] * ent[K].w[0];
+        } else {
+            o = combine_list(s_comb, K, ti, rli, sh_y);
+        }
         if (resid) o = res + o;
         out[size_t(ti) * n + r0 + rli] = o;
     }
@@ -859,10 +872,13 @@ static int dec_down(const DecScratch& s, int n, int ff, int T, int K, const floa
 #define FRT_DN(NBFV)                                                                                           \
     case NBFV:                                                                                                 \
         if (yh)                                                                                                \
-            launch_timed("dec_down", k_dec_down<NBFV, true>, dim3(n / 8), dim3(256), smem, stream, s.ent, s.n_ent, \
-                         s.comb, s.hq, s.hd, n, ff, T, K, resid, out, yh, U_max, S, pf, pf_rows);                   \
+            launch_timed("dec_down", k_dec_down<NBFV, true, false>, dim3(n / 8), dim3(256), smem, stream, s.ent,  \
+                         s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid, out, yh, U_max, S, pf, pf_rows);          \
+        else if (T == 1)                                                                                       \
+            launch_timed("dec_down", k_dec_down<NBFV, false, true>, dim3(n / 8), dim3(256), smem, stream, s.ent,  \
+                         s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid, out, yh, U_max, S, pf, pf_rows);          \
         else                                                                                                   \
-            launch_timed("dec_down", k_dec_down<NBFV, false>, dim3(n / 8), dim3(256), smem, stream, s.ent,       \
+            launch_timed("dec_down", k_dec_down<NBFV, false, false>, dim3(n / 8), dim3(256), smem, stream, s.ent, \
                          s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid, out, yh, U_max, S, pf, pf_rows);          \
         break;
     switch (nbf) {
