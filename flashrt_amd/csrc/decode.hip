@@ -357,10 +357,41 @@ __global__ void k_hits_group(const uint8_t* const* __restrict__ hit_ptr, const i
 // With a down matrix `warm` (the entry's), the workgroup also loads the down rows that the down
 // kernel's workgroups on this XCD will read (down workgroup i runs on XCD i % 8, like this one on
 // XCD (linear id) % 8), so that their loads find them in this XCD's L2 rather than in HBM.
+// This lane's activation block (16 dwords of Q8_0 codes and the two block scales) for each token
+// slot of an entry: lane (row rsub, block b) reads block b (block 0 for a lane past the rows); a
+// token slot past ntok repeats token 0 (skipped where used).
+template <int MT>
+struct DecAct {
+    int xa[MT][16];
+    float xd0[MT], xd1[MT];
+};
+template <int NB, int MT>
+__device__ __forceinline__ void load_act(const int32_t* tok, int ntok, const int8_t* __restrict__ xq,
+                                         const float* __restrict__ xd, int n, DecAct<MT>& a) {
+    constexpr int RPW = (64 % NB == 0) ? 64 / NB : 1;
+    const int lane = threadIdx.x & 63;
+    const int bl = lane / NB < RPW ? lane % NB : 0;
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+        const int tj = tok[j < ntok ? j : 0];
+        const int4* src = reinterpret_cast<const int4*>(xq + size_t(tj) * n + bl * kBlock);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int4 v = src[q];
+            a.xa[j][4 * q + 0] = v.x;
+            a.xa[j][4 * q + 1] = v.y;
+            a.xa[j][4 * q + 2] = v.z;
+            a.xa[j][4 * q + 3] = v.w;
+        }
+        a.xd0[j] = xd[size_t(tj) * (n / kQ8) + 2 * bl];
+        a.xd1[j] = xd[size_t(tj) * (n / kQ8) + 2 * bl + 1];
+    }
+}
+
 template <int NB, int NW, int MT = kDecMaxT>
 __device__ __forceinline__ void gateup_body(const DecEntry& e, int rb, const int8_t* __restrict__ xq, const float* __restrict__ xd,
                             int n, int ff, int8_t* __restrict__ hq, float* __restrict__ hd, float (*hrow)[32],
-                            const uint8_t* warm = nullptr) {
+                            const uint8_t* warm = nullptr, const DecAct<MT>* pre = nullptr) {
     constexpr int RPW = (64 % NB == 0) ? 64 / NB : 1;
     constexpr int ROWS = 32 / NW;                       // rows per wave
     constexpr int PASSES = (ROWS + RPW - 1) / RPW;
@@ -379,23 +410,12 @@ __device__ __forceinline__ void gateup_body(const DecEntry& e, int rb, const int
     // (unconditional, with clamped indices: a token slot past ntok repeats token 0 and is skipped
     // below; a lane or row that is not live gets scale 0, so its products are 0)
     const int bl = live ? b : 0;
-    int xa[MT][16];
-    float xd0[MT], xd1[MT];
-#pragma unroll
-    for (int j = 0; j < MT; ++j) {
-        const int tj = e.tok[j < e.ntok ? j : 0];
-        const int4* src = reinterpret_cast<const int4*>(xq + size_t(tj) * n + bl * kBlock);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int4 v = src[q];
-            xa[j][4 * q + 0] = v.x;
-            xa[j][4 * q + 1] = v.y;
-            xa[j][4 * q + 2] = v.z;
-            xa[j][4 * q + 3] = v.w;
-        }
-        xd0[j] = xd[size_t(tj) * (n / kQ8) + 2 * bl];
-        xd1[j] = xd[size_t(tj) * (n / kQ8) + 2 * bl + 1];
-    }
+    DecAct<MT> act;
+    if (pre) act = *pre;
+    else load_act<NB, MT>(e.tok, e.ntok, xq, xd, n, act);
+    const int(&xa)[MT][16] = act.xa;
+    const float(&xd0)[MT] = act.xd0;
+    const float(&xd1)[MT] = act.xd1;
     uint4 cg[PASSES], cu[PASSES];
     uint32_t sg[PASSES], su[PASSES];   // fp16 scale bits, one per register (no packing waits)
     uint32_t okm = 0;                  // bit p: pass p's row is real
@@ -531,6 +551,13 @@ __global__ void __launch_bounds__(1024) k_dec_route_gateup(const float* __restri
                                                           uint32_t* counts) {
     __shared__ WinLds L;
     __shared__ float hrow[kDecMaxT][32];
+    // a single token (MT = 1): its activation block does not depend on the routing, so its loads
+    // are issued first and land during the logits' round trip
+    DecAct<MT> pre;
+    if (MT == 1) {
+        const int32_t tok0[1] = {0};
+        load_act<NB, MT>(tok0, 1, xq, xd, n, pre);
+    }
     FRT_PROBE_BEGIN();
 #ifdef FRT_PROBE_TWICE
     window_entries<V>(logits, gate, T, E, K, arena, stride, shared_blob, L);
@@ -553,7 +580,8 @@ __global__ void __launch_bounds__(1024) k_dec_route_gateup(const float* __restri
     }
     if (int(blockIdx.y) >= U1) return;
     const DecEntry e = L.ent[blockIdx.y];
-    gateup_body<NB, 16, MT>(e, blockIdx.x, xq, xd, n, ff, hq, hd, hrow, e.blob + 2 * mat_bytes(ff, n));
+    gateup_body<NB, 16, MT>(e, blockIdx.x, xq, xd, n, ff, hq, hd, hrow, e.blob + 2 * mat_bytes(ff, n),
+                            MT == 1 ? &pre : nullptr);
     FRT_PROBE(1, 4);
     FRT_PROBE_END();
 }
