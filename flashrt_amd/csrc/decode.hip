@@ -70,7 +70,9 @@ struct WinLds {
 //   2. one candidate per lane: its rank by logit counts the candidates ahead of it (higher key, or
 //      equal and lower id); the selection is rank < K, and the entry index is the selection's lane
 //      order (ascending id);
-//   3. e = exp(l - max) in rank order through LDS, w = e / (sum of e in rank order).
+//   3. only this workgroup's entry (blockIdx.y) is written, with the rank in slot[0] (w[0]: the
+//      selected logit; the weight is formed later, single_weights, while the weight rows load); the
+//      ids and logits in rank order go to L.ids and L.w.
 // More than 64 candidates (heavily tied logits) sets L.many and writes nothing else; the caller
 // then runs the four-wave path. gl is the shared gate logit in lane 0.
 template <int V>
@@ -114,40 +116,38 @@ __device__ __forceinline__ void route1_wave(const float (&v)[V], int E, int K, f
     }
     const bool sel = cl && rank < K;
     const int u = lanes_below(__ballot(sel));   // entry index: ascending expert id
-    const int top = __builtin_ctzll(__ballot(sel && rank == 0));
-    const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), top));
-    const float e = sel ? expf(cv - mx) : 0.0f;
-    if (sel) S.e[rank] = e;
-    float ws = 0.0f;
-    for (int k = 0; k < K; ++k) ws += S.e[k];
-    const float w = e / ws;
+    // Each workgroup needs only its own entry (blockIdx.y); the entries carry the selected logit in
+    // w[0] (the gate logit for the shared one) and the rank in slot[0], and the down kernel forms
+    // the weights from them. The ids in rank order go to every workgroup's L.ids (published by
+    // the workgroups of the first row block).
+    const int my = int(blockIdx.y);
     if (sel) {
         L.ids[0][rank] = ci;
-        L.w[0][rank] = w;
-        DecEntry& d = L.ent[u];
-        d.blob = arena + size_t(ci) * stride;
-        d.ntok = 1;
-        d.base = u;
-        d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
-        d.slot[0] = rank;
-        d.slot[1] = d.slot[2] = d.slot[3] = -1;
-        d.w[0] = w;
-        d.w[1] = d.w[2] = d.w[3] = 0.0f;
-        L.comb.slot[0][u] = u;
-        L.comb.w[0][u] = w;
+        L.w[0][rank] = cv;   // the selected logits in rank order (for the weights)
+        if (u == my) {
+            DecEntry& d = L.ent[u];
+            d.blob = arena + size_t(ci) * stride;
+            d.ntok = 1;
+            d.base = u;
+            d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
+            d.slot[0] = rank;
+            d.slot[1] = d.slot[2] = d.slot[3] = -1;
+            d.w[0] = cv;
+            d.w[1] = d.w[2] = d.w[3] = 0.0f;
+        }
     }
-    const float sw = sigmoidf_(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gl), 0)));
+    const float g0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gl), 0));
     if (lane == 63) {
-        DecEntry& d = L.ent[K];
-        d.blob = shared_blob;
-        d.ntok = 1;
-        d.base = K;
-        d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
-        d.slot[0] = d.slot[1] = d.slot[2] = d.slot[3] = -1;
-        d.w[0] = sw;
-        d.w[1] = d.w[2] = d.w[3] = 0.0f;
-        L.comb.slot[0][K] = K;
-        L.comb.w[0][K] = sw;
+        if (my == K) {
+            DecEntry& d = L.ent[K];
+            d.blob = shared_blob;
+            d.ntok = 1;
+            d.base = K;
+            d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
+            d.slot[0] = d.slot[1] = d.slot[2] = d.slot[3] = -1;
+            d.w[0] = g0;
+            d.w[1] = d.w[2] = d.w[3] = 0.0f;
+        }
         L.n_ent = K + 1;
         L.many = 0;
     }
@@ -190,39 +190,34 @@ __device__ __forceinline__ int window_entries(const float* __restrict__ logits, 
         }
     }
     topk_group4<V>(logits + size_t(active ? g : 0) * E, E, K, q, active, L.tk[active ? g : 0], mx);
-    if (T == 1) {   // one token: entries are its K experts by ascending id (slot = entry), then the shared expert
+    if (T == 1) {   // one token (heavy ties): every entry, in route1_wave's form (logit in w[0], rank in slot[0])
         if (wave == 0) {
             const float sel_l = lane < K ? L.tk[0].sel_v[lane] : 0.0f;
             const int sel_id = lane < K ? L.tk[0].sel_id[lane] : 0x7fffffff;
-            const float w = topk_weight_sel(sel_l, mx, K);
-            int rank = 0;
-            for (int j = 0; j < K; ++j) rank += int(__builtin_amdgcn_readlane(sel_id, j) < sel_id);
+            int u = 0;
+            for (int j = 0; j < K; ++j) u += int(__builtin_amdgcn_readlane(sel_id, j) < sel_id);
+            const float g0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gl), 0));
             if (lane < K) {
                 L.ids[0][lane] = sel_id;
-                L.w[0][lane] = w;
-                DecEntry& d = L.ent[rank];
+                L.w[0][lane] = sel_l;
+                DecEntry& d = L.ent[u];
                 d.blob = arena + size_t(sel_id) * stride;
                 d.ntok = 1;
-                d.base = rank;
+                d.base = u;
                 d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
                 d.slot[0] = lane;
                 d.slot[1] = d.slot[2] = d.slot[3] = -1;
-                d.w[0] = w;
+                d.w[0] = sel_l;
                 d.w[1] = d.w[2] = d.w[3] = 0.0f;
-                L.comb.slot[0][rank] = rank;
-                L.comb.w[0][rank] = w;
             } else if (lane == K) {
-                const float sw = sigmoidf_(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gl), 0)));
                 DecEntry& d = L.ent[K];
                 d.blob = shared_blob;
                 d.ntok = 1;
                 d.base = K;
                 d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
                 d.slot[0] = d.slot[1] = d.slot[2] = d.slot[3] = -1;
-                d.w[0] = sw;
+                d.w[0] = g0;
                 d.w[1] = d.w[2] = d.w[3] = 0.0f;
-                L.comb.slot[0][K] = K;
-                L.comb.w[0][K] = sw;
                 L.n_ent = K + 1;
             }
         }
@@ -388,10 +383,40 @@ __device__ __forceinline__ void load_act(const int32_t* tok, int ntok, const int
     }
 }
 
+// Work a caller of gateup_body runs while the weight rows are in flight (after their loads are
+// issued, before the first wait for them): a single token's routing weights (single_weights).
+struct AfterLoads {
+    float* wts = nullptr;          // the weights in rank order (workgroup (0, 0))
+    DecEntry* ent_w = nullptr;     // this workgroup's published entry, whose w[0] becomes its weight
+    const float* lg = nullptr;     // the selected logits in rank order (LDS)
+    const DecEntry* e = nullptr;   // this workgroup's entry (rank in slot[0]; shared: gate logit in w[0])
+    int K = 0;
+    bool shared = false;           // the entry is the shared expert's
+};
+// As topk_weight_sel: e = exp(l - max) with max the rank-0 logit, w = e / (the sum of e in rank order
+// from 0); the shared expert's weight is sigmoid(gate). One wave (lane k: rank k).
+__device__ __forceinline__ void single_weights(const AfterLoads& a) {
+    const int lane = threadIdx.x & 63;
+    if (a.shared) {
+        if (lane == 0) a.ent_w->w[0] = sigmoidf_(a.e->w[0]);
+        return;
+    }
+    const bool r = lane < a.K;
+    const float l = r ? a.lg[lane] : 0.0f;
+    const float mx = a.lg[0];
+    const float e = r ? expf(l - mx) : 0.0f;
+    float ws = 0.0f;
+    for (int k = 0; k < a.K; ++k) ws += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), k));
+    const float w = e / ws;
+    if (r && a.wts) a.wts[lane] = w;
+    if (lane == a.e->slot[0]) a.ent_w->w[0] = w;
+}
+
 template <int NB, int NW, int MT = kDecMaxT>
 __device__ __forceinline__ void gateup_body(const DecEntry& e, int rb, const int8_t* __restrict__ xq, const float* __restrict__ xd,
                             int n, int ff, int8_t* __restrict__ hq, float* __restrict__ hd, float (*hrow)[32],
-                            const uint8_t* warm = nullptr, const DecAct<MT>* pre = nullptr) {
+                            const uint8_t* warm = nullptr, const DecAct<MT>* pre = nullptr,
+                            AfterLoads after_loads = {}) {
     constexpr int RPW = (64 % NB == 0) ? 64 / NB : 1;
     constexpr int ROWS = 32 / NW;                       // rows per wave
     constexpr int PASSES = (ROWS + RPW - 1) / RPW;
@@ -452,6 +477,7 @@ __device__ __forceinline__ void gateup_body(const DecEntry& e, int rb, const int
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (after_loads.ent_w && (threadIdx.x >> 6) == 0) single_weights(after_loads);
     int xs0[MT], xs1[MT];   // the halves' code sums
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
@@ -565,7 +591,23 @@ __global__ void __launch_bounds__(1024) k_dec_route_gateup(const float* __restri
     FRT_PROBE(1, 0);
     const int U1 = window_entries<V>(logits, gate, T, E, K, arena, stride, shared_blob, L);
     FRT_PROBE(1, 1);
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
+    if (T == 1) {
+        // a single token: workgroup (0, y) publishes entry y, the id of its selection (rank slot[0])
+        // and its count; its weight (and workgroup (0, 0) the weights in rank order) it forms while
+        // its weight rows load (single_weights)
+        const int y = int(blockIdx.y);
+        if (blockIdx.x == 0 && y < U1) {
+            constexpr int kW0 = int(offsetof(DecEntry, w) / 4);   // w[0]: the weight, written later
+            if (threadIdx.x < int(sizeof(DecEntry) / 4) && int(threadIdx.x) != kW0)
+                reinterpret_cast<int32_t*>(ent_out + y)[threadIdx.x] = reinterpret_cast<const int32_t*>(&L.ent[y])[threadIdx.x];
+            if (threadIdx.x == 0 && y < K) {
+                const int id = L.ids[0][L.ent[y].slot[0]];
+                ids[L.ent[y].slot[0]] = id;
+                if (counts) atomicAdd(counts + id, 1u);
+            }
+            if (threadIdx.x == 0 && y == 0) *n_ent_out = U1;
+        }
+    } else if (blockIdx.x == 0 && blockIdx.y == 0) {
         for (int i = threadIdx.x; i < U1 * int(sizeof(DecEntry) / 4); i += blockDim.x)
             reinterpret_cast<int32_t*>(ent_out)[i] = reinterpret_cast<const int32_t*>(L.ent)[i];
         if (threadIdx.x < T * K) {
@@ -580,8 +622,17 @@ __global__ void __launch_bounds__(1024) k_dec_route_gateup(const float* __restri
     }
     if (int(blockIdx.y) >= U1) return;
     const DecEntry e = L.ent[blockIdx.y];
+    AfterLoads al;
+    if (T == 1 && blockIdx.x == 0) {
+        al.wts = blockIdx.y == 0 ? wts : nullptr;
+        al.ent_w = ent_out + blockIdx.y;
+        al.lg = L.w[0];
+        al.e = &L.ent[blockIdx.y];
+        al.K = K;
+        al.shared = int(blockIdx.y) == K;
+    }
     gateup_body<NB, 16, MT>(e, blockIdx.x, xq, xd, n, ff, hq, hd, hrow, e.blob + 2 * mat_bytes(ff, n),
-                            MT == 1 ? &pre : nullptr);
+                            MT == 1 ? &pre : nullptr, al);
     FRT_PROBE(1, 4);
     FRT_PROBE_END();
 }
