@@ -64,7 +64,7 @@ struct WinLds {
 // entries as topk_group4 followed by the single-token entry code below, with ballots in place of
 // sorts and barriers:
 //   1. lane l holds experts V l .. V l + V - 1; a lower bound on the K-th largest lane maximum (a
-//      search over the keys' upper 16 bits by ballot counts) bounds the K-th largest logit from
+//      search over the keys' upper 12 bits by ballot counts) bounds the K-th largest logit from
 //      below, so every member of the top K is a candidate; candidates are compacted into LDS in
 //      ascending id;
 //   2. one candidate per lane: its rank by logit counts the candidates ahead of it (higher key, or
@@ -87,7 +87,7 @@ __device__ __forceinline__ void route1_wave(const float (&v)[V], int E, int K, f
         key[i] = V * lane + i < E ? logit_key(v[i]) : 0u;
         mk = max(mk, key[i]);
     }
-    const uint32_t t1 = wave_kth_key_hi(mk, K) << 16;
+    const uint32_t t1 = wave_kth_key_hi(mk, K) << 20;
     int c = 0;
 #pragma unroll
     for (int i = 0; i < V; ++i) c += int(key[i] != 0u && key[i] >= t1);
@@ -108,11 +108,18 @@ __device__ __forceinline__ void route1_wave(const float (&v)[V], int E, int K, f
     const bool cl = lane < C;
     const float cv = cl ? S.cand_v[lane] : 0.0f;
     const int ci = cl ? S.cand_id[lane] : 0x7fffffff;
-    const uint32_t ck = cl ? logit_key(cv) : 0u;
+    // rank among the candidates: those ahead by logit, or equal and lower id (= lower slot); the
+    // candidates' logits are read four at a time (the same address in every lane); float order
+    // with -0 == +0 is the keys' order
     int rank = 0;
-    for (int j = 0; j < C; ++j) {
-        const uint32_t kj = uint32_t(__builtin_amdgcn_readlane(int(ck), j));
-        rank += int(kj > ck || (kj == ck && j < lane));
+    for (int j0 = 0; j0 < C; j0 += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(S.cand_v + j0);
+        const float qv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int j = j0 + u;
+            rank += int(j < C && (qv[u] > cv || (qv[u] == cv && j < lane)));
+        }
     }
     const bool sel = cl && rank < K;
     const int u = lanes_below(__ballot(sel));   // entry index: ascending expert id

@@ -111,14 +111,14 @@ __device__ __forceinline__ uint32_t logit_key(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// The largest t < 2^16 with at least K lanes holding key >= t << 16 (K >= 1; 0 when fewer than K
+// The largest t < 2^12 with at least K lanes holding key >= t << 20 (K >= 1; 0 when fewer than K
 // lanes hold a nonzero key): a lower bound on the K-th largest key, found two bits at a time from
-// the top by ballot counts over the keys' upper halves; uniform.
+// the top by ballot counts over the keys' upper 12 bits (sign, exponent, 3 mantissa bits); uniform.
 __device__ __forceinline__ uint32_t wave_kth_key_hi(uint32_t key, int K) {
-    const uint32_t kh = key >> 16;
+    const uint32_t kh = key >> 20;
     uint32_t t = 0;
 #pragma unroll
-    for (int b = 14; b >= 0; b -= 2) {
+    for (int b = 10; b >= 0; b -= 2) {
         const uint32_t c1 = t | (1u << b), c2 = t | (2u << b), c3 = t | (3u << b);
         const int n1 = __popcll(__ballot(kh >= c1)), n2 = __popcll(__ballot(kh >= c2)),
                   n3 = __popcll(__ballot(kh >= c3));
