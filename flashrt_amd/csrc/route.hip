@@ -328,15 +328,17 @@ namespace {
 
 // logits [T][E] (and the shared gate [T] as row E) for many tokens in the canonical order, as a
 // K-split GEMM that follows the order's own tree: the adjacent pairwise tree over the 64 chains is
-// ((S0 + S1) + (S2 + S3)) with S_s the tree over chains 16 s .. 16 s + 15, so workgroup split s
-// computes S_s and k_router_combine forms the top two levels (and adds the bias) exactly.
+// ((S0 + S1) + (S2 + S3)) + ((S4 + S5) + (S6 + S7)) with S_s the tree over chains 8 s .. 8 s + 7,
+// so workgroup split s computes S_s and k_router_combine forms the top three levels (and adds the
+// bias) exactly. (Eight splits rather than four: 2304 workgroups at T = 2048 fill whole rounds of
+// the three per CU, and each thread keeps one level less of pending subtrees.)
 // Within a split, K runs in natural order in tiles of L = n / 64 (one chain each); after each tile
 // the chain sum joins a pairwise-tree stack (a binary counter: chain j merges with the completed
 // subtrees named by the trailing one bits of j + 1).
 // Workgroup tile 64 tokens x 64 rows, 256 threads, 4 x 4 outputs per thread; x and W tiles in LDS
 // as [k][64 (+4 pad)] (a thread reads its 4 tokens and 4 rows as one float4 each); the next chain's tiles
 // are loaded into registers while the current one is multiplied.
-constexpr int kRgSplit = 4, kRgChains = 64 / kRgSplit;
+constexpr int kRgSplit = 8, kRgChains = 64 / kRgSplit, kRgLevels = 3;   // kRgChains = 2^kRgLevels
 
 template <int L>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
@@ -350,7 +352,7 @@ k_router_gemm(const float* __restrict__ x, int T, const float* __restrict__ W, c
     const int t0 = blockIdx.y * 64, e0 = blockIdx.x * 64, c0 = blockIdx.z * kRgChains;
     const int tid = threadIdx.x;
     const int tr = (tid & 15) * 4, er = (tid >> 4) * 4;   // this thread's 4 tokens and 4 rows
-    float lv[4][4][4];   // pending subtrees of the levels 0..3
+    float lv[4][4][kRgLevels];   // pending subtrees of the levels below the split's root
     constexpr int F4 = L / 4;                    // float4 per row and chain
     constexpr int NP = (64 * F4 + 255) / 256;    // staging passes
     float4 rx[NP], rw[NP];
@@ -413,7 +415,7 @@ k_router_gemm(const float* __restrict__ x, int T, const float* __restrict__ W, c
                 float v = acc[i][j];
                 bool parked = false;
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
+                for (int m = 0; m < kRgLevels; ++m) {
                     if (parked) continue;
                     if (((c >> m) & 1) == 0) {
                         lv[i][j][m] = v;
@@ -422,7 +424,7 @@ k_router_gemm(const float* __restrict__ x, int T, const float* __restrict__ W, c
                         v = lv[i][j][m] + v;
                     }
                 }
-                if (!parked) total[i][j] = v;   // c == 15: the split's whole subtree
+                if (!parked) total[i][j] = v;   // the split's last chain: its whole subtree
             }
         if (c + 1 < kRgChains) {
             store(buf ^ 1);
@@ -438,14 +440,16 @@ k_router_gemm(const float* __restrict__ x, int T, const float* __restrict__ W, c
         }
 }
 
-// top of the tree: v = (S0 + S1) + (S2 + S3); logits [T][E] = v + bias, gate [T] = row E's v
+// top of the tree: v = ((S0 + S1) + (S2 + S3)) + ((S4 + S5) + (S6 + S7)); logits [T][E] = v + bias,
+// gate [T] = row E's v
 __global__ void __launch_bounds__(256) k_router_combine(const float* __restrict__ part, int T, int E, int E1,
                                                         const float* __restrict__ bias, float* __restrict__ logits,
                                                         float* __restrict__ gate) {
     const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x, N = size_t(T) * E1;
     if (i >= N) return;
     const int t = int(i / E1), e = int(i % E1);
-    const float v = (part[i] + part[N + i]) + (part[2 * N + i] + part[3 * N + i]);
+    const float v = ((part[i] + part[N + i]) + (part[2 * N + i] + part[3 * N + i])) +
+                    ((part[4 * N + i] + part[5 * N + i]) + (part[6 * N + i] + part[7 * N + i]));
     if (e < E) logits[size_t(t) * E + e] = bias ? v + bias[e] : v;
     else gate[t] = v;
 }
