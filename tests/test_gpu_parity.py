@@ -437,6 +437,58 @@ def test_layer_prefill_graph_replays(F):
         torch.cuda.synchronize()
 
 
+def test_decode_stack_graph_replays(F):
+    """Four config 2 decode layers (single token, RMS-normalised input, residual, the next layer's
+    router warming) captured in a HIP graph, as the bench runs them: three replays, with eager work
+    and synchronizations between them, each equal to the eager chain bit for bit (ids, weights and
+    outputs)."""
+    layers = []
+    for layer in range(4):
+        bias = O.gen_zipf_bias(2, layer, H.E, H.ZIPF_S_STACK)
+        layers.append(H.World(cfg=2, layer=layer, bias=bias, norm_input=True))
+    for l in range(4):
+        layers[l].layer_obj.set_next_router(layers[(l + 1) % 4].router_w)
+    x0 = torch.from_numpy(O.gen_normal(2, 0, O.X_TENSOR + 11, H.N).reshape(1, H.N)).cuda()
+    ws = torch.empty(layers[0].layer_obj.workspace_bytes(1), dtype=torch.uint8, device="cuda")
+    bufs = [torch.empty((1, H.N), dtype=torch.float32, device="cuda") for _ in range(4)]
+    ids = torch.empty((4, H.K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((4, H.K), dtype=torch.float32, device="cuda")
+
+    def chain(stream=None):
+        cur = x0
+        for l in range(4):
+            layers[l].layer_obj.forward(cur, bufs[l], T=1, resid=cur, ids=ids[l], wts=wts[l], ws=ws, stream=stream)
+            cur = bufs[l]
+
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        chain(s)
+    s.synchronize()
+    ref = [b.clone() for b in bufs], ids.clone(), wts.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        chain(s)
+    try:
+        for i in range(3):
+            for b in bufs:
+                b.fill_(float("nan"))
+            ids.fill_(-1)
+            wts.fill_(0.0)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            for l in range(4):
+                assert torch.equal(bufs[l], ref[0][l]), (i, l)
+            assert torch.equal(ids, ref[1]), i
+            assert torch.equal(wts, ref[2]), i
+            with torch.cuda.stream(s):
+                chain(s)   # eager work between the replays
+            s.synchronize()
+    finally:
+        for l in range(4):
+            layers[l].layer_obj.set_next_router(None)
+
+
 def test_layer_mixed_config4(F):
     """Config 4: an 8192-token bf16 prefill chunk plus 16 uncorrelated fp32 decode tokens in one
     launch (T = 8208), with adversarial popularity: +2.8 on the logits of 16 seeded hot experts puts
