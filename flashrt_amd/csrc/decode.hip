@@ -5,14 +5,19 @@
 // shared expert last. Entry c-slots (entry u, token j) are numbered compactly (base[u] + j).
 //
 //   k_dec_route_gateup  per (32 ff rows, entry): every workgroup routes the window itself (top-k
-//                 of each token, topk.hpp) and builds the entry list in LDS, so routing costs no
-//                 launch; then gate and up rows of every token of its entry, SwiGLU, and Q8_0 of
-//                 that 32-row block of h (quant/q2_0/moe_cpu.cpp:43-61 phase A). Workgroup (0, 0)
-//                 publishes ids, weights and the entry list.
+//                 of each token, topk.hpp), so routing costs no launch; then gate and up rows of
+//                 every token of its entry, SwiGLU, and Q8_0 of that 32-row block of h
+//                 (quant/q2_0/moe_cpu.cpp:43-61 phase A). A window (T > 1): four waves per token
+//                 route, every workgroup builds the whole entry list in LDS, and workgroup (0, 0)
+//                 publishes ids, weights, entries and combine lists. A single token: one wave
+//                 routes (route1_wave), each workgroup writes only its own entry, and workgroup
+//                 (0, y) publishes entry y, its id and, formed while its weight rows load, its
+//                 weight (workgroup (0, 0) also the weights in rank order).
 //   k_dec_gateup  the same body for moe_hits, entries from k_hits_group
 //   k_dec_down    per 8 output rows: down rows of every entry, then the weighted sum per token in
 //                 expert order plus shared * sigmoid(gate) (moe_cpu.cpp:63-80 phase B and
-//                 moe_ref.cu:90-97); or, for moe_hits, the per-slot outputs yh.
+//                 moe_ref.cu:90-97; a single token's combine list is the entry list itself); or,
+//                 for moe_hits, the per-slot outputs yh.
 //
 // Inner product per (row, 64-block, token): the 16 code bytes are read as 4 dwords; (code >> 2s)
 // & 0x03030303 lines up with activation dword 4s + w (the planar layout), so 16 v_dot4_i32_i8
