@@ -165,10 +165,16 @@ __device__ __forceinline__ void route1_wave(const float (&v)[V], int E, int K, f
     }
 }
 
-template <int V>
+// after_issue() runs once the routing's own loads are issued (a single token: the logits in wave 0),
+// for loads the caller wants in flight during the routing but not waited for before it.
+struct NoLoads {
+    __device__ void operator()() const {}
+};
+template <int V, class F = NoLoads>
 __device__ __forceinline__ int window_entries(const float* __restrict__ logits, const float* __restrict__ gate, int T,
                                               int E, int K, const uint8_t* __restrict__ arena, size_t stride,
-                                              const uint8_t* __restrict__ shared_blob, WinLds& L) {
+                                              const uint8_t* __restrict__ shared_blob, WinLds& L,
+                                              F after_issue = {}) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g = wave >> 2, q = wave & 3;
     const bool active = g < T;
@@ -177,24 +183,27 @@ __device__ __forceinline__ int window_entries(const float* __restrict__ logits, 
     const float gl = gate[min(lane, T - 1)];
     float mx;
     if (T == 1) {   // one wave selects; the rest of the workgroup waits at the barrier
-        if (wave == 0) {
-            float v[V];
-            if (E == 64 * V) {
-                const float4* l4 = reinterpret_cast<const float4*>(logits + V * lane);
+        // every wave loads the logits (L1 hits after the first), so no load sits under a branch and
+        // no wait is placed at a branch merge ahead of after_issue()'s loads
+        float v[V];
+        if (E == 64 * V) {
+            const float4* l4 = reinterpret_cast<const float4*>(logits + V * lane);
 #pragma unroll
-                for (int i = 0; i < V / 4; ++i) {
-                    const float4 f = l4[i];
-                    v[4 * i] = f.x;
-                    v[4 * i + 1] = f.y;
-                    v[4 * i + 2] = f.z;
-                    v[4 * i + 3] = f.w;
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < V; ++i) v[i] = logits[min(V * lane + i, E - 1)];
+            for (int i = 0; i < V / 4; ++i) {
+                const float4 f = l4[i];
+                v[4 * i] = f.x;
+                v[4 * i + 1] = f.y;
+                v[4 * i + 2] = f.z;
+                v[4 * i + 3] = f.w;
             }
-            route1_wave<V>(v, E, K, gl, arena, stride, shared_blob, L);
+        } else {
+#pragma unroll
+            for (int i = 0; i < V; ++i) v[i] = logits[min(V * lane + i, E - 1)];
         }
+        __builtin_amdgcn_sched_barrier(0);
+        after_issue();   // issued behind the logits: the wait for them leaves these in flight
+        __builtin_amdgcn_sched_barrier(0);
+        if (wave == 0) route1_wave<V>(v, E, K, gl, arena, stride, shared_blob, L);
         __syncthreads();
         if (!L.many) {
             FRT_PROBE(3, 6);
@@ -590,18 +599,20 @@ __global__ void __launch_bounds__(1024) k_dec_route_gateup(const float* __restri
     __shared__ WinLds L;
     __shared__ float hrow[kDecMaxT][32];
     // a single token (MT = 1): its activation block does not depend on the routing, so its loads
-    // are issued first and land during the logits' round trip
+    // are issued right behind the logits' and land during the routing
     DecAct<MT> pre;
-    if (MT == 1) {
-        const int32_t tok0[1] = {0};
-        load_act<NB, MT>(tok0, 1, xq, xd, n, pre);
-    }
+    auto preload = [&]() {
+        if (MT == 1) {
+            const int32_t tok0[1] = {0};
+            load_act<NB, MT>(tok0, 1, xq, xd, n, pre);
+        }
+    };
     FRT_PROBE_BEGIN();
 #ifdef FRT_PROBE_TWICE
     window_entries<V>(logits, gate, T, E, K, arena, stride, shared_blob, L);
 #endif
     FRT_PROBE(1, 0);
-    const int U1 = window_entries<V>(logits, gate, T, E, K, arena, stride, shared_blob, L);
+    const int U1 = window_entries<V>(logits, gate, T, E, K, arena, stride, shared_blob, L, preload);
     FRT_PROBE(1, 1);
     if (T == 1) {
         // a single token: workgroup (0, y) publishes entry y, the id of its selection (rank slot[0])
