@@ -190,6 +190,21 @@ def test_layer_decode_config0(F, w0):
     assert H.out_rel(out, ref) <= H.OUT_REL
 
 
+@pytest.mark.parametrize("E", [300, 128])
+def test_layer_decode_other_expert_counts(F, E):
+    """Single-token decode with E not 64 times the per-lane logit count (300: the clamped logit loads,
+    the last lane's tail past E; 128: two logits per lane), ids, weights and output against the
+    oracle (the reference routes any E up to its kernel's bound, blocks.hpp:130-135)."""
+    w = H.World(cfg=0, E=E)
+    rng = np.random.default_rng(E)
+    x = rng.standard_normal((1, H.N)).astype(np.float32)
+    out, ids, wts = w.gpu_forward(x)
+    ref, rid, rw, _ = w.oracle_forward(x)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    assert H.out_rel(out, ref) <= H.OUT_REL
+
+
 def test_layer_reference_test_shape(F):
     """The reference tests' shape, d_model 2560 and expert ff 640 (tests/test_moe_q2.cpp:68-153),
     through the whole layer: decode at T = 1 and 3 and prefill at T = 128, every token's ids,
