@@ -147,7 +147,8 @@ def run_stack(args, F, torch):
     stream.synchronize()
     kt = kernel_times(F, lambda: eager(args.timing_steps))
     del graph
-    res = dict(ms_per_step=ms_per_step, wall_s=wall, kernels=kt)
+    sync_err = F.layer_sync_error(ws)   # a persistent call that ran out of time would void the run
+    res = dict(ms_per_step=ms_per_step, wall_s=wall, kernels=kt, sync_error=sync_err)
     res["_keep"] = (arena, shared, router, gate, bias, mls, xs, ws)
     return res
 
@@ -323,6 +324,8 @@ def main():
                     help="first run 3 plain device copies of MIB MiB (scales the HBM byte counters of a profile)")
     ap.add_argument("--timing-steps", type=int, default=3, help="decode steps in the per-kernel timing pass")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--decode-path", choices=["fused", "three"], default="fused",
+                    help="single-token layers as one persistent launch (default) or as three kernels")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -342,7 +345,10 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    F.set_option("decode_fused", 1 if args.decode_path == "fused" else 0)
     st = run_stack(args, F, torch)
+    if st["sync_error"]:
+        sys.exit("bench.py: a persistent decode call ran out of time waiting for another workgroup")
     ms = st["ms_per_step"]
     tok_s = 1e3 / ms
     expert_bytes_tok = args.layers * (K + 1) * F.expert_bytes(N, FF)

@@ -81,6 +81,16 @@ int dec_moe(const float* logits, const float* gate, int T, int E, int K, const u
 int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const int8_t* xq, const float* xd, int n,
              int ff, void* scratch, float* yh, hipStream_t stream, int T);
 int dec_check(int T, int K, int n, int ff);
+// decode1.hip
+size_t dec1_sync_bytes();
+int dec1_eligible(int E, int K, int n, int ff);
+int dec1_layer(const float* x, const float* W, const float* bias, const float* gate_w, int E, int K,
+               const uint8_t* arena, size_t stride, const uint8_t* shared, int n, int ff, int norm, const float* resid,
+               float* out, int32_t* ids, float* wts, uint32_t* counts, void* sync_ws, const float* next_w,
+               hipStream_t stream);
+int dec1_status(void* sync_ws, hipStream_t stream, uint32_t* err);
+extern int g_dec1_on;
+extern uint64_t g_dec1_ticks;
 // prefill.hip
 size_t pf_workspace_bytes(int T, int K, int n, int ff, int E, bool shared, bool own_yd);
 int pf_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const float* x, const int32_t* ids, int T, int K,
@@ -116,6 +126,7 @@ static size_t hits_bytes(int K, int ff, int T, int n) {
 }
 
 struct LayerWs {
+    void* sync;    // the single-token layer's sync region (always first, so no other path overwrites it)
     float* logits;
     float* gate;
     float* u;      // normalised input (prefill with FRT_LAYER_NORM_INPUT)
@@ -138,6 +149,7 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
         return r;
     };
     const int E = L.n_expert, K = L.top_k, n = L.d_model, ff = L.d_ff;
+    w.sync = take(dec1_sync_bytes());
     w.logits = reinterpret_cast<float*>(take(size_t(T) * E * 4));
     w.gate = reinterpret_cast<float*>(take(size_t(T) * 4));
     w.ids = reinterpret_cast<int32_t*>(take(size_t(T) * K * 4));
@@ -325,6 +337,9 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     float* wts_o = wts ? wts : w.wts;
     const int norm = (L->flags & FRT_LAYER_NORM_INPUT) ? 1 : 0;
     timing_mark(s, "begin");
+    if (T == 1 && g_dec1_on && dec1_eligible(E, K, n, ff))   // the whole layer in one persistent launch
+        return dec1_layer(x, L->router_w, L->router_bias, L->gate_w, E, K, L->experts, L->stride, L->shared, n, ff,
+                          norm, resid, out, ids_o, wts_o, counts, w.sync, L->next_router_w, s);
     if (T <= kDecodeMaxT && T * K <= 63) {
         if (int rc = dec_check(T, K, n, ff)) return rc;
         // router logits, the shared gate, the RMS scale and Q8_0 of the input in one launch
@@ -350,6 +365,27 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     timing_mark(s, "route_topk");
     return pf_moe(L->experts, L->stride, E, L->shared, n, ff, xin, ids_o, wts_o, w.gate, T, K, resid, out, w.rest,
                   w.rest_bytes, s);
+}
+
+int frt_set_option(const char* name, int64_t value) {
+    if (!name) return set_error(kErrNull, "set_option: null name");
+    if (!std::strcmp(name, "decode_fused")) {
+        g_dec1_on = value ? 1 : 0;
+        return kOk;
+    }
+    if (!std::strcmp(name, "sync_ticks")) {
+        if (value < 0) return set_error(kErrShape, "set_option: sync_ticks < 0");
+        g_dec1_ticks = uint64_t(value);
+        return kOk;
+    }
+    return set_error(kErrShape, "set_option: unknown option '%s'", name);
+}
+
+int frt_moe_layer_sync_error(void* ws, void* stream) {
+    if (!ws) return set_error(kErrNull, "moe_layer_sync_error: null workspace");
+    uint32_t err = 0;
+    if (int rc = dec1_status(ws, static_cast<hipStream_t>(stream), &err)) return rc;
+    return err ? 1 : 0;
 }
 
 int frt_gen_experts(uint64_t seed, int cfg, int layer, int e0, int count, int tensor_base, int n, int ff, float sd,

@@ -79,49 +79,6 @@ inline void launch_timed(const char* name, K kernel, dim3 grid, dim3 block, size
 
 inline size_t up256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Phase probes for latency work (compiled out unless FRT_PHASE_PROBE is defined). Thread 0 of
-// each workgroup keeps the constant-rate (100 MHz) GPU clock of point i of slot k in LDS
-// (FRT_PROBE), and FRT_PROBE_END writes the table to frt_probe[k][workgroup][i] once at the end of
-// the kernel: a global store per point would make the next wait for a load also wait for the store.
-// The instrumented library exports frt_probe_dump() to read the table.
-#ifdef FRT_PHASE_PROBE
-extern __device__ unsigned long long frt_probe[4][2048][8];
-__device__ __forceinline__ unsigned long long* frt_probe_lds() {
-    __shared__ unsigned long long t[32];
-    return t;
-}
-#define FRT_PROBE_BEGIN()                                                  \
-    do {                                                                   \
-        if (threadIdx.x < 32) frt_probe_lds()[threadIdx.x] = 0;            \
-    } while (0)
-#ifdef FRT_PROBE_CYCLES   // shader cycles instead (one workgroup's own timeline)
-#define FRT_PROBE_CLOCK() __builtin_amdgcn_s_memtime()
-#else
-#define FRT_PROBE_CLOCK() wall_clock64()
-#endif
-#define FRT_PROBE(k, i)                                                         \
-    do {                                                                        \
-        if (threadIdx.x == 0) frt_probe_lds()[(k) * 8 + (i)] = FRT_PROBE_CLOCK(); \
-    } while (0)
-#define FRT_PROBE_END()                                                                            \
-    do {                                                                                           \
-        if (threadIdx.x < 32 && frt_probe_lds()[threadIdx.x] &&                                    \
-            blockIdx.x + blockIdx.y * gridDim.x < 2048) /* rows of the table */                       \
-            frt_probe[threadIdx.x / 8][blockIdx.x + blockIdx.y * gridDim.x][threadIdx.x % 8] =     \
-                frt_probe_lds()[threadIdx.x];                                                      \
-    } while (0)
-#else
-#define FRT_PROBE_BEGIN() \
-    do {                  \
-    } while (0)
-#define FRT_PROBE(k, i) \
-    do {                \
-    } while (0)
-#define FRT_PROBE_END() \
-    do {                \
-    } while (0)
-#endif
-
 // ---- device helpers
 
 // A load through the global address space; p must point into device global memory (an LDS or

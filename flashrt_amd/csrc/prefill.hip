@@ -421,8 +421,6 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
     if (ti >= (SMALL ? n_tiles[0] : n_tiles[1])) return;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int sRow[Sh::tokens];
-    FRT_PROBE_BEGIN();
-    FRT_PROBE(0, 0);
     const int2 tile = tiles[ti];
     const int grp = tile.x;
     const int row0 = bounds[grp] + tile.y;
@@ -566,7 +564,6 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
         }
     }
 
-    FRT_PROBE(0, 1);
     // lane: token column c*16 + li; ff rows f = rbase + 32 wave + 16 i + 4 lg + r (i = 0, 1) for gate
     // (acc[i]) and up (acc[2 + i]). The 32 rows of the wave are one Q8_0 block of h.
     const int fbase = rbase + 32 * wave;
@@ -609,8 +606,6 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
             hout[size_t(row0 + col) * ffp + (f & ~255) + perm256_pos(f & 255)] = _Float16(0.0f);
         }
     }
-    FRT_PROBE(0, 2);
-    FRT_PROBE_END();
 }
 
 // k_pf_down: the down GEMM, one workgroup (256 threads) per tile. The tile's activations (h of 64
@@ -637,8 +632,6 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
     if (int(blockIdx.y) >= *n_tiles) return;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int sRow[kTN];
-    FRT_PROBE_BEGIN();
-    FRT_PROBE(1, 0);
     const int2 tile = tiles[blockIdx.y];
     const int grp = tile.x;
     const int row0 = bounds[grp] + tile.y;
@@ -748,9 +741,6 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
         case 3: run(std::integral_constant<int, 3>{}); break;
         default: run(std::integral_constant<int, 4>{}); break;
     }
-    FRT_PROBE(1, 1);
-    FRT_PROBE(1, 2);
-    FRT_PROBE_END();
 }
 
 // ---------------------------------------------------------------- combine

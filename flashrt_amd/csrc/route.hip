@@ -40,8 +40,6 @@ __global__ void __launch_bounds__(256) k_router(const float* __restrict__ x, int
                                                 float* __restrict__ xd) {
     extern __shared__ float xs[];   // [TT][64][L + 1]
     __shared__ float s_r[64];
-    FRT_PROBE_BEGIN();
-    FRT_PROBE(0, 0);
     const int n = 64 * L;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row = blockIdx.x * (blockDim.x >> 6) + wave;
@@ -93,7 +91,6 @@ __global__ void __launch_bounds__(256) k_router(const float* __restrict__ x, int
             }
         }
         __syncthreads();
-        FRT_PROBE(0, 1);
         if (norm) {
             for (int t = wave; t < tn; t += int(blockDim.x >> 6)) {
                 const float r = rms_scale_wave<L>(xs + (t * 64 + lane) * (L + 1), n);
@@ -112,7 +109,6 @@ __global__ void __launch_bounds__(256) k_router(const float* __restrict__ x, int
                 quant32(v, j, xq + size_t(t0 + t) * n + (k - j), xd + size_t(t0 + t) * (n / kQ8) + k / kQ8);
             }
         }
-        FRT_PROBE(0, 2);
         if (!live) continue;
         for (int t = 0; t < tn; ++t) {
             const float* xc = xs + (t * 64 + lane) * (L + 1);
@@ -135,8 +131,6 @@ __global__ void __launch_bounds__(256) k_router(const float* __restrict__ x, int
             }
         }
     }
-    FRT_PROBE(0, 3);
-    FRT_PROBE_END();
 }
 
 // ---- u = x * r per token (canonical RMS scale), one wave per token (prefill inputs)

@@ -33,13 +33,16 @@ __device__ __forceinline__ void sort_desc(float (&v)[V], int (&id)[V]) {
         for (int i = r & 1; i + 1 < V; i += 2) cas_desc<V>(v, id, i, i + 1);
 }
 
-// Value of lane (lane ^ j) for j in {1, 2, 4, 8, 16, 32}: DPP quad_perm, ds_swizzle (xor within
-// 32 lanes) and the gfx950 permlane swaps; no LDS traffic.
+// Value of lane (lane ^ j) for j in {1, 2, 4, 8, 16, 32}: DPP (quad permutations, the half-row
+// mirror, row rotation by 8) and the gfx950 permlane swaps; no LDS traffic.
 template <int J>
 __device__ __forceinline__ int lane_xor(int v) {
     if constexpr (J == 1) return __builtin_amdgcn_mov_dpp(v, kDppXor1, 0xF, 0xF, true);
     else if constexpr (J == 2) return __builtin_amdgcn_mov_dpp(v, kDppXor2, 0xF, 0xF, true);
-    else if constexpr (J == 4 || J == 8) return __builtin_amdgcn_ds_swizzle(v, 0x1F | (J << 10));
+    else if constexpr (J == 4) {   // i ^ 4 = the quad reversal of the half-row mirror (7 - i within 8)
+        const int m = __builtin_amdgcn_mov_dpp(v, kDppHalfMirror, 0xF, 0xF, true);
+        return __builtin_amdgcn_mov_dpp(m, 0x1B, 0xF, 0xF, true);   // quad_perm [3,2,1,0]
+    } else if constexpr (J == 8) return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, true);   // row_ror:8
     else if constexpr (J == 16) {
         const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
         return (threadIdx.x & 16) ? int(r[0]) : int(r[1]);
@@ -310,7 +313,6 @@ template <int V>
 __device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, int K, int q, bool active,
                                             TopkLds& S, float& mx) {
     const int lane = threadIdx.x & 63;
-    FRT_PROBE(3, 0);
     if (!active) {   // a group without a token only keeps the workgroup's barrier count (its SIMDs
                      // are shared with the working groups)
         mx = 0.0f;
@@ -335,10 +337,6 @@ __device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, 
 #pragma unroll
         for (int i = 0; i < V; ++i) v[i] = (active && V * lane + i < E) ? l[V * lane + i] : -INFINITY;
     }
-#ifdef FRT_PHASE_PROBE
-    __builtin_amdgcn_s_waitcnt(0);
-#endif
-    FRT_PROBE(3, 1);
     float lm = v[0];
     int li = V * lane;
 #pragma unroll
@@ -357,7 +355,6 @@ __device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, 
     }
     if (active) S.part[q][lane] = cnt;
     __syncthreads();
-    FRT_PROBE(3, 2);
     const int rank = S.part[0][lane] + S.part[1][lane] + S.part[2][lane] + S.part[3][lane];
     const int kl = __ffsll((long long)__ballot(rank == K - 1)) - 1;
     const int l0 = __ffsll((long long)__ballot(rank == 0)) - 1;
@@ -382,7 +379,6 @@ __device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, 
         }
     }
     __syncthreads();
-    FRT_PROBE(3, 3);
     if (C <= 64) {
         const float cv = lane < C ? S.cand_v[lane] : -INFINITY;
         const int ci = lane < C ? S.cand_id[lane] : 0x7fffffff;
@@ -409,7 +405,6 @@ __device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, 
             cnt2 += int((16 * q + jj < C) & ((ov[jj] > cv) | ((ov[jj] == cv) & (oi[jj] < ci))));
         if (active) S.part[q][lane] = cnt2;
         __syncthreads();
-        FRT_PROBE(3, 4);
         const int r2 = S.part[0][lane] + S.part[1][lane] + S.part[2][lane] + S.part[3][lane];
         if (active && q == 0 && lane < C && r2 < K) {
             S.sel_v[r2] = cv;
@@ -443,7 +438,6 @@ __device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, 
         }
     }
     __syncthreads();
-    FRT_PROBE(3, 5);
 }
 
 // Canonical RMS scale of one token by one wave: chains j = 64 lanes over contiguous L = n / 64

@@ -22,7 +22,8 @@ import torch
 from ._lib import LAYER_NORM_INPUT, FrtArena, FrtError, FrtMoeLayer, check, lib
 
 __all__ = ["FrtError", "ExpertArena", "arena_alloc", "arena_free", "moe_route_topk", "router_logits", "quantize_q8",
-           "moe_dispatch", "moe_q2", "moe_hits_scratch_bytes", "moe_hits", "MoeLayer", "expert_bytes", "gen"]
+           "moe_dispatch", "moe_q2", "moe_hits_scratch_bytes", "moe_hits", "MoeLayer", "expert_bytes", "gen",
+           "set_option", "layer_sync_error"]
 
 
 def _p(t) -> int | None:
@@ -147,7 +148,9 @@ moe_q2 = SimpleNamespace(workspace_bytes=_q2_workspace_bytes, run=_q2_run)
 
 # ---------------------------------------------------------------- decode hits
 
-def moe_hits_scratch_bytes(K: int, ff: int, T: int = 1, n: int = 2048) -> int:
+def moe_hits_scratch_bytes(K: int, ff: int, T: int = 1, n: int = 4096) -> int:
+    """Scratch for moe_hits; n defaults to the largest d_model decode supports (4096), so that a
+    reference-style call without n is never undersized."""
     return int(lib().frt_moe_hits_scratch_bytes(K, ff, T, n))
 
 
@@ -191,6 +194,20 @@ class MoeLayer:
         ws = self.workspace(T) if ws is None else ws
         check(lib().frt_moe_layer_forward(C.byref(self.raw), _p(x), T, _p(resid), _p(out), _p(ids), _p(wts),
                                           _p(counts), _p(ws), ws.numel(), _s(stream)))
+
+
+def set_option(name: str, value: int) -> None:
+    """frt_set_option: "decode_fused" (1: single-token layers in one persistent launch, 0: three
+    kernels) or "sync_ticks" (bound of the persistent launch's waits, 100 MHz ticks)."""
+    check(lib().frt_set_option(name.encode(), int(value)))
+
+
+def layer_sync_error(ws, stream=None) -> bool:
+    """True if a persistent single-token call on this workspace ran out of time since the last check."""
+    rc = lib().frt_moe_layer_sync_error(_p(ws), _s(stream))
+    if rc < 0:
+        check(rc)
+    return rc == 1
 
 
 # ---------------------------------------------------------------- synthetic inputs

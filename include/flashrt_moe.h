@@ -131,9 +131,25 @@ typedef struct frt_moe_layer {
      * No reference counterpart (the reference's router is a ggml linear, blocks.hpp:85). */
     const float* next_router_w;
 } frt_moe_layer;
+/* The workspace's first bytes hold the single-token path's synchronisation words: they are zeroed by
+ * the first call that sees the workspace and must not be written by the caller between calls. */
 size_t frt_moe_layer_workspace_bytes(const frt_moe_layer* L, int T);
 int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out, int32_t* ids,
                           float* wts, uint32_t* counts, void* ws, size_t ws_bytes, void* stream);
+
+/* Runtime options (no reference counterpart; for tests and measurement harnesses):
+ *   "decode_fused" (default 1): single-token layer calls run as one persistent launch (router, then
+ *       routing + gate/up, then down, joined inside the kernel); 0 selects the three-kernel path
+ *       (router kernel, routing + gate/up kernel, down kernel). Both give identical results.
+ *   "sync_ticks" (default 20000000): bound of a persistent call's waits for other workgroups, in
+ *       ticks of the GPU's 100 MHz constant clock; past it the call completes with undefined
+ *       outputs and sets the error word that frt_moe_layer_sync_error reports.
+ * Returns FRT_ERR_SHAPE for an unknown name or a bad value. Not thread-safe against running calls. */
+int frt_set_option(const char* name, int64_t value);
+/* Reads and clears the error word of a layer workspace (synchronises the stream): 1 if a persistent
+ * single-token call on this workspace ran out of time waiting for another workgroup since the last
+ * check, 0 if not, negative on a HIP error. No reference counterpart. */
+int frt_moe_layer_sync_error(void* ws, void* stream);
 
 /* ---- seeded synthetic inputs written on the device (no reference counterpart: the reference's
  * tests draw from std::mt19937; this recipe is documented in flashrt_amd/csrc/gen.hip) ---- */

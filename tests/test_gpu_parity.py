@@ -641,3 +641,103 @@ def test_cpp_mirror_gpu():
     r = subprocess.run([exe, "--gpu"], capture_output=True, text=True, timeout=120)
     print(r.stdout)
     assert r.returncode == 0 and "all passed" in r.stdout, r.stdout + r.stderr
+
+
+# ---------------------------------------------------------------- the persistent single-token layer
+
+def _fused_vs_three(F, w, x, resid=None, reps=3):
+    """The single-token layer through the persistent launch (several calls on one workspace, so the
+    epochs advance) and through the three-kernel path: identical ids, weights and outputs, and no
+    wait ran out of time."""
+    ws = w.layer_obj.workspace(1)
+    outs = []
+    try:
+        F.set_option("decode_fused", 0)
+        ref = w.gpu_forward(x, resid=resid)
+        F.set_option("decode_fused", 1)
+        for _ in range(reps):
+            outs.append(w.gpu_forward(x, resid=resid))
+    finally:
+        F.set_option("decode_fused", 1)
+    assert not F.layer_sync_error(ws)
+    for o in outs:
+        for a, b in zip(o, ref):
+            assert np.array_equal(a, b)
+    return outs[0]
+
+
+@pytest.mark.parametrize("case", ["cfg0", "stack", "E128", "E1000", "n2560", "n1024_ff1024", "K32"])
+def test_decode_fused_matches_three_kernel(F, case):
+    """Persistent single-token layer == three-kernel path bit for bit, and within the bars of the
+    oracle, over shapes: config 0; a config 2 layer (RMS norm, Zipf bias, residual); E = 128 and 1000
+    (one and two wave-halves of logits per lane); the reference tests' 2560 / 640; n = 1024 with
+    ff = 1024 (more h blocks than workgroups); K = 32 (33 entries, a second down batch)."""
+    rng = np.random.default_rng(hash(case) % 1000)
+    kw = {}
+    resid = None
+    if case == "stack":
+        kw = dict(cfg=2, layer=9, bias=O.gen_zipf_bias(2, 9, H.E, H.ZIPF_S_STACK), norm_input=True)
+    elif case == "E128":
+        kw = dict(cfg=0, E=128)
+    elif case == "E1000":
+        kw = dict(cfg=0, E=1000)
+    elif case == "n2560":
+        kw = dict(cfg=0, n=2560, ff=640)
+    elif case == "n1024_ff1024":
+        kw = dict(cfg=0, n=1024, ff=1024)
+    elif case == "K32":
+        kw = dict(cfg=0, K=32)
+    else:
+        kw = dict(cfg=0)
+    w = H.World(**kw)
+    x = (rng.standard_normal((1, w.n)) * (3.0 if case == "stack" else 1.0)).astype(np.float32)
+    if case == "stack":
+        resid = x
+    out, ids, wts = _fused_vs_three(F, w, x, resid=resid)
+    ref, rid, rw, _ = w.oracle_forward(x)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    assert H.out_rel(out - (x if resid is not None else 0), ref) <= H.OUT_REL
+
+
+def test_decode_fused_router_logits_bit_exact(F):
+    """The persistent layer's router logits with the stack's RMS norm (read back from the
+    workspace's tagged logit words) equal the oracle's canonical router on rmsnorm(x) bit for bit,
+    the shared gate logit included."""
+    bias = O.gen_zipf_bias(2, 3, H.E, H.ZIPF_S_STACK)
+    w = H.World(cfg=2, layer=3, bias=bias, norm_input=True)
+    x = (np.random.default_rng(3).standard_normal((1, H.N)) * 4).astype(np.float32)
+    ws = w.layer_obj.workspace(1)
+    xd = dev(x)
+    out = torch.empty((1, H.N), dtype=torch.float32, device="cuda")
+    w.layer_obj.forward(xd, out, T=1, ws=ws)
+    torch.cuda.synchronize()
+    # the logit words follow the 4352-byte header, one per 128-byte line
+    words = ws[4352:4352 + 128 * (H.E + 1)].cpu().numpy().view(np.uint64)[::16]
+    got = (words & np.uint64(0xFFFFFFFF)).astype(np.uint32).view(np.float32)
+    u = O.rmsnorm(x)
+    ref = O.router_logits(u, w.router_h, bias)[0]
+    gate = O.router_logits(u, w.gate_h.reshape(1, H.N), None)[0, 0]
+    assert np.array_equal(got[:H.E], ref)
+    assert got[H.E] == gate
+
+
+def test_decode_fused_timeout_path(F, w0):
+    """With a zero wait bound the persistent layer cannot wait for the other workgroups: every call
+    still completes (no hang), the error word reports it, and the next call with the normal bound
+    returns the right answer again."""
+    x = O.gen_normal(0, 0, O.X_TENSOR, H.N).reshape(1, H.N)
+    ws = w0.layer_obj.workspace(1)
+    good = w0.gpu_forward(x)
+    assert not F.layer_sync_error(ws)
+    try:
+        F.set_option("sync_ticks", 0)
+        w0.gpu_forward(x)
+        flagged = F.layer_sync_error(ws)
+    finally:
+        F.set_option("sync_ticks", 20000000)
+    again = w0.gpu_forward(x)
+    assert not F.layer_sync_error(ws)
+    for a, b in zip(again, good):
+        assert np.array_equal(a, b)
+    print(f"zero bound flagged: {flagged}")
