@@ -98,7 +98,14 @@ def run_stack(args, F, torch):
     ids = torch.empty((layers, K), dtype=torch.int32, device="cuda")
     stream = torch.cuda.Stream()
 
+    stack = F.MoeStack(mls) if args.decode_path == "stack" else None
+    if stack is not None:
+        ws = torch.empty(stack.workspace_bytes(), dtype=torch.uint8, device="cuda")
+
     def step_body():
+        if stack is not None:   # x_{l+1} = x_l + moe_l(x_l) for the 48 layers in one call
+            stack.forward(xin, buf[1], ids=ids, ws=ws)
+            return
         cur = xin
         for l, ml in enumerate(mls):
             nxt = buf[l % 2]
@@ -324,8 +331,10 @@ def main():
                     help="first run 3 plain device copies of MIB MiB (scales the HBM byte counters of a profile)")
     ap.add_argument("--timing-steps", type=int, default=3, help="decode steps in the per-kernel timing pass")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--decode-path", choices=["fused", "three"], default="fused",
-                    help="single-token layers as one persistent launch (default) or as three kernels")
+    ap.add_argument("--decode-grid", type=int, default=0, help="workgroups of a persistent decode call (0: one per CU)")
+    ap.add_argument("--decode-path", choices=["stack", "fused", "three"], default="stack",
+                    help="the 48 layers as one persistent launch (stack, default), one persistent launch per layer "
+                         "(fused), or three kernels per layer (three)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -345,7 +354,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    F.set_option("decode_fused", 1 if args.decode_path == "fused" else 0)
+    F.set_option("decode_fused", 0 if args.decode_path == "three" else 1)
+    F.set_option("decode_grid", args.decode_grid)
     st = run_stack(args, F, torch)
     if st["sync_error"]:
         sys.exit("bench.py: a persistent decode call ran out of time waiting for another workgroup")
@@ -358,6 +368,8 @@ def main():
     # roofline of the dominant decode kernel
     kt = st["kernels"]
     per_launch_bytes = {   # algorithmic HBM bytes per launch (weights read once; activations are KB)
+        "dec1_stack": args.layers * ((K + 1) * F.expert_bytes(N, FF) + E * N * 4 + N * 4),
+        "dec1_layer": (K + 1) * F.expert_bytes(N, FF) + E * N * 4 + N * 4,
         "dec_route_gateup": (K + 1) * 2 * F.lib().frt_q2_mat_bytes(FF, N),
         "dec_down": (K + 1) * F.lib().frt_q2_mat_bytes(N, FF),
         "router_quant": E * N * 4 + N * 4,

@@ -89,8 +89,12 @@ int dec1_layer(const float* x, const float* W, const float* bias, const float* g
                float* out, int32_t* ids, float* wts, uint32_t* counts, void* sync_ws, const float* next_w,
                hipStream_t stream);
 int dec1_status(void* sync_ws, hipStream_t stream, uint32_t* err);
+int dec1_support(int E, int K, int n, int ff);
+int dec1_stack(const frt_moe_layer* L, int n_layer, const float* x, float* out, int32_t* ids, float* wts,
+               void* sync_ws, hipStream_t stream);
 extern int g_dec1_on;
 extern uint64_t g_dec1_ticks;
+extern int g_dec1_grid_cap;
 // prefill.hip
 size_t pf_workspace_bytes(int T, int K, int n, int ff, int E, bool shared, bool own_yd);
 int pf_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const float* x, const int32_t* ids, int T, int K,
@@ -337,7 +341,7 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     float* wts_o = wts ? wts : w.wts;
     const int norm = (L->flags & FRT_LAYER_NORM_INPUT) ? 1 : 0;
     timing_mark(s, "begin");
-    if (T == 1 && g_dec1_on && dec1_eligible(E, K, n, ff))   // the whole layer in one persistent launch
+    if (T == 1 && g_dec1_on && dec1_support(E, K, n, ff) >= 1)   // the whole layer in one persistent launch
         return dec1_layer(x, L->router_w, L->router_bias, L->gate_w, E, K, L->experts, L->stride, L->shared, n, ff,
                           norm, resid, out, ids_o, wts_o, counts, w.sync, L->next_router_w, s);
     if (T <= kDecodeMaxT && T * K <= 63) {
@@ -367,10 +371,65 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
                   w.rest_bytes, s);
 }
 
+size_t frt_moe_stack_workspace_bytes(const frt_moe_layer* layers, int n_layer) {
+    if (!layers || n_layer < 1) return 0;
+    return frt_moe_layer_workspace_bytes(&layers[0], 1) + 2 * up256(size_t(layers[0].d_model) * 4);
+}
+
+int frt_moe_stack_forward(const frt_moe_layer* layers, int n_layer, const float* x, float* out, int32_t* ids,
+                          float* wts, void* ws, size_t ws_bytes, void* stream) {
+    if (!layers || !x || !out || !ws) return set_error(kErrNull, "moe_stack: null pointer");
+    if (n_layer < 1) return set_error(kErrShape, "moe_stack: n_layer=%d", n_layer);
+    const frt_moe_layer& L0 = layers[0];
+    for (int l = 0; l < n_layer; ++l) {
+        const frt_moe_layer& Ll = layers[l];
+        if (!Ll.experts || !Ll.shared || !Ll.router_w || !Ll.gate_w) return set_error(kErrNull, "moe_stack: layer %d weights missing", l);
+        if (Ll.n_expert != L0.n_expert || Ll.top_k != L0.top_k || Ll.d_model != L0.d_model || Ll.d_ff != L0.d_ff ||
+            Ll.stride != L0.stride || Ll.flags != L0.flags)
+            return set_error(kErrShape, "moe_stack: layer %d differs in shape, stride or flags from layer 0", l);
+    }
+    const size_t need = frt_moe_stack_workspace_bytes(layers, n_layer);
+    if (ws_bytes < need) return set_error(kErrWorkspace, "moe_stack: workspace %zu < %zu", ws_bytes, need);
+    const int E = L0.n_expert, K = L0.top_k, n = L0.d_model, ff = L0.d_ff;
+    if (E < 1 || E > 1024 || K < 1 || K > 32 || K > E) return set_error(kErrShape, "moe_stack: E=%d K=%d", E, K);
+    if (L0.stride < expert_bytes(n, ff)) return set_error(kErrShape, "moe_stack: stride %zu < blob", L0.stride);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t lw = frt_moe_layer_workspace_bytes(&L0, 1);
+    float* buf[2] = {reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + lw),
+                     reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + lw + up256(size_t(n) * 4))};
+    constexpr int kChunk = 64;   // layers of one persistent launch
+    const float* cur = x;
+    if (g_dec1_on && dec1_support(E, K, n, ff) == 2) {
+        const LayerWs w = layer_carve(ws, L0, 1, ws_bytes);
+        for (int l0 = 0, c = 0; l0 < n_layer; l0 += kChunk, ++c) {
+            const int nl = n_layer - l0 < kChunk ? n_layer - l0 : kChunk;
+            float* dst = l0 + nl == n_layer ? out : buf[c % 2];
+            if (int rc = dec1_stack(layers + l0, nl, cur, dst, ids ? ids + size_t(l0) * K : nullptr,
+                                    wts ? wts + size_t(l0) * K : nullptr, w.sync, s))
+                return rc;
+            cur = dst;
+        }
+        return kOk;
+    }
+    for (int l = 0; l < n_layer; ++l) {   // layer by layer
+        float* dst = l + 1 == n_layer ? out : buf[l % 2];
+        if (int rc = frt_moe_layer_forward(&layers[l], cur, 1, cur, dst, ids ? ids + size_t(l) * K : nullptr,
+                                           wts ? wts + size_t(l) * K : nullptr, nullptr, ws, lw, stream))
+            return rc;
+        cur = dst;
+    }
+    return kOk;
+}
+
 int frt_set_option(const char* name, int64_t value) {
     if (!name) return set_error(kErrNull, "set_option: null name");
     if (!std::strcmp(name, "decode_fused")) {
         g_dec1_on = value ? 1 : 0;
+        return kOk;
+    }
+    if (!std::strcmp(name, "decode_grid")) {
+        if (value < 0 || value > 1024) return set_error(kErrShape, "set_option: decode_grid %lld", (long long)value);
+        g_dec1_grid_cap = int(value);
         return kOk;
     }
     if (!std::strcmp(name, "sync_ticks")) {

@@ -27,7 +27,23 @@
 // call's. Every wait is bounded by ticks of the 100 MHz constant clock
 // (20M by default) for the whole call: past it the call sets the error word and finishes with what it read, so a
 // workgroup that never became resident cannot hang the GPU.
+#include <hip/hip_runtime.h>
+
+// In this file threadIdx.x is read through an empty volatile asm: values derived from it are then
+// computed where they are used rather than hoisted out of the stack kernel's layer loop, which kept
+// dozens of per-thread addresses live across the whole loop and spilled registers.
+struct FrtOpaqueTid {
+    __device__ unsigned get_x() const {
+        unsigned t = __builtin_amdgcn_workitem_id_x();
+        asm volatile("" : "+v"(t));
+        return t;
+    }
+    __declspec(property(get = get_x)) unsigned x;
+};
+#define threadIdx (FrtOpaqueTid{})
 #include "decode_parts.hpp"
+
+#include "../../include/flashrt_moe.h"
 
 #include <map>
 #include <mutex>
@@ -39,9 +55,10 @@ namespace frt {
 constexpr int kMaxGrid = 1024;
 constexpr int kLgStride = 16;   // words between two logits: every workgroup polls every logit, and
                                 // pollers of one line queue on it
+constexpr uint32_t kErrMagic = 0x5E7C0DE5u;   // upper half of a set error word (garbage rarely matches)
 struct Dec1Sync {
-    uint32_t err;                // bit 0: a wait ran out of time
-    uint32_t pad[63];
+    uint64_t err;                // (kErrMagic << 32) | epoch of a call whose wait ran out of time; else anything
+    uint32_t pad[62];
     uint32_t epoch[kMaxGrid];    // per workgroup: its last call's epoch
 };
 
@@ -60,11 +77,11 @@ __device__ __forceinline__ uint64_t peek(const uint64_t* p) {
 }
 
 // Waits for the tagged words i = threadIdx.x + k kNT1 < count (k < MAXK), word i at base + i STRIDE,
-// and hands each payload to put(i, payload). Out of time: sets the error word and hands over what it
-// last read.
+// and hands each payload to put(i, payload). Out of time: sets the error word (err_val) and hands
+// over what it last read.
 template <int MAXK, int STRIDE = 1, class F>
 __device__ __forceinline__ void wait_words(const uint64_t* base, int count, uint32_t tag, uint64_t deadline,
-                                           uint32_t* err, F put) {
+                                           uint64_t* err, uint64_t err_val, F put) {
     uint32_t pend = 0;
 #pragma unroll
     for (int k = 0; k < MAXK; ++k)
@@ -80,7 +97,7 @@ __device__ __forceinline__ void wait_words(const uint64_t* base, int count, uint
                 pend &= ~(1u << k);
             }
         if (pend && wall_clock64() > deadline) {
-            atomicOr(err, 1u);
+            __hip_atomic_store(err, err_val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
             for (int k = 0; k < MAXK; ++k)
                 if ((pend >> k) & 1u) put(int(threadIdx.x) + k * kNT1, uint32_t(v[k]));
@@ -90,19 +107,27 @@ __device__ __forceinline__ void wait_words(const uint64_t* base, int count, uint
 }
 
 
-struct Dec1Args {
-    const float* x;        // [n] layer input
+constexpr int kMaxStack = 64;   // layers of one stack call (their table travels in the kernel arguments)
+
+struct Dec1Layer {
     const float* W;        // [E][n] router
     const float* bias;     // [E] or null
     const float* gate_w;   // [n] shared-expert gate
     const uint8_t* arena;  // routed expert 0 of the layer
-    size_t stride;
     const uint8_t* shared;
-    const float* resid;    // [n] or null
-    float* out;            // [n]
-    int32_t* ids;          // [K] rank order
-    float* wts;            // [K]
-    uint32_t* counts;      // [E] or null
+};
+
+struct Dec1Args {
+    Dec1Layer lay[kMaxStack];
+    int n_layer;           // 1: one layer (resid optional); more: a stack, x_{l+1} = x_l + moe_l(x_l)
+    const float* x;        // [n] the (first) layer's input
+    size_t stride;
+    const float* resid;    // [n] or null (one layer)
+    float* out;            // [n] the (last) layer's output
+    int32_t* ids;          // [n_layer][K] rank order, or null
+    float* wts;            // [n_layer][K], or null
+    uint32_t* counts;      // [E] or null (one layer)
+    uint64_t* xb;          // [n] tagged words of the next layer's input (a stack)
     Dec1Sync* sync;
     uint64_t* lg;          // [E + 1] tagged logits (the shared gate last), one per 128-byte line (kLgStride words)
     uint64_t* hb;          // [U * ff/32][9] tagged h blocks: 8 words of 4 codes, then the scale
@@ -111,13 +136,20 @@ struct Dec1Args {
     int E, K, ff, norm;
 };
 
+typedef const __attribute__((address_space(4))) Dec1Args KArgs;
+typedef const __attribute__((address_space(4))) Dec1Layer KLayer;
+
 struct Dec1Lds {
     WinLds R;
     float s_h[32];
 };
 
-template <int NB, int V, int NBF>
-__global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
+template <int NB, int V, int NBF, bool STACK>
+__global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
+    // the arguments are read where they lie (the kernel argument segment, scalar loads): indexing
+    // the layer table of a by-value copy would place the whole block in private memory
+    (void)a_byval;
+    const KArgs& a = *(const KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
     constexpr int n = 64 * NB, L = NB;   // the router's 64 chains are L = n / 64 long
     extern __shared__ __align__(16) uint8_t smem[];   // sh_q [U][ff] | sh_d [U][ff/32] | sh_y [U][8]
     __shared__ float xs[64 * (L + 1)];                // x by chain, each chain padded by one float
@@ -146,19 +178,23 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
     const int s0 = b + wave * G;
     const bool rs = s0 <= E;
     float wr[L];
-    if (rs) {
-        const float* wrow = s0 < E ? a.W + size_t(s0) * n : a.gate_w;
-        const float4* w4 = reinterpret_cast<const float4*>(wrow + lane * L);
+    float bias_v = 0.0f;
+    auto load_router = [&](const KLayer& LY) {
+        if (rs) {
+            const float* wrow = s0 < E ? LY.W + size_t(s0) * n : LY.gate_w;
+            const float4* w4 = reinterpret_cast<const float4*>(wrow + lane * L);
 #pragma unroll
-        for (int i = 0; i < L / 4; ++i) {
-            const float4 v = w4[i];
-            wr[4 * i] = v.x;
-            wr[4 * i + 1] = v.y;
-            wr[4 * i + 2] = v.z;
-            wr[4 * i + 3] = v.w;
+            for (int i = 0; i < L / 4; ++i) {
+                const float4 v = w4[i];
+                wr[4 * i] = v.x;
+                wr[4 * i + 1] = v.y;
+                wr[4 * i + 2] = v.z;
+                wr[4 * i + 3] = v.w;
+            }
         }
-    }
-    const float bias_v = a.bias ? a.bias[min(s0, E - 1)] : 0.0f;
+        bias_v = LY.bias ? LY.bias[min(s0, E - 1)] : 0.0f;
+    };
+    load_router(a.lay[0]);
     constexpr int XV = (n / 4 + kNT1 - 1) / kNT1;
     float4 xv[XV];
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
@@ -183,7 +219,20 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
 #pragma unroll
     for (int w = 1; w < kNW1; ++w) ep = max(ep, s_ep[w]);
     ep += 1u;
-    const uint32_t tag = sync_tag(ep);
+    constexpr bool stack = STACK;
+    const uint64_t err_val = (uint64_t(kErrMagic) << 32) | ep;
+    const int n_layer = STACK ? a.n_layer : 1;
+    for (int l = 0; l < n_layer; ++l) {
+    const KLayer& LY = a.lay[l];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;   // per layer (see FrtOpaqueTid)
+    const uint32_t tag = sync_tag(ep * uint32_t(kMaxStack) + uint32_t(l));
+    if (l > 0) {   // x_l from the previous layer's down rows
+        load_router(LY);   // rows warmed into this XCD's L2 by the previous layer: they land during the wait
+        __syncthreads();   // the previous combine has read xs
+        wait_words<(64 * 64 + kNT1 - 1) / kNT1>(a.xb, n, tag, deadline, &a.sync->err, err_val,
+                                                [&](int i, uint32_t p) { xs[(i / L) * (L + 1) + i % L] = __uint_as_float(p); });
+        __syncthreads();
+    }
     const float r = a.norm ? rms_scale_wave<L>(xs + lane * (L + 1), n) : 1.0f;
     auto router_dot = [&](int s, const float (&w)[L], float bv) {
         const float* xc = xs + lane * (L + 1);
@@ -199,16 +248,16 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
             for (int i = 0; i < L; ++i) acc = fmaf(w[i], xc[i], acc);
         }
         acc = wave_sum_tree(acc);
-        if (s < E && a.bias) acc = acc + bv;
+        if (s < E && LY.bias) acc = acc + bv;
         if (lane == 0) pub(a.lg + size_t(s) * kLgStride, tag, __float_as_uint(acc));
     };
     if (rs) router_dot(s0, wr, bias_v);
     for (int s = s0 + kNW1 * G; s <= E; s += kNW1 * G) {   // only with fewer than (E + 1) / 8 workgroups
         float w2[L];
-        const float* wrow = s < E ? a.W + size_t(s) * n : a.gate_w;
+        const float* wrow = s < E ? LY.W + size_t(s) * n : LY.gate_w;
 #pragma unroll
         for (int i = 0; i < L; ++i) w2[i] = wrow[lane * L + i];
-        router_dot(s, w2, a.bias && s < E ? a.bias[s] : 0.0f);
+        router_dot(s, w2, LY.bias && s < E ? LY.bias[s] : 0.0f);
     }
     // Q8_0 of the experts' input (u = x r with the norm) by the last two waves, which hold no router
     // row (with one workgroup per CU, (E + 1) / G < 6): a lane pair per 32-block, 16 values a lane
@@ -243,7 +292,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
     }
 
     // ---- 2. all logits, the routing, gate/up
-    wait_words<(1024 + 1 + kNT1 - 1) / kNT1, kLgStride>(a.lg, E + 1, tag, deadline, &a.sync->err,
+    wait_words<(1024 + 1 + kNT1 - 1) / kNT1, kLgStride>(a.lg, E + 1, tag, deadline, &a.sync->err, err_val,
                                             [&](int i, uint32_t p) { s_lg[i] = __uint_as_float(p); });
     __syncthreads();
     if (wave == 0) {
@@ -261,7 +310,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
 #pragma unroll
             for (int i = 0; i < V; ++i) v[i] = s_lg[min(V * lane + i, E - 1)];   // past E: masked by the keys
         }
-        route1_wave<V, true>(v, E, K, s_lg[E], a.arena, a.stride, a.shared, R);
+        route1_wave<V, true>(v, E, K, s_lg[E], LY.arena, a.stride, LY.shared, R);
     }
     __syncthreads();
     if (R.many) {   // more than 64 candidates (heavily tied logits): four waves select, as window_entries
@@ -276,7 +325,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
                 R.ids[0][lane] = sel_id;
                 R.w[0][lane] = sel_l;
                 DecEntry& d = R.ent[u];
-                d.blob = a.arena + size_t(sel_id) * a.stride;
+                d.blob = LY.arena + size_t(sel_id) * a.stride;
                 d.ntok = 1;
                 d.base = u;
                 d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
@@ -286,7 +335,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
                 d.w[1] = d.w[2] = d.w[3] = 0.0f;
             } else if (lane == K) {
                 DecEntry& d = R.ent[K];
-                d.blob = a.shared;
+                d.blob = LY.shared;
                 d.ntok = 1;
                 d.base = K;
                 d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
@@ -401,15 +450,15 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
     // sum in rank order; the shared expert's: sigmoid(gate)), then each entry's
     if (wave == 0) {
         const bool rk = lane < K;
-        const float l = rk ? R.w[0][lane] : 0.0f;
-        const float e = rk ? expf(l - R.w[0][0]) : 0.0f;
+        const float lv = rk ? R.w[0][lane] : 0.0f;
+        const float e = rk ? expf(lv - R.w[0][0]) : 0.0f;
         float ws = 0.0f;
         for (int k = 0; k < K; ++k) ws += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), k));
         const float w = e / ws;
         if (b == 0 && rk) {
             const int id = R.ids[0][lane];
-            a.ids[lane] = id;
-            a.wts[lane] = w;
+            if (a.ids) a.ids[l * K + lane] = id;
+            if (a.wts) a.wts[l * K + lane] = w;
             if (a.counts) atomicAdd(a.counts + id, 1u);
         }
         const int rank = lane < U ? R.ent[lane].slot[0] : 0;
@@ -434,14 +483,17 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
     // the down rows of this workgroup's 8 output rows for every entry (the first 16 entries), issued
     // once the gate/up rows no longer compete with them; they land during the wait below
     if (has_down) down_load<NBF, BATCH, kNW1, true>(R.ent, U, wave, r0, n, ff, D);
+    // warm this XCD's L2 with the router rows this workgroup reads next: the next layer's (a stack),
+    // else the next call's
+    const float* warm_w = l + 1 < n_layer ? a.lay[l + 1].W : a.next_w;
     float4 nv[L / 4];
-    const bool warm = a.next_w && rs && s0 < E;
+    const bool warm = warm_w && rs && s0 < E;
     if (warm) {
-        const float4* w4 = reinterpret_cast<const float4*>(a.next_w + size_t(s0) * n + lane * L);
+        const float4* w4 = reinterpret_cast<const float4*>(warm_w + size_t(s0) * n + lane * L);
 #pragma unroll
         for (int i = 0; i < L / 4; ++i) nv[i] = w4[i];
     }
-    wait_words<kMaxHWords / kNT1>(a.hb, NU * 9, tag, deadline, &a.sync->err, [&](int i, uint32_t p) {
+    wait_words<kMaxHWords / kNT1>(a.hb, NU * 9, tag, deadline, &a.sync->err, err_val, [&](int i, uint32_t p) {
         const int q = i / 9, part = i % 9, u = q / RB, rb = q % RB;
         if (part < 8) *reinterpret_cast<uint32_t*>(sh_q + size_t(u) * ff + rb * 32 + 4 * part) = p;
         else sh_d[u * (ff / kQ8) + rb] = __uint_as_float(p);
@@ -449,6 +501,8 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
     __syncthreads();
     // combine of rows g0 .. g0 + 7 (threads 0..7): the routed entries in ascending expert id from 0,
     // then the shared expert, then the residual (k_dec_down's single-token order)
+    // (a stack adds the layer's input x_l and hands the row to the next layer as a tagged word)
+    const uint32_t tag_next = sync_tag(ep * uint32_t(kMaxStack) + uint32_t(l + 1));
     auto combine = [&](int g0, float rv) {
         if (tid < 8) {
             float acc = 0.0f;
@@ -457,8 +511,11 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
                 acc = acc + p;
             }
             float o = acc + sh_y[K * 8 + tid] * R.ent[K].w[0];
-            if (a.resid) o = rv + o;
-            a.out[g0 + tid] = o;
+            const int row = g0 + tid;
+            if (stack) o = xs[(row / L) * (L + 1) + row % L] + o;
+            else if (a.resid) o = rv + o;
+            if (l + 1 < n_layer) pub(a.xb + row, tag_next, __float_as_uint(o));
+            else a.out[row] = o;
         }
     };
     if (has_down) {
@@ -472,7 +529,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
         combine(r0, res);
     }
     for (int g0 = r0 + 8 * G; g0 < n; g0 += 8 * G) {   // more 8-row groups than workgroups
-        const float rv = a.resid ? a.resid[g0 + (tid & 7)] : 0.0f;
+        const float rv = (!stack && a.resid) ? a.resid[g0 + (tid & 7)] : 0.0f;
         __syncthreads();   // sh_y of the previous group is combined
         for (int u0 = wave; u0 < U; u0 += kNW1 * BATCH) {
             DownRegs<NBF, BATCH> D2;
@@ -488,6 +545,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a) {
         for (int i = 0; i < L / 4; ++i) z += nv[i].x + nv[i].y + nv[i].z + nv[i].w;
         if (E < 0) a.out[0] = z;
     }
+    }   // layers
     if (tid == 0) __hip_atomic_store(&a.sync->epoch[b], ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -504,7 +562,8 @@ __global__ void k_dec1_zero(uint64_t* p, size_t words) {
 constexpr size_t kDec1Head = (sizeof(Dec1Sync) + 255) / 256 * 256;
 constexpr size_t kDec1Lg = size_t(1024 + 1 + 31) / 32 * 32 * 8 * kLgStride;
 constexpr size_t kDec1Hb = size_t(kMaxHWords) * 8;
-size_t dec1_sync_bytes() { return kDec1Head + kDec1Lg + kDec1Hb; }
+constexpr size_t kDec1Xb = size_t(64 * 64) * 8;   // a stack's next-layer input, n <= 4096
+size_t dec1_sync_bytes() { return kDec1Head + kDec1Lg + kDec1Hb + kDec1Xb; }
 
 int dec1_eligible(int E, int K, int n, int ff) {
     const int nb = n / 64, nbf = ff / 64;
@@ -514,6 +573,8 @@ int dec1_eligible(int E, int K, int n, int ff) {
     if ((K + 1) * (ff / 32) * 9 > kMaxHWords) return 0;
     return 1;
 }
+
+constexpr int kErrUnfit = 1;   // internal: the persistent kernel cannot run this shape
 
 namespace {
 std::mutex g_dec1_mu;
@@ -525,38 +586,28 @@ std::map<std::pair<int, const void*>, int> g_dec1_grid;   // (device, kernel) ->
 // the bound of a call's waits (200 ms of the 100 MHz constant clock by default).
 int g_dec1_on = 1;
 uint64_t g_dec1_ticks = 20000000ull;
+int g_dec1_grid_cap = 0;   // workgroups per call (0: one per CU)
 
-int dec1_layer(const float* x, const float* W, const float* bias, const float* gate_w, int E, int K,
-               const uint8_t* arena, size_t stride, const uint8_t* shared, int n, int ff, int norm, const float* resid,
-               float* out, int32_t* ids, float* wts, uint32_t* counts, void* sync_ws, const float* next_w,
-               hipStream_t stream) {
+// Launches the persistent kernel for a filled-in argument block (layers, input and outputs).
+// Returns kErrUnfit (no error message) when the kernel for this shape cannot have every workgroup
+// resident; probe_only: only that check, no launch.
+static int dec1_launch(Dec1Args& a, int E, int K, int n, int ff, int norm, void* sync_ws, const float* next_w,
+                       hipStream_t stream, bool probe_only = false) {
     if (!dec1_eligible(E, K, n, ff)) return set_error(kErrShape, "decode1: E=%d K=%d n=%d ff=%d", E, K, n, ff);
     int dev = 0;
     FRT_HIP(hipGetDevice(&dev));
     uint8_t* base = static_cast<uint8_t*>(sync_ws);
-    Dec1Args a{};
-    a.x = x;
-    a.W = W;
-    a.bias = bias;
-    a.gate_w = gate_w;
-    a.arena = arena;
-    a.stride = stride;
-    a.shared = shared;
-    a.resid = resid;
-    a.out = out;
-    a.ids = ids;
-    a.wts = wts;
-    a.counts = counts;
     a.sync = reinterpret_cast<Dec1Sync*>(base);
     a.lg = reinterpret_cast<uint64_t*>(base + kDec1Head);
     a.hb = reinterpret_cast<uint64_t*>(base + kDec1Head + kDec1Lg);
+    a.xb = reinterpret_cast<uint64_t*>(base + kDec1Head + kDec1Lg + kDec1Hb);
     a.next_w = next_w;
     a.ticks = g_dec1_ticks;
     a.E = E;
     a.K = K;
     a.ff = ff;
     a.norm = norm;
-    {
+    if (!probe_only) {
         // a sync region not seen before is zeroed first: the epochs agree over any cell contents, but
         // leftover words could by chance carry the next call's tag
         std::lock_guard<std::mutex> lk(g_dec1_mu);
@@ -575,30 +626,38 @@ int dec1_layer(const float* x, const float* W, const float* bias, const float* g
             std::lock_guard<std::mutex> lk(g_dec1_mu);
             auto it = g_dec1_grid.find({dev, kfn});
             if (it == g_dec1_grid.end()) {
-                // every workgroup must be resident at once: one per CU, and the kernel must fit
+                // every workgroup must be resident at once: one per CU, the kernel must fit, and it
+                // must need no private (scratch) memory, whose allocation could hold workgroups back
                 int cus = 0, per_cu = 0;
+                hipFuncAttributes fa{};
                 FRT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
                 FRT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kNT1, smem));
-                grid = (per_cu >= 1 && cus >= 1) ? (cus < kMaxGrid ? cus : kMaxGrid) : 0;
+                FRT_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(kern)));
+                grid = (per_cu >= 1 && cus >= 1 && fa.localSizeBytes == 0) ? (cus < kMaxGrid ? cus : kMaxGrid) : 0;
                 g_dec1_grid[{dev, kfn}] = grid;
             } else {
                 grid = it->second;
             }
         }
-        if (grid < 1) return set_error(kErrShape, "decode1: the kernel does not fit one workgroup per CU");
-        launch_timed("dec1_layer", kern, dim3(grid), dim3(kNT1), smem, stream, a);
+        if (grid < 1) return kErrUnfit;
+        if (g_dec1_grid_cap > 0 && g_dec1_grid_cap < grid) grid = g_dec1_grid_cap;
+        if (probe_only) return kOk;
+        launch_timed(a.n_layer > 1 ? "dec1_stack" : "dec1_layer", kern, dim3(grid), dim3(kNT1), smem, stream, a);
         FRT_LAUNCHED("decode1 layer");
         return kOk;
     };
     const int nb = n / 64, nbf = ff / 64;
     const bool v8 = E <= 512;
-#define FRT_D1F(NBV, VV)                                   \
-    switch (nbf) {                                         \
-        case 4: return launch(k_dec1<NBV, VV, 4>);         \
-        case 8: return launch(k_dec1<NBV, VV, 8>);         \
-        case 10: return launch(k_dec1<NBV, VV, 10>);       \
-        case 16: return launch(k_dec1<NBV, VV, 16>);       \
-    }                                                      \
+    const bool st = a.n_layer > 1;
+#define FRT_D1S(NBV, VV, NBFV) \
+    return st ? launch(k_dec1<NBV, VV, NBFV, true>) : launch(k_dec1<NBV, VV, NBFV, false>);
+#define FRT_D1F(NBV, VV)                       \
+    switch (nbf) {                             \
+        case 4: FRT_D1S(NBV, VV, 4)            \
+        case 8: FRT_D1S(NBV, VV, 8)            \
+        case 10: FRT_D1S(NBV, VV, 10)          \
+        case 16: FRT_D1S(NBV, VV, 16)          \
+    }                                          \
     break;
 #define FRT_D1N(NBV)              \
     case NBV:                     \
@@ -613,18 +672,66 @@ int dec1_layer(const float* x, const float* W, const float* bias, const float* g
     }
 #undef FRT_D1N
 #undef FRT_D1F
+#undef FRT_D1S
     return set_error(kErrShape, "decode1: n=%d ff=%d", n, ff);
+}
+
+int dec1_layer(const float* x, const float* W, const float* bias, const float* gate_w, int E, int K,
+               const uint8_t* arena, size_t stride, const uint8_t* shared, int n, int ff, int norm, const float* resid,
+               float* out, int32_t* ids, float* wts, uint32_t* counts, void* sync_ws, const float* next_w,
+               hipStream_t stream) {
+    Dec1Args a{};
+    a.lay[0] = Dec1Layer{W, bias, gate_w, arena, shared};
+    a.n_layer = 1;
+    a.x = x;
+    a.stride = stride;
+    a.resid = resid;
+    a.out = out;
+    a.ids = ids;
+    a.wts = wts;
+    a.counts = counts;
+    return dec1_launch(a, E, K, n, ff, norm, sync_ws, next_w, stream);
+}
+
+// A stack of single-token layers in one launch: x_{l+1} = x_l + moe_l(x_l), out = x_L.
+int dec1_stack(const frt_moe_layer* L, int n_layer, const float* x, float* out, int32_t* ids, float* wts,
+               void* sync_ws, hipStream_t stream) {
+    if (n_layer < 1 || n_layer > kMaxStack) return set_error(kErrShape, "decode1 stack: %d layers (1..%d)", n_layer, kMaxStack);
+    Dec1Args a{};
+    for (int l = 0; l < n_layer; ++l)
+        a.lay[l] = Dec1Layer{L[l].router_w, L[l].router_bias, L[l].gate_w, L[l].experts, L[l].shared};
+    a.n_layer = n_layer;
+    a.x = x;
+    a.stride = L[0].stride;
+    a.out = out;
+    a.ids = ids;
+    a.wts = wts;
+    const int norm = (L[0].flags & FRT_LAYER_NORM_INPUT) ? 1 : 0;
+    if (n_layer == 1) a.resid = x;
+    return dec1_launch(a, L[0].n_expert, L[0].top_k, L[0].d_model, L[0].d_ff, norm, sync_ws,
+                       L[n_layer - 1].next_router_w, stream);
+}
+
+// Whether the persistent kernels can run this shape: 2 = the stack kernel too, 1 = single layers only, 0 = none.
+int dec1_support(int E, int K, int n, int ff) {
+    if (!dec1_eligible(E, K, n, ff)) return 0;
+    Dec1Args a{};
+    a.n_layer = 1;
+    if (dec1_launch(a, E, K, n, ff, 0, nullptr, nullptr, nullptr, true) != kOk) return 0;
+    a.n_layer = 2;
+    return dec1_launch(a, E, K, n, ff, 0, nullptr, nullptr, nullptr, true) == kOk ? 2 : 1;
 }
 
 // Reads and clears the error word of a sync region (synchronous; for tests and harnesses).
 int dec1_status(void* sync_ws, hipStream_t stream, uint32_t* err) {
-    Dec1Sync h{};
-    FRT_HIP(hipMemcpyAsync(&h, sync_ws, sizeof h, hipMemcpyDeviceToHost, stream));
+    uint64_t e = 0;
+    FRT_HIP(hipMemcpyAsync(&e, static_cast<uint8_t*>(sync_ws) + offsetof(Dec1Sync, err), 8, hipMemcpyDeviceToHost,
+                           stream));
     FRT_HIP(hipStreamSynchronize(stream));
-    *err = h.err;
-    if (h.err) {
-        const uint32_t z = 0;
-        FRT_HIP(hipMemcpyAsync(static_cast<uint8_t*>(sync_ws) + offsetof(Dec1Sync, err), &z, 4, hipMemcpyHostToDevice,
+    *err = uint32_t(e >> 32) == kErrMagic ? 1u : 0u;
+    if (e) {
+        const uint64_t z = 0;
+        FRT_HIP(hipMemcpyAsync(static_cast<uint8_t*>(sync_ws) + offsetof(Dec1Sync, err), &z, 8, hipMemcpyHostToDevice,
                                stream));
         FRT_HIP(hipStreamSynchronize(stream));
     }

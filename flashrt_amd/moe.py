@@ -23,7 +23,7 @@ from ._lib import LAYER_NORM_INPUT, FrtArena, FrtError, FrtMoeLayer, check, lib
 
 __all__ = ["FrtError", "ExpertArena", "arena_alloc", "arena_free", "moe_route_topk", "router_logits", "quantize_q8",
            "moe_dispatch", "moe_q2", "moe_hits_scratch_bytes", "moe_hits", "MoeLayer", "expert_bytes", "gen",
-           "set_option", "layer_sync_error"]
+           "set_option", "layer_sync_error", "MoeStack"]
 
 
 def _p(t) -> int | None:
@@ -194,6 +194,35 @@ class MoeLayer:
         ws = self.workspace(T) if ws is None else ws
         check(lib().frt_moe_layer_forward(C.byref(self.raw), _p(x), T, _p(resid), _p(out), _p(ids), _p(wts),
                                           _p(counts), _p(ws), ws.numel(), _s(stream)))
+
+
+class MoeStack:
+    """A stack of single-token MoE layers run as one call (frt_moe_stack_forward):
+    x_{l+1} = x_l + moe_l(x_l), out = x_L. All layers share shape, stride and flags."""
+
+    def __init__(self, layers: list):
+        self.layers = list(layers)
+        self.raw = (FrtMoeLayer * len(self.layers))(*[ml.raw for ml in self.layers])
+        self._ws = None
+
+    def refresh(self) -> None:
+        """Re-reads the layers' descriptors (after set_next_router on one of them)."""
+        for i, ml in enumerate(self.layers):
+            self.raw[i] = ml.raw
+
+    def workspace_bytes(self) -> int:
+        return int(lib().frt_moe_stack_workspace_bytes(self.raw, len(self.layers)))
+
+    def workspace(self) -> torch.Tensor:
+        need = self.workspace_bytes()
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        return self._ws
+
+    def forward(self, x, out, ids=None, wts=None, ws=None, stream=None) -> None:
+        ws = self.workspace() if ws is None else ws
+        check(lib().frt_moe_stack_forward(self.raw, len(self.layers), _p(x), _p(out), _p(ids), _p(wts), _p(ws),
+                                          ws.numel(), _s(stream)))
 
 
 def set_option(name: str, value: int) -> None:

@@ -141,6 +141,8 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
  *   "decode_fused" (default 1): single-token layer calls run as one persistent launch (router, then
  *       routing + gate/up, then down, joined inside the kernel); 0 selects the three-kernel path
  *       (router kernel, routing + gate/up kernel, down kernel). Both give identical results.
+ *   "decode_grid" (default 0): workgroups of a persistent single-token call, at most one per CU (0:
+ *       one per CU).
  *   "sync_ticks" (default 20000000): bound of a persistent call's waits for other workgroups, in
  *       ticks of the GPU's 100 MHz constant clock; past it the call completes with undefined
  *       outputs and sets the error word that frt_moe_layer_sync_error reports.
@@ -150,6 +152,17 @@ int frt_set_option(const char* name, int64_t value);
  * single-token call on this workspace ran out of time waiting for another workgroup since the last
  * check, 0 if not, negative on a HIP error. No reference counterpart. */
 int frt_moe_layer_sync_error(void* ws, void* stream);
+
+/* ---- a stack of single-token MoE layers (no reference counterpart as one call: the engine calls
+ * moe_block_fast once per layer, arch/qwen4exp/forward.cu:214-217; BASELINE config 2 is a stack of
+ * MoE layers chained by the residual). x_0 = x, x_{l+1} = x_l + moe_l(x_l) with each layer's own
+ * flags (all layers share E, K, d_model, d_ff, stride and flags), out = x_{n_layer} [d_model].
+ * ids/wts [n_layer][K] optional. Runs as one persistent launch per 64 layers ("decode_fused", the
+ * default), else as n_layer calls of frt_moe_layer_forward; both give identical results. The last
+ * layer's next_router_w (if any) is warmed for the next call. */
+size_t frt_moe_stack_workspace_bytes(const frt_moe_layer* layers, int n_layer);
+int frt_moe_stack_forward(const frt_moe_layer* layers, int n_layer, const float* x, float* out, int32_t* ids,
+                          float* wts, void* ws, size_t ws_bytes, void* stream);
 
 /* ---- seeded synthetic inputs written on the device (no reference counterpart: the reference's
  * tests draw from std::mt19937; this recipe is documented in flashrt_amd/csrc/gen.hip) ---- */

@@ -741,3 +741,72 @@ def test_decode_fused_timeout_path(F, w0):
     for a, b in zip(again, good):
         assert np.array_equal(a, b)
     print(f"zero bound flagged: {flagged}")
+
+
+def _stack_worlds(nl, x_seed=21):
+    layers = []
+    for layer in range(nl):
+        bias = O.gen_zipf_bias(2, layer, H.E, H.ZIPF_S_STACK)
+        layers.append(H.World(cfg=2, layer=layer, bias=bias, norm_input=True))
+    x0 = torch.from_numpy(O.gen_normal(2, 0, O.X_TENSOR + x_seed, H.N).reshape(1, H.N)).cuda()
+    return layers, x0
+
+
+def _layer_chain(layers, x0):
+    cur = x0
+    outs, ids, wts = [], torch.empty((len(layers), H.K), dtype=torch.int32, device="cuda"), \
+        torch.empty((len(layers), H.K), dtype=torch.float32, device="cuda")
+    for l, w in enumerate(layers):
+        nxt = torch.empty((1, H.N), dtype=torch.float32, device="cuda")
+        w.layer_obj.forward(cur, nxt, T=1, resid=cur, ids=ids[l], wts=wts[l])
+        outs.append(nxt)
+        cur = nxt
+    torch.cuda.synchronize()
+    return outs, ids, wts
+
+
+@pytest.mark.parametrize("nl", [1, 6])
+def test_decode_stack_call_matches_layer_calls(F, nl):
+    """frt_moe_stack_forward (config 2 layers: RMS norm, Zipf bias, residual chain) as one
+    persistent launch equals the chain of single-layer calls bit for bit (ids, weights, output),
+    with the three-kernel layer-by-layer path too; three graph replays of the stack call equal it."""
+    layers, x0 = _stack_worlds(nl)
+    st = F.MoeStack([w.layer_obj for w in layers])
+    outs, ids_ref, wts_ref = _layer_chain(layers, x0)
+    out = torch.empty((1, H.N), dtype=torch.float32, device="cuda")
+    ids = torch.full((nl, H.K), -1, dtype=torch.int32, device="cuda")
+    wts = torch.zeros((nl, H.K), dtype=torch.float32, device="cuda")
+    ws = st.workspace()
+    st.forward(x0, out, ids=ids, wts=wts, ws=ws)
+    torch.cuda.synchronize()
+    assert not F.layer_sync_error(ws)
+    assert torch.equal(ids, ids_ref)
+    assert torch.equal(wts, wts_ref)
+    assert torch.equal(out, outs[-1])
+    try:
+        F.set_option("decode_fused", 0)
+        out3 = torch.empty_like(out)
+        st.forward(x0, out3, ws=ws)
+        torch.cuda.synchronize()
+    finally:
+        F.set_option("decode_fused", 1)
+    assert torch.equal(out3, out)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        st.forward(x0, out, ids=ids, wts=wts, ws=ws, stream=s)
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        st.forward(x0, out, ids=ids, wts=wts, ws=ws, stream=s)
+    for i in range(3):
+        out.fill_(float("nan"))
+        ids.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, outs[-1]), i
+        assert torch.equal(ids, ids_ref), i
+        with torch.cuda.stream(s):
+            st.forward(x0, out, ws=ws, stream=s)   # eager work between the replays
+        s.synchronize()
+    assert not F.layer_sync_error(ws)
