@@ -53,8 +53,11 @@ struct FrtOpaqueTid {
 namespace frt {
 
 constexpr int kMaxGrid = 1024;
-constexpr int kLgStride = 16;   // words between two logits: every workgroup polls every logit, and
-                                // pollers of one line queue on it
+// Words between two published words of the logits, h blocks and x: every workgroup polls every
+// word, pollers of one line queue on it, and more lines mean more requests (measured: 4 / 1 / 1).
+constexpr int kLgStride = 4;
+constexpr int kHbStride = 1;
+constexpr int kXbStride = 1;
 constexpr uint32_t kErrMagic = 0x5E7C0DE5u;   // upper half of a set error word (garbage rarely matches)
 struct Dec1Sync {
     uint64_t err;                // (kErrMagic << 32) | epoch of a call whose wait ran out of time; else anything
@@ -229,7 +232,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
     if (l > 0) {   // x_l from the previous layer's down rows
         load_router(LY);   // rows warmed into this XCD's L2 by the previous layer: they land during the wait
         __syncthreads();   // the previous combine has read xs
-        wait_words<(64 * 64 + kNT1 - 1) / kNT1>(a.xb, n, tag, deadline, &a.sync->err, err_val,
+        wait_words<(64 * 64 + kNT1 - 1) / kNT1, kXbStride>(a.xb, n, tag, deadline, &a.sync->err, err_val,
                                                 [&](int i, uint32_t p) { xs[(i / L) * (L + 1) + i % L] = __uint_as_float(p); });
         __syncthreads();
     }
@@ -436,9 +439,9 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
             const int l4 = (4 * lane) & 63;
             const uint32_t word = uint32_t(__shfl(c, l4)) | (uint32_t(__shfl(c, l4 + 1)) << 8) |
                                   (uint32_t(__shfl(c, l4 + 2)) << 16) | (uint32_t(__shfl(c, l4 + 3)) << 24);
-            uint64_t* dst = a.hb + size_t(q) * 9;
-            if (lane < 8) pub(dst + lane, tag, word);
-            if (lane == 8) pub(dst + 8, tag, __float_as_uint(f16_round(d)));
+            uint64_t* dst = a.hb + size_t(q) * 9 * kHbStride;
+            if (lane < 8) pub(dst + lane * kHbStride, tag, word);
+            if (lane == 8) pub(dst + 8 * kHbStride, tag, __float_as_uint(f16_round(d)));
         }
     };
 
@@ -493,7 +496,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
 #pragma unroll
         for (int i = 0; i < L / 4; ++i) nv[i] = w4[i];
     }
-    wait_words<kMaxHWords / kNT1>(a.hb, NU * 9, tag, deadline, &a.sync->err, err_val, [&](int i, uint32_t p) {
+    wait_words<kMaxHWords / kNT1, kHbStride>(a.hb, NU * 9, tag, deadline, &a.sync->err, err_val, [&](int i, uint32_t p) {
         const int q = i / 9, part = i % 9, u = q / RB, rb = q % RB;
         if (part < 8) *reinterpret_cast<uint32_t*>(sh_q + size_t(u) * ff + rb * 32 + 4 * part) = p;
         else sh_d[u * (ff / kQ8) + rb] = __uint_as_float(p);
@@ -514,7 +517,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
             const int row = g0 + tid;
             if (stack) o = xs[(row / L) * (L + 1) + row % L] + o;
             else if (a.resid) o = rv + o;
-            if (l + 1 < n_layer) pub(a.xb + row, tag_next, __float_as_uint(o));
+            if (l + 1 < n_layer) pub(a.xb + size_t(row) * kXbStride, tag_next, __float_as_uint(o));
             else a.out[row] = o;
         }
     };
@@ -560,9 +563,9 @@ __global__ void k_dec1_zero(uint64_t* p, size_t words) {
 // The sync region at the front of every layer workspace: the error word and the epoch cells, then
 // the tagged words (sized for the largest eligible call: E <= 1024, 4096 h words).
 constexpr size_t kDec1Head = (sizeof(Dec1Sync) + 255) / 256 * 256;
-constexpr size_t kDec1Lg = size_t(1024 + 1 + 31) / 32 * 32 * 8 * kLgStride;
-constexpr size_t kDec1Hb = size_t(kMaxHWords) * 8;
-constexpr size_t kDec1Xb = size_t(64 * 64) * 8;   // a stack's next-layer input, n <= 4096
+constexpr size_t kDec1Lg = size_t(1024 + 1 + 31) / 32 * 32 * 8 * 16;   // room for any logit stride up to 16
+constexpr size_t kDec1Hb = size_t(kMaxHWords) * 8 * kHbStride;
+constexpr size_t kDec1Xb = size_t(64 * 64) * 8 * kXbStride;   // a stack's next-layer input, n <= 4096
 size_t dec1_sync_bytes() { return kDec1Head + kDec1Lg + kDec1Hb + kDec1Xb; }
 
 int dec1_eligible(int E, int K, int n, int ff) {

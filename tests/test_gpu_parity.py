@@ -712,8 +712,8 @@ def test_decode_fused_router_logits_bit_exact(F):
     out = torch.empty((1, H.N), dtype=torch.float32, device="cuda")
     w.layer_obj.forward(xd, out, T=1, ws=ws)
     torch.cuda.synchronize()
-    # the logit words follow the 4352-byte header, one per 128-byte line
-    words = ws[4352:4352 + 128 * (H.E + 1)].cpu().numpy().view(np.uint64)[::16]
+    # the logit words follow the 4352-byte header, one every 4 words (32 bytes)
+    words = ws[4352:4352 + 32 * (H.E + 1)].cpu().numpy().view(np.uint64)[::4]
     got = (words & np.uint64(0xFFFFFFFF)).astype(np.uint32).view(np.float32)
     u = O.rmsnorm(x)
     ref = O.router_logits(u, w.router_h, bias)[0]
