@@ -39,6 +39,8 @@ SIGNATURES = {
     "frt_moe_layer_workspace_bytes": (_sz, [_vp, _i]),
     "frt_moe_layer_forward": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "frt_set_option": (_i, [C.c_char_p, C.c_int64]),
+    "frt_noalloc_scratch_bytes": (_sz, []),
+    "frt_moe_layer_forward_noalloc": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "frt_moe_stack_workspace_bytes": (_sz, [_vp, _i]),
     "frt_moe_stack_forward": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "frt_moe_layer_sync_error": (_i, [_vp, _vp]),

@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -172,6 +173,32 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
     w.bytes = size_t(p - static_cast<uint8_t*>(base));
     (void)total;
     return w;
+}
+
+// ---- the allocation-free decode entry point's workspace: a file-scope device array, one copy per
+// GPU, held until the process ends. Host code never passes the array's name to a kernel or a copy:
+// it uses the device address hipGetSymbolAddress returns, looked up once per device.
+constexpr size_t kNoAllocScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+static int scratch_ptr(void** out) {
+    int dev = 0;
+    FRT_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(kErrShape, "noalloc scratch: device %d", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {   // once per device, with that device current
+        void* p = nullptr;
+        FRT_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return set_error(kErrHip, "noalloc scratch: no device address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return kOk;
 }
 
 }  // namespace frt
@@ -369,6 +396,23 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     timing_mark(s, "route_topk");
     return pf_moe(L->experts, L->stride, E, L->shared, n, ff, xin, ids_o, wts_o, w.gate, T, K, resid, out, w.rest,
                   w.rest_bytes, s);
+}
+
+size_t frt_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+int frt_moe_layer_forward_noalloc(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out,
+                                  int32_t* ids, float* wts, uint32_t* counts, void* stream) {
+    if (!L) return set_error(kErrNull, "moe_layer_forward_noalloc: null layer");
+    if (T < 1 || T > kDecodeMaxT || T * L->top_k > 63)
+        return set_error(kErrShape, "moe_layer_forward_noalloc: decode windows only (1 <= T <= %d, T * K <= 63), "
+                                    "got T=%d K=%d", kDecodeMaxT, T, L->top_k);
+    const size_t need = frt_moe_layer_workspace_bytes(L, T);
+    if (need == 0 || need > kNoAllocScratchBytes)
+        return set_error(kErrWorkspace, "moe_layer_forward_noalloc: needs %zu bytes of workspace; the static "
+                                        "scratch holds %zu", need, kNoAllocScratchBytes);
+    void* p = nullptr;
+    if (int rc = scratch_ptr(&p)) return rc;
+    return frt_moe_layer_forward(L, x, T, resid, out, ids, wts, counts, p, kNoAllocScratchBytes, stream);
 }
 
 size_t frt_moe_stack_workspace_bytes(const frt_moe_layer* layers, int n_layer) {

@@ -23,7 +23,7 @@ from ._lib import LAYER_NORM_INPUT, FrtArena, FrtError, FrtMoeLayer, check, lib
 
 __all__ = ["FrtError", "ExpertArena", "arena_alloc", "arena_free", "moe_route_topk", "router_logits", "quantize_q8",
            "moe_dispatch", "moe_q2", "moe_hits_scratch_bytes", "moe_hits", "MoeLayer", "expert_bytes", "gen",
-           "set_option", "layer_sync_error", "MoeStack"]
+           "set_option", "layer_sync_error", "MoeStack", "noalloc_scratch_bytes"]
 
 
 def _p(t) -> int | None:
@@ -195,6 +195,13 @@ class MoeLayer:
         check(lib().frt_moe_layer_forward(C.byref(self.raw), _p(x), T, _p(resid), _p(out), _p(ids), _p(wts),
                                           _p(counts), _p(ws), ws.numel(), _s(stream)))
 
+    def forward_noalloc(self, x, out, T: int | None = None, resid=None, ids=None, wts=None, counts=None,
+                        stream=None) -> None:
+        """frt_moe_layer_forward_noalloc: a decode window (T <= 4) with the library's static scratch."""
+        T = x.shape[0] if T is None else T
+        check(lib().frt_moe_layer_forward_noalloc(C.byref(self.raw), _p(x), T, _p(resid), _p(out), _p(ids), _p(wts),
+                                                  _p(counts), _s(stream)))
+
 
 class MoeStack:
     """A stack of single-token MoE layers run as one call (frt_moe_stack_forward):
@@ -237,6 +244,10 @@ def layer_sync_error(ws, stream=None) -> bool:
     if rc < 0:
         check(rc)
     return rc == 1
+
+
+def noalloc_scratch_bytes() -> int:
+    return int(lib().frt_noalloc_scratch_bytes())
 
 
 # ---------------------------------------------------------------- synthetic inputs

@@ -153,6 +153,17 @@ int frt_set_option(const char* name, int64_t value);
  * check, 0 if not, negative on a HIP error. No reference counterpart. */
 int frt_moe_layer_sync_error(void* ws, void* stream);
 
+/* ---- allocation-free decode: frt_moe_layer_forward for decode windows (1 <= T <= 4, T * K <= 63)
+ * with the workspace taken from a static device array of frt_noalloc_scratch_bytes() (1 MiB) per
+ * GPU, held until the process ends. No reference counterpart: for callers that cannot allocate
+ * device memory or pass a workspace (code under graph capture, tight serving loops, harnesses that
+ * forbid allocation). The call itself allocates nothing. All calls on one GPU share that GPU's
+ * array: calls that overlap on one GPU (other streams, other host threads) race. Larger T, or a
+ * shape whose workspace exceeds the array, is refused (FRT_ERR_SHAPE / FRT_ERR_WORKSPACE). */
+size_t frt_noalloc_scratch_bytes(void);
+int frt_moe_layer_forward_noalloc(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out,
+                                  int32_t* ids, float* wts, uint32_t* counts, void* stream);
+
 /* ---- a stack of single-token MoE layers (no reference counterpart as one call: the engine calls
  * moe_block_fast once per layer, arch/qwen4exp/forward.cu:214-217; BASELINE config 2 is a stack of
  * MoE layers chained by the residual). x_0 = x, x_{l+1} = x_l + moe_l(x_l) with each layer's own
