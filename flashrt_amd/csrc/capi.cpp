@@ -317,7 +317,7 @@ int frt_moe_dispatch(void* stream, const int32_t* ids, int T, int K, int E, int3
 }
 
 size_t frt_moe_q2_workspace_bytes(int T, int K, int n, int ff, int E) {
-    return pf_workspace_bytes(T, K, n, ff, E, false, true);   // room for the fp32 outputs of yd_bf16
+    return pf_workspace_bytes(T, K, n, ff, E, false, false);
 }
 int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const float* x, const int32_t* ids,
                    int T, int K, void* yd, void* ws, size_t ws_bytes, void* stream, int block64, int yd_bf16) {

@@ -619,12 +619,26 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
 // row block; a weight block past the row's last (the pad) is read as the row's last block, whose
 // finite products with the pad's zeros are 0. TAIL: the stretch count is not a multiple of 4, and
 // the last round of 4 steps has steps past the end (loads repeated, no products).
-template <int NQ, bool TAIL>
+// 4 consecutive per-slot outputs as float, fp16 or bf16 (round to nearest even)
+__device__ __forceinline__ void store4(float* p, floatx4 v) { *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]); }
+__device__ __forceinline__ void store4(_Float16* p, floatx4 v) {
+    typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+    const half4v h = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
+    *reinterpret_cast<half4v*>(p) = h;
+}
+__device__ __forceinline__ void store4(__hip_bfloat16* p, floatx4 v) {
+    p[0] = __float2bfloat16(v[0]);
+    p[1] = __float2bfloat16(v[1]);
+    p[2] = __float2bfloat16(v[2]);
+    p[3] = __float2bfloat16(v[3]);
+}
+
+template <int NQ, bool TAIL, typename OutT>
 __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ arena, size_t stride, int E,
                                                  const uint8_t* __restrict__ shared_blob, int n, int ff,
                                                  const _Float16* __restrict__ h, const int32_t* __restrict__ bounds,
                                                  const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-                                                 float* __restrict__ yd, const int32_t* __restrict__ slot_of) {
+                                                 OutT* __restrict__ yd, const int32_t* __restrict__ slot_of) {
     constexpr int ffp = NQ * 256;      // h row length
     const int nbk = ff / kBlock;       // weight blocks per row
     constexpr int cpt = ffp / 8;       // 16-byte activation chunks per token
@@ -717,8 +731,7 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int r = rb * 256 + 64 * wave + 16 * i + 4 * lg;
-                            *reinterpret_cast<float4*>(yd + yslot[c] + r) =
-                                make_float4(acc[i][c][0], acc[i][c][1], acc[i][c][2], acc[i][c][3]);
+                            store4(yd + yslot[c] + r, acc[i][c]);
                         }
                     }
 #pragma unroll
@@ -790,17 +803,6 @@ __global__ void __launch_bounds__(256) k_pf_combine(const InT* __restrict__ yd, 
     *reinterpret_cast<float4*>(out + size_t(t) * n + i) = make_float4(o[0], o[1], o[2], o[3]);
 }
 
-// fp32 -> bf16 (round to nearest even), 4 per thread (count % 4 == 0)
-__global__ void k_to_bf16(const float* __restrict__ src, __hip_bfloat16* __restrict__ dst, size_t count) {
-    const size_t i = (size_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
-    if (i >= count) return;
-    const float4 v = *reinterpret_cast<const float4*>(src + i);
-    dst[i] = __float2bfloat16(v.x);
-    dst[i + 1] = __float2bfloat16(v.y);
-    dst[i + 2] = __float2bfloat16(v.z);
-    dst[i + 3] = __float2bfloat16(v.w);
-}
-
 }  // namespace
 
 // ---------------------------------------------------------------- host side
@@ -810,7 +812,7 @@ struct PfWs {
     int2* tiles;
     _Float16 *xhi, *xlo;   // x = code * d as an exact fp16 pair, perm256 order [T][n]
     _Float16* h16;         // h = code * d as fp16, perm256 order [S][ffp], ffp = ff rounded up to 256
-    float* yd;   // fp32 per-slot outputs when the caller does not receive them as fp32
+    _Float16* yd;   // fp16 per-slot outputs of a whole layer (combined by k_pf_combine)
     size_t bytes;
 };
 
@@ -836,7 +838,7 @@ static PfWs pf_carve(void* base, int T, int K, int n, int ff, int E, bool shared
     w.xhi = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
     w.xlo = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
     w.h16 = reinterpret_cast<_Float16*>(take(size_t(S) * ((ff + 255) & ~255) * 2));
-    w.yd = own_yd ? reinterpret_cast<float*>(take(size_t(S) * n * 4)) : nullptr;
+    w.yd = own_yd ? reinterpret_cast<_Float16*>(take(size_t(S) * n * 2)) : nullptr;
     w.bytes = size_t(p - static_cast<uint8_t*>(base));
     return w;
 }
@@ -869,11 +871,11 @@ static int pf_gemm_attr() {
     return kOk;
 }
 
-template <int NQ, bool TAIL>
+template <int NQ, bool TAIL, typename OutT>
 static int pf_down_attr(size_t lds) {
     static bool done = false;
     if (!done) {
-        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_down<NQ, TAIL>),
+        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_down<NQ, TAIL, OutT>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
         done = true;
     }
@@ -881,9 +883,10 @@ static int pf_down_attr(size_t lds) {
 }
 
 // The two grouped GEMMs: gate/up (k_pf_gemm) on the exact x pairs, SwiGLU and Q8_0 of h in the
-// epilogue; down (k_pf_down) on h -> fp32 yd per slot.
+// epilogue; down (k_pf_down) on h -> yd per slot as OutT.
+template <typename OutT>
 static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, int n, int ff,
-                           const PfWs& w, int mt, float* ydf, hipStream_t stream) {
+                           const PfWs& w, int mt, OutT* ydf, hipStream_t stream) {
     if (int rc = pf_gemm_attr<false>()) return rc;
     if (int rc = pf_gemm_attr<true>()) return rc;
     // tiles of 2-4 token columns, then those of one (the tile list is ordered longest first)
@@ -902,8 +905,8 @@ static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uin
     const bool tail = (n / 256) * nq % 4 != 0;
 #define FRT_PF_DOWN(NQV, TL)                                                                                 \
     if (nq == NQV && tail == TL) {                                                                           \
-        if (int rc = pf_down_attr<NQV, TL>(down_lds)) return rc;                                             \
-        launch_timed("pf_down", k_pf_down<NQV, TL>, dim3(1, mt), dim3(256), down_lds, stream, arena, stride, E, \
+        if (int rc = pf_down_attr<NQV, TL, OutT>(down_lds)) return rc;                                       \
+        launch_timed("pf_down", k_pf_down<NQV, TL, OutT>, dim3(1, mt), dim3(256), down_lds, stream, arena, stride, E, \
                      shared_blob, n, ff, (const _Float16*)w.h16, (const int32_t*)w.bounds, (const int2*)w.tiles, \
                      (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of);                             \
     }
@@ -914,7 +917,7 @@ static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uin
 }
 
 // The grouped expert products for routed ids (+ optionally the shared expert as group E).
-// yd_kind: 0 float, 1 bf16 (moe_q2::run's yd_bf16)
+// yd_kind: 0 float, 1 bf16 (moe_q2::run's yd_bf16), 2 fp16 (a whole layer's, combined here)
 static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, int n, int ff,
                       const float* x, const int32_t* ids, int T, int K, void* yd, int yd_kind, const PfWs& w,
                       hipStream_t stream) {
@@ -933,12 +936,11 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
                  ids, T * K, K, E, id_bits, w.cnt, w.tok_of, w.slot_of, shared ? T : 0);
     timing_mark(stream, "pf_dispatch");
     const int mt = pf_max_tiles(S, G);
-    float* ydf = yd_kind == 1 ? w.yd : static_cast<float*>(yd);
-    if (int rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, w, mt, ydf, stream)) return rc;
-    if (yd_kind == 1) {
-        const size_t cntv = size_t(S) * n;
-        k_to_bf16<<<unsigned((cntv / 4 + 255) / 256), 256, 0, stream>>>(ydf, static_cast<__hip_bfloat16*>(yd), cntv);
-    }
+    int rc = kOk;
+    if (yd_kind == 1) rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, w, mt, static_cast<__hip_bfloat16*>(yd), stream);
+    else if (yd_kind == 2) rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, w, mt, static_cast<_Float16*>(yd), stream);
+    else rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, w, mt, static_cast<float*>(yd), stream);
+    if (rc) return rc;
     timing_mark(stream, "pf_down");
     FRT_LAUNCHED("prefill experts");
     return kOk;
@@ -950,7 +952,7 @@ int pf_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const fl
     if (int rc = pf_check(T, K, n, ff, E)) return rc;
     if (block64) return set_error(kErrShape, "moe_q2::run: block64 activations are not supported (Q8_0 blocks of 32 only)");
     if (!experts || !x || !ids || !yd || !ws) return set_error(kErrNull, "moe_q2::run: null pointer");
-    const PfWs w = pf_carve(ws, T, K, n, ff, E, false, yd_bf16 != 0);
+    const PfWs w = pf_carve(ws, T, K, n, ff, E, false, false);
     if (w.bytes > ws_bytes) return set_error(kErrWorkspace, "moe_q2::run: workspace %zu < %zu", ws_bytes, w.bytes);
     return pf_experts(experts, stride, E, nullptr, n, ff, x, ids, T, K, yd, yd_bf16 ? 1 : 0, w, stream);
 }
@@ -962,9 +964,9 @@ int pf_moe(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blo
     if (int rc = pf_check(T, K, n, ff, E)) return rc;
     const PfWs w = pf_carve(ws, T, K, n, ff, E, true, true);
     if (w.bytes > ws_bytes) return set_error(kErrWorkspace, "prefill: workspace %zu < %zu", ws_bytes, w.bytes);
-    if (int rc = pf_experts(arena, stride, E, shared_blob, n, ff, x, ids, T, K, w.yd, 0, w, stream)) return rc;
-    launch_timed("pf_combine", k_pf_combine<float>, dim3((n + 1023) / 1024, T), dim3(256), 0, stream,
-                 (const float*)w.yd, ids, wts, gate, T, K, n, 1, resid, out);
+    if (int rc = pf_experts(arena, stride, E, shared_blob, n, ff, x, ids, T, K, w.yd, 2, w, stream)) return rc;
+    launch_timed("pf_combine", k_pf_combine<_Float16>, dim3((n + 1023) / 1024, T), dim3(256), 0, stream,
+                 (const _Float16*)w.yd, ids, wts, gate, T, K, n, 1, resid, out);
     timing_mark(stream, "pf_combine");
     FRT_LAUNCHED("prefill combine");
     return kOk;
