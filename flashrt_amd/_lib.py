@@ -39,6 +39,10 @@ SIGNATURES = {
     "frt_moe_layer_workspace_bytes": (_sz, [_vp, _i]),
     "frt_moe_layer_forward": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "frt_set_option": (_i, [C.c_char_p, C.c_int64]),
+    "frt_q2_repack": (_sz, [_vp, _i, _i, _vp]),
+    "frt_q2_repack_expert": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "frt_load_experts": (_i, [_vp, _i, _vp, _i, _i, _vp, _i, _vp]),
+    "frt_moe_layer_forward_ex": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _sz, _vp]),
     "frt_noalloc_scratch_bytes": (_sz, []),
     "frt_moe_layer_forward_noalloc": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "frt_moe_stack_workspace_bytes": (_sz, [_vp, _i]),
@@ -72,6 +76,14 @@ class FrtMoeLayer(C.Structure):
                 ("router_w", C.c_void_p), ("router_bias", C.c_void_p), ("gate_w", C.c_void_p),
                 ("d_model", C.c_int), ("d_ff", C.c_int), ("top_k", C.c_int), ("flags", C.c_int),
                 ("next_router_w", C.c_void_p)]
+
+
+class FrtExpertSlab(C.Structure):
+    _fields_ = [("shard", C.c_int), ("file_offset", C.c_uint64)]
+
+
+class FrtLoadStats(C.Structure):
+    _fields_ = [("seconds", C.c_double), ("bytes_read", C.c_uint64)]
 
 
 _lib = None

@@ -91,6 +91,10 @@ int dec1_layer(const float* x, const float* W, const float* bias, const float* g
                hipStream_t stream);
 int dec1_status(void* sync_ws, hipStream_t stream, uint32_t* err);
 int dec1_support(int E, int K, int n, int ff);
+const float* dec1_logits(const void* sync_ws, int* stride_floats);
+// route.hip
+int layer_trace(const float* lg, int ls, const int32_t* ids, int T, int E, int K, uint32_t* tail_counts, int tail_from,
+                float* probs, hipStream_t stream);
 int dec1_stack(const frt_moe_layer* L, int n_layer, const float* x, float* out, int32_t* ids, float* wts,
                void* sync_ws, hipStream_t stream);
 extern int g_dec1_on;
@@ -489,6 +493,19 @@ int frt_moe_layer_sync_error(void* ws, void* stream) {
     uint32_t err = 0;
     if (int rc = dec1_status(ws, static_cast<hipStream_t>(stream), &err)) return rc;
     return err ? 1 : 0;
+}
+
+int frt_moe_layer_forward_ex(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out,
+                             int32_t* ids, float* wts, uint32_t* counts, uint32_t* tail_counts, int tail_from,
+                             float* probs, void* ws, size_t ws_bytes, void* stream) {
+    if (int rc = frt_moe_layer_forward(L, x, T, resid, out, ids, wts, counts, ws, ws_bytes, stream)) return rc;
+    if (!tail_counts && !probs) return kOk;
+    const int E = L->n_expert, K = L->top_k, n = L->d_model, ff = L->d_ff;
+    const LayerWs w = layer_carve(ws, *L, T, ws_bytes);
+    const float* lg = w.logits;
+    int ls = 1;
+    if (T == 1 && g_dec1_on && dec1_support(E, K, n, ff) >= 1) lg = dec1_logits(w.sync, &ls);   // the persistent call's
+    return layer_trace(lg, ls, ids ? ids : w.ids, T, E, K, tail_counts, tail_from, probs, static_cast<hipStream_t>(stream));
 }
 
 int frt_gen_experts(uint64_t seed, int cfg, int layer, int e0, int count, int tensor_base, int n, int ff, float sd,

@@ -42,6 +42,7 @@ enum Status : int {
     kErrWorkspace = -2,   // workspace / scratch too small
     kErrHip = -3,         // a HIP call failed
     kErrNull = -4,        // required pointer missing
+    kErrIo = -5,          // a file could not be read
 };
 
 // Records the message of the last failure (thread-local) and returns code.

@@ -715,6 +715,13 @@ int dec1_stack(const frt_moe_layer* L, int n_layer, const float* x, float* out, 
                        L[n_layer - 1].next_router_w, stream);
 }
 
+// The last single-token call's logits in a sync region: logit e at the returned pointer + e * stride
+// (the payload half of each tagged word).
+const float* dec1_logits(const void* sync_ws, int* stride_floats) {
+    *stride_floats = 2 * kLgStride;
+    return reinterpret_cast<const float*>(static_cast<const uint8_t*>(sync_ws) + kDec1Head);
+}
+
 // Whether the persistent kernels can run this shape: 2 = the stack kernel too, 1 = single layers only, 0 = none.
 int dec1_support(int E, int K, int n, int ff) {
     if (!dec1_eligible(E, K, n, ff)) return 0;

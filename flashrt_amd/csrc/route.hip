@@ -231,6 +231,28 @@ __global__ void __launch_bounds__(256) k_route_topk(const float* __restrict__ lo
     }
 }
 
+// ---- the routing records of a layer call from its logits (logit e of token t at
+// lg[(t * E + e) * ls]): probs [T][K] = exp(l - max) / sum_e exp(l_e - max) with the sum in double
+// (moe_ref.cu:146-164), tail_counts += 1 per selection of tokens t >= tail_from. One wave per token.
+__global__ void __launch_bounds__(64) k_layer_trace(const float* __restrict__ lg, int ls, const int32_t* __restrict__ ids,
+                                                    int T, int E, int K, uint32_t* __restrict__ tail_counts, int tail_from,
+                                                    float* __restrict__ probs) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    if (t >= T) return;
+    const float* l = lg + size_t(t) * E * ls;
+    float mx = -INFINITY;
+    for (int e = lane; e < E; e += 64) mx = fmaxf(mx, l[size_t(e) * ls]);
+    mx = wave_max(mx);
+    double s = 0.0;
+    for (int e = lane; e < E; e += 64) s += double(expf(l[size_t(e) * ls] - mx));
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if (lane < K) {
+        const int id = ids[t * K + lane];
+        if (probs) probs[t * K + lane] = float(double(expf(l[size_t(id) * ls] - mx)) / s);
+        if (tail_counts && t >= tail_from) atomicAdd(tail_counts + id, 1u);
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- host entry points
@@ -471,6 +493,14 @@ int router_gemm(const float* x, int T, const float* W, const float* bias, const 
     const size_t N = size_t(T) * E1;
     k_router_combine<<<unsigned((N + 255) / 256), 256, 0, stream>>>(part, T, E, E1, bias, logits, gate);
     FRT_LAUNCHED("router_combine");
+    return kOk;
+}
+
+int layer_trace(const float* lg, int ls, const int32_t* ids, int T, int E, int K, uint32_t* tail_counts, int tail_from,
+                float* probs, hipStream_t stream) {
+    if (T < 1) return kOk;
+    k_layer_trace<<<T, 64, 0, stream>>>(lg, ls, ids, T, E, K, tail_counts, tail_from, probs);
+    FRT_LAUNCHED("layer trace");
     return kOk;
 }
 

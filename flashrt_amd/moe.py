@@ -19,11 +19,12 @@ from types import SimpleNamespace
 
 import torch
 
-from ._lib import LAYER_NORM_INPUT, FrtArena, FrtError, FrtMoeLayer, check, lib
+from ._lib import LAYER_NORM_INPUT, FrtArena, FrtError, FrtExpertSlab, FrtLoadStats, FrtMoeLayer, check, lib
 
 __all__ = ["FrtError", "ExpertArena", "arena_alloc", "arena_free", "moe_route_topk", "router_logits", "quantize_q8",
            "moe_dispatch", "moe_q2", "moe_hits_scratch_bytes", "moe_hits", "MoeLayer", "expert_bytes", "gen",
-           "set_option", "layer_sync_error", "MoeStack", "noalloc_scratch_bytes"]
+           "set_option", "layer_sync_error", "MoeStack", "noalloc_scratch_bytes", "q2_repack",
+           "q2_repack_expert", "load_experts"]
 
 
 def _p(t) -> int | None:
@@ -189,11 +190,16 @@ class MoeLayer:
         return self._ws
 
     def forward(self, x, out, T: int | None = None, resid=None, ids=None, wts=None, counts=None, ws=None,
-                stream=None) -> None:
+                stream=None, tail_counts=None, tail_from: int = 1 << 30, probs=None) -> None:
         T = x.shape[0] if T is None else T
         ws = self.workspace(T) if ws is None else ws
-        check(lib().frt_moe_layer_forward(C.byref(self.raw), _p(x), T, _p(resid), _p(out), _p(ids), _p(wts),
-                                          _p(counts), _p(ws), ws.numel(), _s(stream)))
+        if tail_counts is None and probs is None:
+            check(lib().frt_moe_layer_forward(C.byref(self.raw), _p(x), T, _p(resid), _p(out), _p(ids), _p(wts),
+                                              _p(counts), _p(ws), ws.numel(), _s(stream)))
+        else:
+            check(lib().frt_moe_layer_forward_ex(C.byref(self.raw), _p(x), T, _p(resid), _p(out), _p(ids), _p(wts),
+                                                 _p(counts), _p(tail_counts), tail_from, _p(probs), _p(ws),
+                                                 ws.numel(), _s(stream)))
 
     def forward_noalloc(self, x, out, T: int | None = None, resid=None, ids=None, wts=None, counts=None,
                         stream=None) -> None:
@@ -244,6 +250,37 @@ def layer_sync_error(ws, stream=None) -> bool:
     if rc < 0:
         check(rc)
     return rc == 1
+
+
+def q2_repack(ggml_rows, rows: int, cols: int):
+    """Planar repack of ggml Q2_0 blocks (host bytes; quant/q2_0/q2_0.cpp:21-62): returns a uint8 array."""
+    import numpy as np
+    src = np.ascontiguousarray(ggml_rows, dtype=np.uint8)
+    out = np.zeros(rows * (cols // 64) * 18, np.uint8)
+    nb = lib().frt_q2_repack(src.ctypes.data, rows, cols, out.ctypes.data)
+    if nb == 0:
+        raise FrtError(-1, lib().frt_last_error().decode())
+    return out
+
+
+def q2_repack_expert(gate, up, down, d_model: int, d_ff: int):
+    import numpy as np
+    g, u, d = (np.ascontiguousarray(a, dtype=np.uint8) for a in (gate, up, down))
+    out = np.zeros(expert_bytes(d_model, d_ff), np.uint8)
+    check(lib().frt_q2_repack_expert(g.ctypes.data, u.ctypes.data, d.ctypes.data, d_model, d_ff, out.ctypes.data))
+    return out
+
+
+def load_experts(shards: list[str], slabs: list[tuple[int, int]], d_model: int, d_ff: int, arena: ExpertArena,
+                 threads: int = 4) -> tuple[float, int]:
+    """frt_load_experts: slabs [n_layer * 3] of (shard, file offset) for gate, up, down of each layer.
+    Returns (seconds, bytes read)."""
+    paths = (C.c_char_p * len(shards))(*[s.encode() for s in shards])
+    sl = (FrtExpertSlab * len(slabs))(*[FrtExpertSlab(int(a), int(b)) for a, b in slabs])
+    st = FrtLoadStats()
+    check(lib().frt_load_experts(C.cast(paths, C.c_void_p), len(shards), C.cast(sl, C.c_void_p), d_model, d_ff,
+                                 C.byref(arena._raw), threads, C.byref(st)))
+    return st.seconds, int(st.bytes_read)
 
 
 def noalloc_scratch_bytes() -> int:

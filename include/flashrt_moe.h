@@ -28,6 +28,7 @@ extern "C" {
 #define FRT_ERR_WORKSPACE -2  /* workspace or scratch too small */
 #define FRT_ERR_HIP -3        /* a HIP call failed */
 #define FRT_ERR_NULL -4       /* a required pointer is missing */
+#define FRT_ERR_IO -5         /* a file could not be opened or read */
 
 /* Message of the last failure on this thread (static storage; "" when none). */
 const char* frt_last_error(void);
@@ -61,6 +62,29 @@ int frt_arena_alloc(int n_layer, int n_expert, size_t blob_bytes, frt_arena* out
 int frt_arena_free(frt_arena* a);
 uint8_t* frt_arena_blob(const frt_arena* a, int layer, int expert);
 size_t frt_arena_total_bytes(const frt_arena* a);
+/* ---- Q2_0 repack, ggml block order -> planar (quant/q2_0/q2_0.cpp:21-62 repack, :64-80 repack_expert),
+ * host memory. A ggml block is {fp16 d; u8 qs[16]}, element j at byte j/4, bits 2(j%4). frt_q2_repack
+ * writes mat_bytes(rows, cols) bytes and returns that count (0 on a bad shape: cols a multiple of 64). */
+size_t frt_q2_repack(const void* ggml_rows, int rows, int cols, void* dst);
+int frt_q2_repack_expert(const void* gate, const void* up, const void* down, int d_model, int d_ff, void* blob);
+
+/* ---- expert loader (arch/qwen4exp/experts.cpp:65-131 load_experts): the three expert slabs of every
+ * layer (ffn_gate_exps, ffn_up_exps, ffn_down_exps: n_expert consecutive ggml-layout Q2_0 matrices,
+ * gate/up [d_ff][d_model], down [d_model][d_ff]) read with O_DIRECT from GGUF shard files, repacked
+ * and uploaded into the HBM arena (one copy per 32 experts). slabs [n_layer][3] give each slab's
+ * shard and absolute file offset (GgufTensor::shard / file_offset). Synchronous; FRT_ERR_IO on a
+ * failed open or read. */
+typedef struct frt_expert_slab {
+    int shard;
+    uint64_t file_offset;
+} frt_expert_slab;
+typedef struct frt_load_stats {
+    double seconds;
+    uint64_t bytes_read;
+} frt_load_stats;
+int frt_load_experts(const char* const* shards, int n_shards, const frt_expert_slab* slabs, int d_model, int d_ff,
+                     const frt_arena* arena, int threads, frt_load_stats* stats);
+
 /* Copies one repacked blob from host memory into (layer, expert) (the per-expert step of
  * arch/qwen4exp/experts.cpp:93-116 load_experts, minus the file read). */
 int frt_arena_upload(const frt_arena* a, int layer, int expert, const void* host_blob, void* stream);
@@ -131,6 +155,13 @@ typedef struct frt_moe_layer {
      * No reference counterpart (the reference's router is a ggml linear, blocks.hpp:85). */
     const float* next_router_w;
 } frt_moe_layer;
+/* frt_moe_layer_forward with the routing records of moe_route_topk and MoeTrace (blocks.hpp:130-135,
+ * :267-286): tail_counts [E] (optional) += 1 per selection of tokens t >= tail_from; probs [T][K]
+ * (optional) = each selection's probability before renormalisation, exp(l - max) / sum_e exp(l_e - max)
+ * (the sum in double, as moe_block). */
+int frt_moe_layer_forward_ex(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out,
+                             int32_t* ids, float* wts, uint32_t* counts, uint32_t* tail_counts, int tail_from,
+                             float* probs, void* ws, size_t ws_bytes, void* stream);
 /* The workspace's first bytes hold the single-token path's synchronisation words: they are zeroed by
  * the first call that sees the workspace and must not be written by the caller between calls. */
 size_t frt_moe_layer_workspace_bytes(const frt_moe_layer* L, int T);

@@ -53,6 +53,35 @@ def test_argument_errors_before_device_work():
         _lib.check(L.frt_moe_q2_run(None, 0, 512, 2048, 512, None, None, 16, 10, None, None, 0, None, 1, 0))
 
 
+def test_q2_repack_matches_reference_fixture():
+    """The product's host repack (frt_q2_repack) reproduces the reference's compiled repack on the
+    golden blocks bit for bit (tests/golden/q2_format.npz, 8 rows x 4096), and repack_expert places
+    gate | up | down back to back (quant/q2_0/q2_0.cpp:64-80); bad shapes are refused."""
+    import numpy as np
+    import flashrt_amd as F
+    g = np.load(os.path.join(ROOT, "tests", "golden", "q2_format.npz"))
+    assert np.array_equal(F.q2_repack(g["repack_in"], 8, 4096), g["repack_out"])
+    rng = np.random.default_rng(1)
+    n, ff = 256, 128
+    mats = [rng.integers(0, 256, r * (c // 64) * 18, dtype=np.uint8) for r, c in ((ff, n), (ff, n), (n, ff))]
+    blob = F.q2_repack_expert(*mats, n, ff)
+    want = np.concatenate([F.q2_repack(mats[0], ff, n), F.q2_repack(mats[1], ff, n), F.q2_repack(mats[2], n, ff)])
+    assert np.array_equal(blob, want)
+    with pytest.raises(F.FrtError):
+        F.q2_repack(mats[0], ff, 100)
+
+
+def test_load_experts_reports_io_errors():
+    """A missing shard file is an FRT_ERR_IO error with its path in the message (checked before any
+    device work)."""
+    import flashrt_amd as F
+    arena = F._lib.FrtArena(C.c_void_p(1), F.expert_bytes(1024, 256), 0, 1, 1)
+    a = F.ExpertArena(arena)
+    with pytest.raises(F.FrtError) as e:
+        F.load_experts(["/nonexistent/model.gguf"], [(0, 0)] * 3, 1024, 256, a, threads=1)
+    assert e.value.code == -5 and "/nonexistent/model.gguf" in str(e.value)
+
+
 def test_product_does_not_use_the_oracle():
     """The product package never imports or loads anything under oracle/."""
     pkg = os.path.join(ROOT, "flashrt_amd")

@@ -810,3 +810,102 @@ def test_decode_stack_call_matches_layer_calls(F, nl):
             st.forward(x0, out, ws=ws, stream=s)   # eager work between the replays
         s.synchronize()
     assert not F.layer_sync_error(ws)
+
+
+# ---------------------------------------------------------------- loader, routing records
+
+def test_load_experts_into_arena_and_layer(F, tmp_path):
+    """frt_load_experts: ggml-layout Q2_0 slabs of a 2-layer, 12-expert model (d_model 1024, ff 256)
+    written to a file at GGUF-like 4 KiB-aligned offsets, read into the HBM arena: every blob equals
+    the host repack of its bytes, and a layer over the loaded arena matches the oracle (ids bit-exact,
+    outputs within 2e-3). The reference model (FLASHRT_TEST_MODEL) is not in this image."""
+    rng = np.random.default_rng(9)
+    L_, E_, n, ff, K_ = 2, 12, 1024, 256, 4
+    shapes = ((ff, n), (ff, n), (n, ff))
+    path = str(tmp_path / "experts.gguf")
+    slabs, data, off = [], [], 4096
+    with open(path, "wb") as f:
+        f.write(b"\0" * 4096)
+        for l in range(L_):
+            for r, c in shapes:
+                nb = r * (c // 64) * E_
+                blocks = np.zeros((nb, 18), np.uint8)
+                blocks[:, 2:] = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+                blocks[:, :2] = (rng.uniform(0.005, 0.02, nb).astype(np.float16)).view(np.uint8).reshape(nb, 2)
+                raw = blocks.reshape(-1)
+                slabs.append((0, off))
+                data.append(raw)
+                f.write(raw.tobytes())
+                off += raw.size
+                pad = (-off) % 4096
+                f.write(b"\0" * pad)
+                off += pad
+    eb = F.expert_bytes(n, ff)
+    arena = F.arena_alloc(L_, E_, eb)
+    try:
+        secs, nread = F.load_experts([path], slabs, n, ff, arena, threads=3)
+        assert nread >= sum(d.size for d in data)
+        for l in range(L_):
+            for e in range(E_):
+                parts = [data[3 * l + k][e * r * (c // 64) * 18:(e + 1) * r * (c // 64) * 18]
+                         for k, (r, c) in enumerate(shapes)]
+                want = F.q2_repack_expert(*parts, n, ff)
+                got = torch.empty(eb, dtype=torch.uint8, device="cuda")
+                import ctypes as C
+                hip = C.CDLL("libamdhip64.so")
+                assert hip.hipMemcpy(C.c_void_p(got.data_ptr()), C.c_void_p(arena.blob(l, e)), C.c_size_t(eb), 3) == 0
+                assert np.array_equal(got.cpu().numpy(), want), (l, e)
+        # a layer over the loaded experts (layer 1; the shared expert is layer 0's expert 11)
+        arena_h = np.zeros(E_ * arena.stride, np.uint8)
+        for e in range(E_):
+            parts = [data[3 + k][e * r * (c // 64) * 18:(e + 1) * r * (c // 64) * 18] for k, (r, c) in enumerate(shapes)]
+            arena_h[e * arena.stride:e * arena.stride + eb] = F.q2_repack_expert(*parts, n, ff)
+        sh_parts = [data[k][11 * r * (c // 64) * 18:12 * r * (c // 64) * 18] for k, (r, c) in enumerate(shapes)]
+        shared_h = F.q2_repack_expert(*sh_parts, n, ff)
+        router = (rng.standard_normal((E_, n)) * 0.02).astype(np.float32)
+        gate = (rng.standard_normal(n) * 0.02).astype(np.float32)
+        rd, gd = dev(router), dev(gate)
+        ml = F.MoeLayer(arena.blob(1, 0), arena.stride, E_, arena.blob(0, 11), rd, gd, n, ff, K_)
+        for T in (1, 3, 40):
+            x = rng.standard_normal((T, n)).astype(np.float32)
+            out = torch.empty((T, n), dtype=torch.float32, device="cuda")
+            ids = torch.empty((T, K_), dtype=torch.int32, device="cuda")
+            wts = torch.empty((T, K_), dtype=torch.float32, device="cuda")
+            ml.forward(dev(x), out, T=T, ids=ids, wts=wts)
+            torch.cuda.synchronize()
+            ref, rid, rw, _ = O.moe_layer(arena_h, arena.stride, E_, shared_h, router, None, gate, n, ff, K_, x)
+            assert np.array_equal(ids.cpu().numpy(), rid), T
+            assert H.w_rel(wts.cpu().numpy(), rw) <= H.W_REL, T
+            assert H.out_rel(out.cpu().numpy(), ref) <= H.OUT_REL, T
+    finally:
+        F.arena_free(arena)
+
+
+@pytest.mark.parametrize("T", [1, 3, 300])
+def test_layer_routing_records(F, w0, T):
+    """frt_moe_layer_forward_ex: probs (before renormalisation) and tail_counts, as moe_block's
+    MoeTrace and moe_route_topk's tail_counts (blocks.hpp:130-135, :280-283), against the oracle's
+    softmax: probs within 1e-6 relative, their renormalisation the weights, tail counts exact."""
+    rng = np.random.default_rng(T)
+    x = rng.standard_normal((T, H.N)).astype(np.float32)
+    out = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    ids = torch.empty((T, H.K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, H.K), dtype=torch.float32, device="cuda")
+    probs = torch.empty((T, H.K), dtype=torch.float32, device="cuda")
+    counts = torch.zeros(H.E, dtype=torch.int32, device="cuda")
+    tail = torch.zeros(H.E, dtype=torch.int32, device="cuda")
+    tail_from = T // 2
+    w0.layer_obj.forward(dev(x), out, T=T, ids=ids, wts=wts, counts=counts, tail_counts=tail, tail_from=tail_from,
+                         probs=probs)
+    torch.cuda.synchronize()
+    lg = O.router_logits(x, w0.router_h, None).astype(np.float64)
+    p = np.exp(lg - lg.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    i = ids.cpu().numpy()
+    want = np.take_along_axis(p, i, axis=1)
+    got = probs.cpu().numpy()
+    assert float((np.abs(got - want) / want).max()) <= 1e-6
+    assert H.w_rel(wts.cpu().numpy(), (want / want.sum(axis=1, keepdims=True)).astype(np.float32)) <= 1e-5
+    tc = np.bincount(i[tail_from:].reshape(-1), minlength=H.E)
+    assert np.array_equal(tail.cpu().numpy(), tc)
+    assert np.array_equal(counts.cpu().numpy(), np.bincount(i.reshape(-1), minlength=H.E))
