@@ -162,28 +162,33 @@ def run_stack(args, F, torch):
 
 # ---------------------------------------------------------------- config 3: 2K prefill
 
-def run_prefill(args, F, torch):
-    from types import SimpleNamespace
-    T = 2048
+def build_layer(F, torch, cfg, bias_np=None):
+    """One layer of BASELINE configs[cfg]: its own arena (E experts), shared expert, router, gate."""
     eb = F.expert_bytes(N, FF)
     stride = (eb + 4095) // 4096 * 4096
     g = F.gen
     arena = torch.empty(E * stride, dtype=torch.uint8, device="cuda")
-    g.experts(arena, stride, 3, 0, 0, E, N, FF)
+    g.experts(arena, stride, cfg, 0, 0, E, N, FF)
     shared = torch.empty(eb, dtype=torch.uint8, device="cuda")
-    g.experts(shared, eb, 3, 0, 0, 1, N, FF, tensor_base=g.SHARED_TENSOR)
+    g.experts(shared, eb, cfg, 0, 0, 1, N, FF, tensor_base=g.SHARED_TENSOR)
     router = torch.empty((E, N), dtype=torch.float32, device="cuda")
-    g.normal(router, 3, 0, g.ROUTER_TENSOR, 0.02)
+    g.normal(router, cfg, 0, g.ROUTER_TENSOR, 0.02)
     gate = torch.empty(N, dtype=torch.float32, device="cuda")
-    g.normal(gate, 3, 0, g.GATE_TENSOR, 0.02)
-    bias = torch.from_numpy(g.zipf_bias(3, 0, E, ZIPF_PREFILL, PREFILL_ALPHA)).cuda()
+    g.normal(gate, cfg, 0, g.GATE_TENSOR, 0.02)
+    bias = None if bias_np is None else torch.from_numpy(np.ascontiguousarray(bias_np, np.float32)).cuda()
     ml = F.MoeLayer(arena.data_ptr(), stride, E, shared.data_ptr(), router, gate, N, FF, K, router_bias=bias)
-    x = torch.empty((T, N), dtype=torch.float32, device="cuda")
-    g.normal(x, 3, 0, g.X_TENSOR, 1.0, round_bf16=True)
+    ml._bench_keep = (arena, shared, router, gate, bias)
+    return ml
+
+
+def time_prefill_layer(F, torch, ml, x, reps):
+    """ms per call of a prefill-size layer call (event-timed on its stream, after 3 warm calls),
+    the per-kernel durations and the grouped GEMMs' MFMA utilisation."""
+    from types import SimpleNamespace
+    T = x.shape[0]
     out = torch.empty((T, N), dtype=torch.float32, device="cuda")
     ws = ml.workspace(T)
     stream = torch.cuda.Stream()
-    reps = args.prefill_reps
     with torch.cuda.stream(stream):
         for _ in range(3):
             ml.forward(x, out, T=T, ws=ws)
@@ -215,17 +220,121 @@ def run_prefill(args, F, torch):
                               mfma_frac=fl / (avg_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS,
                               kernels=list(parts))
     flops = gu_flops + dn_flops
-    log(f"prefill 2K: {ms:.3f} ms/layer, {T / ms * 1e3:.0f} tok/s, experts {flops / 1e9:.1f} GFLOP")
     return SimpleNamespace(ms=ms, tokens_per_s=T / ms * 1e3, kernels=kt, util=util, flops=flops)
+
+
+def run_prefill(args, F, torch):
+    """one layer, 2048 bf16 tokens, Zipf(1.2) popularity."""
+    ml = build_layer(F, torch, 3, F.gen.zipf_bias(3, 0, E, ZIPF_PREFILL, PREFILL_ALPHA))
+    x = torch.empty((2048, N), dtype=torch.float32, device="cuda")
+    F.gen.normal(x, 3, 0, F.gen.X_TENSOR, 1.0, round_bf16=True)
+    r = time_prefill_layer(F, torch, ml, x, args.prefill_reps)
+    log(f"prefill 2K: {r.ms:.3f} ms/layer, {r.tokens_per_s:.0f} tok/s, experts {r.flops / 1e9:.1f} GFLOP")
+    return r
+
+
+def run_mixed(args, F, torch):
+    """configs[4]: one launch of 8192 bf16 prefill tokens plus 16 uncorrelated fp32 decode tokens;
+    +2.8 on the logits of 16 seeded hot experts puts about 90% of the selections on them."""
+    hot = np.random.default_rng(4).permutation(E)[:16]
+    bias = np.zeros(E, np.float32)
+    bias[hot] = 2.8
+    ml = build_layer(F, torch, 4, bias)
+    x = torch.empty((8192 + 16, N), dtype=torch.float32, device="cuda")
+    F.gen.normal(x[:8192], 4, 0, F.gen.X_TENSOR, 1.0, round_bf16=True)
+    F.gen.normal(x[8192:], 4, 0, F.gen.X_TENSOR + 1, 1.0)
+    r = time_prefill_layer(F, torch, ml, x, max(2, args.prefill_reps // 4))
+    log(f"mixed 8192+16: {r.ms:.3f} ms/layer, {r.tokens_per_s:.0f} tok/s")
+    return r
+
+
+def run_windows(args, F, torch, st):
+    """configs[0] (T = 1) and configs[1] (T = 3, pairwise cosine 0.8) as single-layer calls, and the
+    other verify-window sizes T = 2, 5, 8: configs[0]-shaped layers (no prior, no input norm) over
+    the 48 layers of the stack's arena, one call per layer captured as a graph and replayed, so that
+    every call streams its experts from HBM as a lone layer call would. Per T: us per call and the
+    HBM rate on the bytes the call must read (its distinct routed experts + shared + router)."""
+    arena, shared, router, gate, bias, mls, _, _ = st["_keep"]
+    layers = len(mls)
+    eb = F.expert_bytes(N, FF)
+    lay = [F.MoeLayer(arena.blob(l, 0), arena.stride, E, shared[l].data_ptr(), router[l], gate[l], N, FF, K)
+           for l in range(layers)]
+    stream = torch.cuda.Stream()
+    res = {}
+    reps = max(2, args.window_reps)
+    for T in (1, 2, 3, 5, 8):
+        x = torch.empty((layers, T, N), dtype=torch.float32, device="cuda")
+        for l in range(layers):
+            if T == 3:
+                F.gen.correlated(x[l], 1, l, F.gen.X_TENSOR, 3, N, 0.8)
+            else:
+                F.gen.normal(x[l], 0, l, F.gen.X_TENSOR + T, 1.0)
+        out = torch.empty((layers, T, N), dtype=torch.float32, device="cuda")
+        ids = torch.empty((layers, T, K), dtype=torch.int32, device="cuda")
+        ws = torch.empty(lay[0].workspace_bytes(T), dtype=torch.uint8, device="cuda")
+
+        def body():
+            for l in range(layers):
+                lay[l].forward(x[l], out[l], T=T, ids=ids[l], ws=ws)
+        with torch.cuda.stream(stream):
+            body()
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            body()
+        with torch.cuda.stream(stream):
+            g.replay()
+        stream.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for _ in range(reps):
+                g.replay()
+            e1.record(stream)
+        stream.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * layers)
+        idh = ids.cpu().numpy()
+        distinct = float(np.mean([len(np.unique(idh[l])) for l in range(layers)]))
+        need = (distinct + 1) * eb + E * N * 4 + N * 4
+        path = "decode" if T * K <= 63 and T <= 4 else "prefill"
+        res[f"T{T}"] = dict(us_per_call=round(us, 2), tokens_per_s=round(T / us * 1e6, 1), path=path,
+                            distinct_experts=round(distinct, 2), GBps=round(need / (us * 1e-6) / 1e9, 1))
+        del g
+        log(f"window T={T}: {us:.2f} us/call ({path}), {distinct:.2f} distinct experts")
+    return res
 
 
 # ---------------------------------------------------------------- CPU baseline
 
+def _host_cpus():
+    """(CPUs in this process's affinity mask, physical cores among them, the CPU model name)."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        try:
+            with open(f"/sys/devices/system/cpu/cpu{c}/topology/thread_siblings_list") as f:
+                cores.add(f.read().strip())
+        except OSError:
+            cores.add(str(c))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return len(cpus), len(cores), model
+
+
 def cpu_baseline(args, F, torch, stack):
-    """The reference's moe_cpu (oracle/_ref, AVX-512 VNNI on its CpuPool) or, when that was not
-    built, the oracle's restatement, on a sample of config 2: the first `cpu_layers` layers' experts
-    copied to host RAM, tokens chained through them with routing done on the host (numpy fp32 router
-    GEMV + top-10 + softmax); the per-layer time is scaled to 48 layers."""
+    """The reference's moe_cpu (oracle/_ref: its own CPU sources compiled here, AVX-512 VNNI on its
+    CpuPool) or, when that was not built, the oracle's restatement, on a sample of config 2: the
+    first `cpu_layers` layers' experts copied to host RAM, tokens chained through them with routing
+    done on the host (numpy fp32 router GEMV + top-10 + softmax); the per-layer time is scaled to 48
+    layers. Run with one worker per physical core of this process's CPUs (the reported value) and
+    again with 8 workers."""
     from oracle import oracle as O
     arena, shared, router, gate, bias, mls, _, _ = stack["_keep"]
     nl = args.cpu_layers
@@ -242,70 +351,81 @@ def cpu_baseline(args, F, torch, stack):
     gw = gate[:nl].cpu().numpy()
     bh = bias[:nl].cpu().numpy()
     host_np = host.numpy()
-    n_aff = len(os.sched_getaffinity(0))
-    workers = max(1, min(n_aff, int(os.environ.get("OMP_NUM_THREADS", "16")), 16))
+    n_aff, n_phys, model = _host_cpus()
     kind = "reference" if O.have_ref() else "port"
     R = O.ref() if O.have_ref() else None
-    pool = R.ref_pool_create(workers, 0) if R else None
     rng_x = O.gen_normal(2, 0, O.X_TENSOR, 64 * N).reshape(64, N)
     blobs = (C.c_void_p * 11)()
-    route_times, moe_times = [], []
-    t_end = time.perf_counter() + args.cpu_seconds
-    steps = 0
     try:
         from threadpoolctl import threadpool_limits
-        limiter = threadpool_limits(1)
     except Exception:
-        limiter = None
-    while time.perf_counter() < t_end and steps < 64:
-        x = rng_x[steps].copy()
-        for l in range(nl):
-            t0 = time.perf_counter()
-            u = (x / np.sqrt(np.float32((x.astype(np.float64) ** 2).mean()) + np.float32(1e-6))).astype(np.float32)
-            lg = rw[l] @ u + bh[l]
-            top = np.argsort(-lg, kind="stable")[:K]
-            p = np.exp((lg - lg.max()).astype(np.float64))
-            p /= p.sum()
-            w = (p[top] / p[top].sum()).astype(np.float32)
-            gl = float(gw[l] @ u)
-            order = np.argsort(top)
-            for i, k in enumerate(order):
-                blobs[i] = host_np[l, top[k]].ctypes.data
-            blobs[10] = sh_h[l].ctypes.data
-            ntok = np.ones(11, np.int32)
-            tok = np.zeros(44, np.int32)
-            wv = np.zeros(44, np.float32)
-            wv[0:40:4] = w[order]
-            wv[40] = 1.0 / (1.0 + np.exp(-np.clip(gl, -80.0, 80.0)))
-            out = np.zeros(N, np.float32)
-            t1 = time.perf_counter()
-            if R:
-                prep = R.ref_moe_prepare(pool, N, FF, C.cast(blobs, C.c_void_p), ntok, tok, wv, 11, u, 1)
-                R.ref_moe_run(pool, prep, out, N)
-                R.ref_moe_free(prep)
-            else:
-                qs, d = O.quantize_q8(u)
-                O.lib().orc_moe_cpu(N, FF, C.cast(blobs, C.c_void_p), ntok, tok, wv, 11, qs, d, 1, out, N, workers, 1)
-            t2 = time.perf_counter()
-            route_times.append(t1 - t0)
-            moe_times.append(t2 - t1)
-            x = x + out
-        steps += 1
-    if limiter is not None:
-        limiter.unregister() if hasattr(limiter, "unregister") else None
-    if pool:
-        R.ref_pool_destroy(pool)
-    layer_times = [a + b for a, b in zip(route_times, moe_times)]
-    t_layer = float(np.median(layer_times))
-    return dict(value=1.0 / (LAYERS * t_layer), unit="tokens/s", cores=workers, kind=kind,
-                sample=(f"{steps} tokens x {nl} of {LAYERS} layers of configs[2] on the host CPU ({n_aff} CPUs in "
-                        f"this process's affinity mask): RMS norm + numpy fp32 router + top-10 on one thread "
-                        f"(median {np.median(route_times) * 1e6:.0f} us), then the "
-                        f"{'reference moe_cpu (AVX-512 VNNI) on its CpuPool' if R else 'oracle moe_cpu port'} with "
-                        f"{workers} workers over the 10 routed + shared experts (median "
-                        f"{np.median(moe_times) * 1e6:.0f} us); median {t_layer * 1e6:.0f} us/layer x {LAYERS} layers"),
-                moe_cpu_us=round(float(np.median(moe_times)) * 1e6, 1),
-                moe_cpu_GBps=round(11 * F.expert_bytes(N, FF) / float(np.median(moe_times)) / 1e9, 2))
+        threadpool_limits = None
+
+    def sample(workers, seconds):
+        pool = R.ref_pool_create(workers, 0) if R else None
+        # numpy's BLAS threads stay at one: idle BLAS workers spinning beside the pool's would steal its cores
+        limiter = threadpool_limits(1) if threadpool_limits else None
+        route_times, moe_times = [], []
+        t_end = time.perf_counter() + seconds
+        steps = 0
+        try:
+            while time.perf_counter() < t_end and steps < 64:
+                x = rng_x[steps].copy()
+                for l in range(nl):
+                    t0 = time.perf_counter()
+                    u = (x / np.sqrt(np.float32((x.astype(np.float64) ** 2).mean()) + np.float32(1e-6))).astype(np.float32)
+                    lg = rw[l] @ u + bh[l]
+                    top = np.argsort(-lg, kind="stable")[:K]
+                    p = np.exp((lg - lg.max()).astype(np.float64))
+                    p /= p.sum()
+                    w = (p[top] / p[top].sum()).astype(np.float32)
+                    gl = float(gw[l] @ u)
+                    order = np.argsort(top)
+                    for i, k in enumerate(order):
+                        blobs[i] = host_np[l, top[k]].ctypes.data
+                    blobs[10] = sh_h[l].ctypes.data
+                    ntok = np.ones(11, np.int32)
+                    tok = np.zeros(44, np.int32)
+                    wv = np.zeros(44, np.float32)
+                    wv[0:40:4] = w[order]
+                    wv[40] = 1.0 / (1.0 + np.exp(-np.clip(gl, -80.0, 80.0)))
+                    out = np.zeros(N, np.float32)
+                    t1 = time.perf_counter()
+                    if R:
+                        prep = R.ref_moe_prepare(pool, N, FF, C.cast(blobs, C.c_void_p), ntok, tok, wv, 11, u, 1)
+                        R.ref_moe_run(pool, prep, out, N)
+                        R.ref_moe_free(prep)
+                    else:
+                        qs, d = O.quantize_q8(u)
+                        O.lib().orc_moe_cpu(N, FF, C.cast(blobs, C.c_void_p), ntok, tok, wv, 11, qs, d, 1, out, N,
+                                            workers, 1)
+                    t2 = time.perf_counter()
+                    route_times.append(t1 - t0)
+                    moe_times.append(t2 - t1)
+                    x = x + out
+                steps += 1
+        finally:
+            if limiter is not None and hasattr(limiter, "unregister"):
+                limiter.unregister()
+            if pool:
+                R.ref_pool_destroy(pool)
+        t_layer = float(np.median([a + b for a, b in zip(route_times, moe_times)]))
+        return dict(workers=workers, tokens=steps, us_per_layer=round(t_layer * 1e6, 1),
+                    route_us=round(float(np.median(route_times)) * 1e6, 1),
+                    moe_cpu_us=round(float(np.median(moe_times)) * 1e6, 1),
+                    moe_cpu_GBps=round(11 * F.expert_bytes(N, FF) / float(np.median(moe_times)) / 1e9, 2),
+                    tokens_per_s=round(1.0 / (LAYERS * t_layer), 2))
+
+    full = sample(n_phys, args.cpu_seconds)
+    eight = sample(8, args.cpu_seconds / 2)
+    what = "the reference moe_cpu (AVX-512 VNNI) on its CpuPool" if R else "the oracle's moe_cpu restatement"
+    return dict(value=full["tokens_per_s"], unit="tokens/s", cores=n_phys, kind=kind, cpu_model=model,
+                sample=(f"{full['tokens']} tokens x {nl} of {LAYERS} layers of configs[2] on the host CPU "
+                        f"({model}; {n_aff} CPUs in this process's affinity mask, {n_phys} physical cores): RMS norm "
+                        f"+ numpy fp32 router + top-10 on one thread (median {full['route_us']:.0f} us), then {what} with "
+                        f"{n_phys} workers over the 10 routed + shared experts (median {full['moe_cpu_us']:.0f} us); "
+                        f"median {full['us_per_layer']:.0f} us/layer x {LAYERS} layers"),
+                all_cores=full, workers_8=eight)
 
 
 def _copy_arena_layer(arena, l, dst):
@@ -331,6 +451,9 @@ def main():
                     help="first run 3 plain device copies of MIB MiB (scales the HBM byte counters of a profile)")
     ap.add_argument("--timing-steps", type=int, default=3, help="decode steps in the per-kernel timing pass")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-windows", action="store_true", help="skip configs[0]/[1] and the other window sizes")
+    ap.add_argument("--window-reps", type=int, default=8, help="replays of the 48-call graph per window size")
+    ap.add_argument("--no-mixed", action="store_true", help="skip configs[4]")
     ap.add_argument("--decode-grid", type=int, default=0, help="workgroups of a persistent decode call (0: one per CU)")
     ap.add_argument("--decode-path", choices=["stack", "fused", "three"], default="stack",
                     help="the 48 layers as one persistent launch (stack, default), one persistent launch per layer "
@@ -417,18 +540,28 @@ def main():
                                                        / HBM_PEAK_GBS, 4),
                   "kernels": kernels},
     }
+    def pf_entry(pf):
+        return {"tokens_per_s": round(pf.tokens_per_s, 1), "ms_per_layer": round(pf.ms, 4),
+                "expert_gflop": round(pf.flops / 1e9, 2),
+                "mfma_frac_layer": round(pf.flops / (pf.ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                "kernels": {k: dict(avg_us=round(v[0] / v[1] * 1e3, 2), launches=v[1]) for k, v in pf.kernels.items()},
+                "mfma": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                         for k, v in pf.util.items()}}
     if not args.no_prefill:
-        pf = run_prefill(args, F, torch)
-        line["prefill_2k"] = {"tokens_per_s": round(pf.tokens_per_s, 1), "ms_per_layer": round(pf.ms, 4),
-                              "expert_gflop": round(pf.flops / 1e9, 2),
-                              "mfma_frac_layer": round(pf.flops / (pf.ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-                              "kernels": {k: dict(avg_us=round(v[0] / v[1] * 1e3, 2), launches=v[1])
-                                          for k, v in pf.kernels.items()},
-                              "mfma": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                                       for k, v in pf.util.items()}}
+        line["prefill_2k"] = pf_entry(run_prefill(args, F, torch))
+    if not args.no_mixed:
+        line["mixed_cfg4"] = pf_entry(run_mixed(args, F, torch))
+    if not args.no_windows:
+        win = run_windows(args, F, torch, st)
+        line["decode_cfg0"] = win["T1"]
+        line["decode_cfg1"] = win["T3"]
+        line["decode_windows"] = win
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args, F, torch, st)
     print(json.dumps(line), flush=True)
+    st.clear()
+    torch.cuda.synchronize()
+    sys.stderr.flush()
 
 
 if __name__ == "__main__":

@@ -40,7 +40,7 @@ __global__ void k_hits_group(const uint8_t* const* __restrict__ hit_ptr, const i
         for (int k = 0; k < h; ++k) {
             const uint8_t* p = hit_ptr[t * K + k];
             int u = 0;
-            while (u < U && ent[u].blob != p) ++u;
+            while (u < U && (ent[u].blob != p || ent[u].ntok == kDecMaxT)) ++u;   // a full entry: the repeat opens another
             if (u == U) {
                 DecEntry d{};
                 d.blob = p;
@@ -540,7 +540,13 @@ static int dec_down(const DecScratch& s, int n, int ff, int T, int K, const floa
 int dec_check(int T, int K, int n, int ff) {
     if (T < 1 || T > kDecMaxT) return set_error(kErrShape, "decode: T=%d (1..4)", T);
     if (K < 1 || K > 32 || T * K > 63) return set_error(kErrShape, "decode: K=%d with T=%d (T*K <= 63)", K, T);
-    if (n % 64 || ff % 64 || n % 8 || ff % 32) return set_error(kErrShape, "decode: n=%d ff=%d", n, ff);
+    if (n % 64 || ff % 64) return set_error(kErrShape, "decode: n=%d ff=%d (multiples of 64)", n, ff);
+    // the instantiated GEMV shapes, checked here so that a refused call launches nothing
+    const int nb = n / kBlock, nbf = ff / kBlock;
+    if (nb != 16 && nb != 32 && nb != 40 && nb != 48 && nb != 64)
+        return set_error(kErrShape, "decode: n=%d unsupported (n/64 in {16,32,40,48,64})", n);
+    if (nbf != 4 && nbf != 8 && nbf != 10 && nbf != 16)
+        return set_error(kErrShape, "decode: ff=%d unsupported (ff/64 in {4,8,10,16})", ff);
     return kOk;
 }
 

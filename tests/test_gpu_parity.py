@@ -190,14 +190,17 @@ def test_layer_decode_config0(F, w0):
     assert H.out_rel(out, ref) <= H.OUT_REL
 
 
-@pytest.mark.parametrize("E", [300, 128])
-def test_layer_decode_other_expert_counts(F, E):
-    """Single-token decode with E not 64 times the per-lane logit count (300: the clamped logit loads,
-    the last lane's tail past E; 128: two logits per lane), ids, weights and output against the
-    oracle (the reference routes any E up to its kernel's bound, blocks.hpp:130-135)."""
+@pytest.mark.parametrize("T", [1, 2])
+@pytest.mark.parametrize("E", [300, 128, 1000, 1024])
+def test_layer_decode_other_expert_counts(F, E, T):
+    """Decode routing with other expert counts. Each lane holds V consecutive logits (V = 8 for
+    E <= 512, 16 above): E = 128 fills 16 lanes, 300 ends inside a lane (clamped loads, tail past
+    E), 1000 and 1024 take the V = 16 selection. T = 1 runs the single-token selection, T = 2 the
+    four-wave one. Ids, weights and output against the oracle (the reference routes any E up to
+    its kernel's bound, blocks.hpp:130-135)."""
     w = H.World(cfg=0, E=E)
-    rng = np.random.default_rng(E)
-    x = rng.standard_normal((1, H.N)).astype(np.float32)
+    rng = np.random.default_rng(E + T)
+    x = rng.standard_normal((T, H.N)).astype(np.float32)
     out, ids, wts = w.gpu_forward(x)
     ref, rid, rw, _ = w.oracle_forward(x)
     assert np.array_equal(ids, rid)
@@ -276,6 +279,34 @@ def test_moe_hits(F, w0):
         torch.cuda.synchronize()
         a = y1.cpu().numpy()[0, :hit_n[t]]
         assert np.array_equal(a, y[t, :hit_n[t]])
+
+
+def test_moe_hits_repeated_blob(F, w0):
+    """One blob hit more often in a window than one grouped entry holds (four token slots): twice
+    by token 0 and once by each of tokens 1-3, plus a token listing another blob three times. Every
+    slot against the oracle (the reference's k_moe_group keeps one slot per (expert, token),
+    moe_fast.cu:195-232), pad slots untouched."""
+    T, K = 4, 8
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((T, H.N)).astype(np.float32)
+    hit_n = np.array([8, 6, 7, 8], np.int32)
+    experts = rng.choice(512, size=(T, K), replace=True).astype(np.int64)
+    experts[0, 1] = experts[0, 5] = experts[1, 0] = experts[2, 6] = experts[3, 3] = 77
+    experts[3, 0] = experts[3, 4] = experts[3, 7] = 300
+    base = w0.arena.data_ptr()
+    ptr = torch.tensor((base + experts * w0.stride).reshape(-1), dtype=torch.int64, device="cuda")
+    yh = torch.full((T, K, H.N), float("nan"), dtype=torch.float32, device="cuda")
+    scratch = torch.empty(F.moe_hits_scratch_bytes(K, H.FF, T, H.N), dtype=torch.uint8, device="cuda")
+    F.moe_hits(ptr, dev(hit_n), K, dev(x), H.N, H.FF, scratch, yh, T=T)
+    torch.cuda.synchronize()
+    y = yh.cpu().numpy()
+    for t in range(T):
+        assert np.isnan(y[t, hit_n[t]:]).all()
+        for k in range(hit_n[t]):
+            ref = O.expert_ffn(w0.blob(int(experts[t, k])), H.N, H.FF, x[t])
+            assert H.out_rel(y[t, k][None], ref) <= H.OUT_REL, (t, k)
+    assert np.array_equal(y[0, 1], y[0, 5])
+    assert np.array_equal(y[3, 0], y[3, 4]) and np.array_equal(y[3, 0], y[3, 7])
 
 
 @pytest.mark.parametrize("T,K", [(8, 10), (5, 32)])
@@ -622,13 +653,31 @@ def test_stack_layers_teacher_forced(F, T):
         x = out
 
 
-def test_rmsnorm_router_bit_exact(F):
-    """The stack's normalised input feeds the router: logits with norm_input equal the oracle's on
-    rmsnorm(x), bit for bit (checked through the layer's ids above and here on the logits path)."""
-    rng = np.random.default_rng(11)
-    x = (rng.standard_normal((2, H.N)) * 5).astype(np.float32)
-    u = O.rmsnorm(x)
-    assert np.allclose((u.astype(np.float64) ** 2).mean(axis=1), 1.0, rtol=1e-5)
+@pytest.mark.parametrize("T", [3, 300])
+def test_norm_input_routing(F, T):
+    """The layer with the stack's RMS norm on its input (FRT_LAYER_NORM_INPUT) off the single-token
+    path: a decode window (T = 3) and the prefill router GEMM (T = 300) route rmsnorm(x) as the
+    oracle does: ids bit-exact, each selection's probability within 1e-6 relative of the oracle's
+    softmax over its logits on rmsnorm(x), outputs within the layer bar. (The single-token path's
+    logits are compared bit for bit in test_decode_fused_router_logits_bit_exact.)"""
+    bias = O.gen_zipf_bias(2, 5, H.E, H.ZIPF_S_STACK)
+    w = H.World(cfg=2, layer=5, bias=bias, norm_input=True)
+    x = (np.random.default_rng(T).standard_normal((T, H.N)) * 3).astype(np.float32)
+    out = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    ids = torch.empty((T, H.K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, H.K), dtype=torch.float32, device="cuda")
+    probs = torch.empty((T, H.K), dtype=torch.float32, device="cuda")
+    w.layer_obj.forward(dev(x), out, T=T, ids=ids, wts=wts, probs=probs)
+    torch.cuda.synchronize()
+    ref, rid, rw, lg = w.oracle_forward(x)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    assert H.w_rel(wts.cpu().numpy(), rw) <= H.W_REL
+    lg = lg.astype(np.float64)
+    p = np.exp(lg - lg.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    want = np.take_along_axis(p, rid, axis=1)
+    assert float((np.abs(probs.cpu().numpy() - want) / want).max()) <= 1e-6
+    assert H.out_rel(out.cpu().numpy(), ref) <= H.OUT_REL
 
 
 def test_cpp_mirror_gpu():
