@@ -401,7 +401,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 template <bool SMALL>
 __global__ void __launch_bounds__(GuShape<SMALL>::threads, GuShape<SMALL>::min_waves)
 k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t* __restrict__ shared_blob, int n,
-          int ff, const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
+          int np, int hblk, int ff, const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
           const int32_t* __restrict__ tok_of, const int32_t* __restrict__ bounds, const int2* __restrict__ tiles,
           const int32_t* __restrict__ n_tiles, _Float16* __restrict__ hout) {
     using Sh = GuShape<SMALL>;
@@ -436,23 +436,25 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
     __syncthreads();
 
     // this lane's weight rows: ff row rbase + 32 wave + 16 (i & 1) + li of gate (i < 2) and up;
-    // rows past the end load any row and are never stored. aoff = row * nbk + lg: the chunk and
-    // scale index of block lg of stretch 0.
+    // rows past the end load any row and are never stored. aoff = row * nbk: the chunk and scale
+    // index of the row's block 0. K runs to np (n rounded up to 512, the activations zero past n):
+    // a block past the row's last is read as its last, whose finite products with zeros are 0.
     const uint8_t* const mG = blob;
     const uint8_t* const mU = blob + mb;
     const size_t scale_off = size_t(ff) * nbk * 16;
     uint32_t aoff[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) aoff[i] = uint32_t(min(rbase + 32 * wave + 16 * i + li, ff - 1)) * nbk + lg;
+    for (int i = 0; i < 2; ++i) aoff[i] = uint32_t(min(rbase + 32 * wave + 16 * i + li, ff - 1)) * nbk;
     struct ARegs {
         uint4 cw[4];
         uint32_t sc[4];
     };
     auto load_a = [&](int q, ARegs& a) {   // stretch q (blocks 4q + lg)
+        const int bq = min(4 * q + lg, nbk - 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint8_t* m = i < 2 ? mG : mU;
-            const size_t o = size_t(aoff[i & 1]) + 4 * q;
+            const size_t o = size_t(aoff[i & 1]) + bq;
             a.cw[i] = gld_u4(m + o * 16);
             a.sc[i] = gld<uint16_t>(m + scale_off + o * 2);
         }
@@ -462,7 +464,7 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
 #pragma unroll
     for (int p = 0; p < Sh::dma; ++p) {
         const int P = Sh::threads * p + tid, j = P / Sh::cpt, kc = (P % Sh::cpt) ^ (j & (Sh::cpt - 1));
-        boff[p] = uint32_t(sRow[j]) * n + kc * 8;
+        boff[p] = uint32_t(sRow[j]) * np + kc * 8;
     }
     auto issue_b = [&](int st, int slot) {
         uint8_t* b = smem + slot * NP * Sh::slot_b;
@@ -516,8 +518,8 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
     // registers / a slot nothing reads any more), so the wait counts are constants and the
     // compiler's own waits for the weight registers never see a path without later loads (at such
     // a merge it would wait for every load in flight).
-    const int nst = n / Sh::stage_k;   // stages
-    const int nq = n / 256;            // stretches (even)
+    const int nst = np / Sh::stage_k;   // stages
+    const int nq = np / 256;            // stretches (even)
     auto run = [&](auto nc) {
         ARegs a0, a1;   // stretches of even / odd index (named, so they stay in registers)
         // the loads of stages -max(ahead, sps) .. -1 of the steady-state pattern below
@@ -581,6 +583,14 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
             }
         am = fmaxf(am, __builtin_bit_cast(float, lane_xor16(__builtin_bit_cast(int, am))));
         am = fmaxf(am, __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(int, am))));
+        if (hblk == 64) {   // ff rows 64 m .. 64 m + 63 are waves 2m' and 2m' + 1 (rbase is a multiple of 128)
+            wait_vm<0>();      // the ring's last direct-to-LDS loads (repeats past the end) have landed
+            __syncthreads();   // (uniform: hblk is a kernel argument) every wave is past its last LDS read
+            float* sam = reinterpret_cast<float*>(smem);
+            if (lg == 0) sam[wave * 16 + li] = am;
+            __syncthreads();
+            am = fmaxf(am, sam[(wave ^ 1) * 16 + li]);
+        }
         const float d = q8_scale(am);
         const float id = q8_inv(d);
         const float dr = f16_round(d);
@@ -663,20 +673,24 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
         ldsdma16(h + size_t(sRow[j]) * ffp + kc * 8, smem + P * 16 - lane * 16);
     }
 
-    uint32_t aoff[4];   // chunk index of block 0 of this lane's row in row block 0, for tile i
+    uint32_t aoff[4];   // this lane's row in its row block, for tile i
 #pragma unroll
-    for (int i = 0; i < 4; ++i) aoff[i] = uint32_t(64 * wave + 16 * i + li) * nbk;
+    for (int i = 0; i < 4; ++i) aoff[i] = uint32_t(64 * wave + 16 * i + li);
     struct ARegs {
         uint4 cw[4];
         uint32_t sc[4];
     };
-    const int nsx = (n / 256) * NQ;   // stretches in all (a multiple of 4 unless TAIL)
-    auto load_a = [&](int s, ARegs& a) {   // stretch s: row block s / NQ, blocks 4 (s % NQ) + lg
-        const size_t base = size_t(s / NQ) * 256 * nbk + min(4 * (s % NQ) + lg, nbk - 1);
+    const int nsx = ((n + 255) / 256) * NQ;   // stretches in all (a multiple of 4 unless TAIL)
+    // stretch s: row block s / NQ, blocks 4 (s % NQ) + lg; rows past n (a last block of 128 rows)
+    // read row n - 1 and are never stored
+    auto load_a = [&](int s, ARegs& a) {
+        const int rb = s / NQ;
+        const uint32_t blk = min(4 * (s % NQ) + lg, nbk - 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            a.cw[i] = gld_u4(md + (base + aoff[i]) * 16);
-            a.sc[i] = gld<uint16_t>(md + scale_off + (base + aoff[i]) * 2);
+            const size_t o = size_t(min(rb * 256 + int(aoff[i]), n - 1)) * nbk + blk;
+            a.cw[i] = gld_u4(md + o * 16);
+            a.sc[i] = gld<uint16_t>(md + scale_off + o * 2);
         }
     };
     const DqMagic mg = dq_magic();
@@ -731,7 +745,7 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int r = rb * 256 + 64 * wave + 16 * i + 4 * lg;
-                            store4(yd + yslot[c] + r, acc[i][c]);
+                            if (r < n) store4(yd + yslot[c] + r, acc[i][c]);   // (n % 4 == 0)
                         }
                     }
 #pragma unroll
@@ -817,6 +831,8 @@ struct PfWs {
 };
 
 static int pf_max_tiles(int S, int G) { return (S + kTN - 1) / kTN + G; }
+// the gate/up GEMM's K extent: n rounded up to whole pairs of 256-element stretches
+static int pf_np(int n) { return (n + 511) & ~511; }
 
 static PfWs pf_carve(void* base, int T, int K, int n, int ff, int E, bool shared, bool own_yd) {
     PfWs w{};
@@ -835,8 +851,8 @@ static PfWs pf_carve(void* base, int T, int K, int n, int ff, int E, bool shared
     w.slot_of = reinterpret_cast<int32_t*>(take(size_t(S) * 4));
     w.n_tiles = reinterpret_cast<int32_t*>(take(8));   // [0] tiles, [1] first tile of one column
     w.tiles = reinterpret_cast<int2*>(take(size_t(pf_max_tiles(S, G)) * 8));
-    w.xhi = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
-    w.xlo = reinterpret_cast<_Float16*>(take(size_t(T) * n * 2));
+    w.xhi = reinterpret_cast<_Float16*>(take(size_t(T) * pf_np(n) * 2));
+    w.xlo = reinterpret_cast<_Float16*>(take(size_t(T) * pf_np(n) * 2));
     w.h16 = reinterpret_cast<_Float16*>(take(size_t(S) * ((ff + 255) & ~255) * 2));
     w.yd = own_yd ? reinterpret_cast<_Float16*>(take(size_t(S) * n * 2)) : nullptr;
     w.bytes = size_t(p - static_cast<uint8_t*>(base));
@@ -847,15 +863,14 @@ size_t pf_workspace_bytes(int T, int K, int n, int ff, int E, bool shared, bool 
     return pf_carve(nullptr, T, K, n, ff, E, shared, own_yd).bytes + 256;
 }
 
-int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xhi, _Float16* xlo,
-                hipStream_t stream);
+int quantize_pairs(const float* x, int rows, int n, int np, int blk, _Float16* xhi, _Float16* xlo, hipStream_t stream);
 
 int pf_check(int T, int K, int n, int ff, int E) {
     if (T < 1 || K < 1 || K > 32 || E < 1 || E > 4096 || K > E) return set_error(kErrShape, "prefill: T=%d K=%d E=%d", T, K, E);
-    // gate/up: whole pairs of 256-element weight stretches along n, slices of 128 ff rows; down: the
-    // tile's h (ff rounded up to 256) in LDS, at most 1024
-    if (n % 512 || n < 512 || ff % 128 || ff < 128 || ff > 1024)
-        return set_error(kErrShape, "prefill: n=%d ff=%d (n a multiple of 512; ff a multiple of 128 up to 1024)", n,
+    // n and ff multiples of 128 (moe_q2.cu:516-517); gate/up: slices of 128 ff rows; down: the tile's
+    // h (ff rounded up to 256) in LDS, at most 1024
+    if (n % 128 || n < 128 || n > 65536 || ff % 128 || ff < 128 || ff > 1024)
+        return set_error(kErrShape, "prefill: n=%d ff=%d (n a multiple of 128; ff a multiple of 128 up to 1024)", n,
                          ff);
     return kOk;
 }
@@ -886,23 +901,23 @@ static int pf_down_attr(size_t lds) {
 // epilogue; down (k_pf_down) on h -> yd per slot as OutT.
 template <typename OutT>
 static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, int n, int ff,
-                           const PfWs& w, int mt, OutT* ydf, hipStream_t stream) {
+                           int blk, const PfWs& w, int mt, OutT* ydf, hipStream_t stream) {
     if (int rc = pf_gemm_attr<false>()) return rc;
     if (int rc = pf_gemm_attr<true>()) return rc;
     // tiles of 2-4 token columns, then those of one (the tile list is ordered longest first)
     const int mt8 = (mt + 7) / 8 * 8;
     launch_timed("pf_gateup", k_pf_gemm<false>, dim3(ff / GuShape<false>::ff_rows * mt8), dim3(GuShape<false>::threads),
-                 GuShape<false>::smem, stream, arena, stride, E, shared_blob, n, ff, (const _Float16*)w.xhi,
+                 GuShape<false>::smem, stream, arena, stride, E, shared_blob, n, pf_np(n), blk, ff, (const _Float16*)w.xhi,
                  (const _Float16*)w.xlo, (const int32_t*)w.tok_of, (const int32_t*)w.bounds, (const int2*)w.tiles,
                  (const int32_t*)w.n_tiles, w.h16);
     launch_timed("pf_gateup1", k_pf_gemm<true>, dim3(ff / GuShape<true>::ff_rows * mt8), dim3(GuShape<true>::threads),
-                 GuShape<true>::smem, stream, arena, stride, E, shared_blob, n, ff, (const _Float16*)w.xhi,
+                 GuShape<true>::smem, stream, arena, stride, E, shared_blob, n, pf_np(n), blk, ff, (const _Float16*)w.xhi,
                  (const _Float16*)w.xlo, (const int32_t*)w.tok_of, (const int32_t*)w.bounds, (const int2*)w.tiles,
                  (const int32_t*)w.n_tiles, w.h16);
     timing_mark(stream, "pf_gateup");
     const int nq = (ff + 255) / 256;                     // stretches per h row
     const size_t down_lds = size_t(kTN) * nq * 256 * 2;  // the tile's activations
-    const bool tail = (n / 256) * nq % 4 != 0;
+    const bool tail = ((n + 255) / 256) * nq % 4 != 0;
 #define FRT_PF_DOWN(NQV, TL)                                                                                 \
     if (nq == NQV && tail == TL) {                                                                           \
         if (int rc = pf_down_attr<NQV, TL, OutT>(down_lds)) return rc;                                       \
@@ -919,7 +934,7 @@ static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uin
 // The grouped expert products for routed ids (+ optionally the shared expert as group E).
 // yd_kind: 0 float, 1 bf16 (moe_q2::run's yd_bf16), 2 fp16 (a whole layer's, combined here)
 static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, int n, int ff,
-                      const float* x, const int32_t* ids, int T, int K, void* yd, int yd_kind, const PfWs& w,
+                      const float* x, const int32_t* ids, int T, int K, void* yd, int yd_kind, int blk, const PfWs& w,
                       hipStream_t stream) {
     const bool shared = shared_blob != nullptr;
     const int S = T * K + (shared ? T : 0);
@@ -927,7 +942,7 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
     const int nchunk = (T * K + kChunk - 1) / kChunk;
     int id_bits = 1;
     while ((1 << id_bits) < E) ++id_bits;
-    if (int rc = quantize_q8(x, T, n, nullptr, nullptr, w.xhi, w.xlo, stream)) return rc;
+    if (int rc = quantize_pairs(x, T, n, pf_np(n), blk, w.xhi, w.xlo, stream)) return rc;
     timing_mark(stream, "pf_quant_x");
     launch_timed("pf_hist", k_pf_hist, dim3(nchunk), dim3(256), size_t(E) * 4, stream, ids, T * K, E, w.cnt);
     launch_timed("pf_scan", k_pf_scan, dim3(1), dim3(1024), 0, stream, w.cnt, nchunk, E, T, K, shared ? 1 : 0, w.bounds,
@@ -937,9 +952,9 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
     timing_mark(stream, "pf_dispatch");
     const int mt = pf_max_tiles(S, G);
     int rc = kOk;
-    if (yd_kind == 1) rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, w, mt, static_cast<__hip_bfloat16*>(yd), stream);
-    else if (yd_kind == 2) rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, w, mt, static_cast<_Float16*>(yd), stream);
-    else rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, w, mt, static_cast<float*>(yd), stream);
+    if (yd_kind == 1) rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, blk, w, mt, static_cast<__hip_bfloat16*>(yd), stream);
+    else if (yd_kind == 2) rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, blk, w, mt, static_cast<_Float16*>(yd), stream);
+    else rc = pf_expert_gemms(arena, stride, E, shared_blob, n, ff, blk, w, mt, static_cast<float*>(yd), stream);
     if (rc) return rc;
     timing_mark(stream, "pf_down");
     FRT_LAUNCHED("prefill experts");
@@ -950,11 +965,11 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
 int pf_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const float* x, const int32_t* ids, int T, int K,
            void* yd, void* ws, size_t ws_bytes, hipStream_t stream, int block64, int yd_bf16) {
     if (int rc = pf_check(T, K, n, ff, E)) return rc;
-    if (block64) return set_error(kErrShape, "moe_q2::run: block64 activations are not supported (Q8_0 blocks of 32 only)");
     if (!experts || !x || !ids || !yd || !ws) return set_error(kErrNull, "moe_q2::run: null pointer");
     const PfWs w = pf_carve(ws, T, K, n, ff, E, false, false);
     if (w.bytes > ws_bytes) return set_error(kErrWorkspace, "moe_q2::run: workspace %zu < %zu", ws_bytes, w.bytes);
-    return pf_experts(experts, stride, E, nullptr, n, ff, x, ids, T, K, yd, yd_bf16 ? 1 : 0, w, stream);
+    // block64: x and h quantized in Q8_0 blocks of 64 values rather than 32 (moe_q2.cu's AB = 64)
+    return pf_experts(experts, stride, E, nullptr, n, ff, x, ids, T, K, yd, yd_bf16 ? 1 : 0, block64 ? 64 : 32, w, stream);
 }
 
 // The whole prefill layer after routing: ids/wts [T][K], gate [T] -> out [T][n] (+ resid)
@@ -964,7 +979,7 @@ int pf_moe(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blo
     if (int rc = pf_check(T, K, n, ff, E)) return rc;
     const PfWs w = pf_carve(ws, T, K, n, ff, E, true, true);
     if (w.bytes > ws_bytes) return set_error(kErrWorkspace, "prefill: workspace %zu < %zu", ws_bytes, w.bytes);
-    if (int rc = pf_experts(arena, stride, E, shared_blob, n, ff, x, ids, T, K, w.yd, 2, w, stream)) return rc;
+    if (int rc = pf_experts(arena, stride, E, shared_blob, n, ff, x, ids, T, K, w.yd, 2, 32, w, stream)) return rc;
     launch_timed("pf_combine", k_pf_combine<_Float16>, dim3((n + 1023) / 1024, T), dim3(256), 0, stream,
                  (const _Float16*)w.yd, ids, wts, gate, T, K, n, 1, resid, out);
     timing_mark(stream, "pf_combine");

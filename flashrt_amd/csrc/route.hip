@@ -182,18 +182,23 @@ __global__ void k_quant_q8(const float* __restrict__ x, int n_blocks, int8_t* __
 // wave per 256-element stretch, 4 consecutive elements per lane (8 lanes per Q8_0 block of 32). The
 // pairs go through LDS so that each lane then writes 4 consecutive positions (8 bytes) of each.
 // Same values as k_quant_q8 with xhi / xlo.
-__global__ void __launch_bounds__(256) k_quant_pairs(const float* __restrict__ x, int n_stretch,
+// x [rows][n] -> the pairs [rows][np] (np >= n a multiple of 256; positions n .. np - 1 are zeros),
+// Q8_0 blocks of blk = 32 or 64 values (moe_q2::run's block64).
+__global__ void __launch_bounds__(256) k_quant_pairs(const float* __restrict__ x, int n, int np, int n_stretch, int blk,
                                                      _Float16* __restrict__ xhi, _Float16* __restrict__ xlo) {
     __shared__ _Float16 sp[4][2][256];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int st = blockIdx.x * 4 + wave;
     if (st >= n_stretch) return;   // whole waves; no workgroup barrier below
-    const float4 v4 = *reinterpret_cast<const float4*>(x + size_t(st) * 256 + lane * 4);
+    const int spr = np / 256, row = st / spr, col = (st % spr) * 256 + lane * 4;   // n % 4 == 0
+    const float4 v4 = col < n ? *reinterpret_cast<const float4*>(x + size_t(row) * n + col) : make_float4(0, 0, 0, 0);
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
     float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     am = fmaxf(am, __shfl_xor(am, 1));
     am = fmaxf(am, __shfl_xor(am, 2));
-    am = fmaxf(am, __shfl_xor(am, 4));   // the 8 lanes of the block
+    am = fmaxf(am, __shfl_xor(am, 4));   // the 8 lanes of a 32-block
+    const float am16 = fmaxf(am, __shfl_xor(am, 8));
+    am = blk == 64 ? am16 : am;          // the 16 lanes of a 64-block
     const float d = q8_scale(am);
     const float id = q8_inv(d);
     const float dr = f16_round(d);
@@ -212,6 +217,7 @@ __global__ void __launch_bounds__(256) k_quant_pairs(const float* __restrict__ x
     *reinterpret_cast<uint2*>(xhi + size_t(st) * 256 + lane * 4) = h;
     *reinterpret_cast<uint2*>(xlo + size_t(st) * 256 + lane * 4) = l;
 }
+// (a zero block quantizes to codes 0 with d = 0: the pad reads as exact zeros)
 
 // wave per token
 template <int V>
@@ -308,16 +314,22 @@ int rmsnorm(const float* x, int T, int n, float* u, hipStream_t stream) {
     return kOk;
 }
 
+// The prefill GEMM's activation pairs alone: rows of np (a multiple of 256, >= n) in perm256 order,
+// Q8_0 blocks of blk (32 or 64) values.
+int quantize_pairs(const float* x, int rows, int n, int np, int blk, _Float16* xhi, _Float16* xlo, hipStream_t stream) {
+    if (rows < 1 || n % 128 || np % 256 || np < n || (blk != 32 && blk != 64))
+        return set_error(kErrShape, "quantize_pairs: n=%d np=%d blk=%d", n, np, blk);
+    const int ns = rows * (np / 256);
+    launch_timed("pf_quant_x", k_quant_pairs, dim3((ns + 3) / 4), dim3(256), 0, stream, x, n, np, ns, blk, xhi, xlo);
+    FRT_LAUNCHED("quantize_pairs");
+    return kOk;
+}
+
 int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xhi, _Float16* xlo,
                 hipStream_t stream) {
     if (rows < 1 || n % 64) return set_error(kErrShape, "quantize_q8: n=%d not a multiple of 64", n);
     const int nb = rows * (n / kQ8);
-    if (xhi && xlo && !xq && !xd && n % 256 == 0) {   // the prefill GEMM's pairs alone
-        const int ns = rows * (n / 256);
-        launch_timed("pf_quant_x", k_quant_pairs, dim3((ns + 3) / 4), dim3(256), 0, stream, x, ns, xhi, xlo);
-        FRT_LAUNCHED("quantize_q8");
-        return kOk;
-    }
+    if (xhi && xlo && !xq && !xd && n % 256 == 0) return quantize_pairs(x, rows, n, n, 32, xhi, xlo, stream);
     const int waves = (nb + 1) / 2;
     launch_timed("pf_quant_x", k_quant_q8, dim3((waves + 3) / 4), dim3(256), 0, stream, x, nb, xq, xd, xhi, xlo, n);
     FRT_LAUNCHED("quantize_q8");

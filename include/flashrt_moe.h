@@ -114,9 +114,9 @@ int frt_moe_dispatch(void* stream, const int32_t* ids, int T, int K, int E, int3
 
 /* ---- prefill grouped expert GEMM (kernels/cuda/moe_q2.h:20-30 moe_q2::workspace_bytes, run).
  * yd [T*K][n]: slot t*K + k gets down(silu(gate x_t) * up x_t) of expert ids[t*K + k], expert e's
- * blob at experts + e * stride. yd_bf16 selects bf16 output. block64 (activations quantized per
- * 64) is not supported here: it returns FRT_ERR_SHAPE (activations use Q8_0 blocks of 32, the CPU
- * path's quantization). Shapes: n a multiple of 512, ff a multiple of 128 up to 1024 (FRT_ERR_SHAPE otherwise; the reference takes multiples of 128 for both). */
+ * blob at experts + e * stride. yd_bf16 selects bf16 output. block64: x and h are quantized in Q8
+ * blocks of 64 values instead of the CPU path's 32 (moe_q2.cu's AB = 64). Shapes: n and ff multiples
+ * of 128 (moe_q2.cu:516-517), ff at most 1024 (FRT_ERR_SHAPE otherwise). */
 size_t frt_moe_q2_workspace_bytes(int T, int K, int n, int ff, int E);
 int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const float* x, const int32_t* ids,
                    int T, int K, void* yd, void* ws, size_t ws_bytes, void* stream, int block64, int yd_bf16);

@@ -221,6 +221,23 @@ void orc_quantize_q8(const float* x, int n, int8_t* qs, float* d) {
     for (int i = 0; i < n / kQ8; ++i) quant_block(x + size_t(i) * kQ8, qs + size_t(i) * kQ8, d + i);
 }
 
+// Q8 in blocks of blk = 32 or 64 values: quant_block's rule over blk values (moe_q2's block64
+// activations, kernels/cuda/moe_q2.cu:58-81 with AB = 64; d fp16-rounded as the CPU path stores it).
+// The scales are stored one per 32 values (a 64-block's repeated), the layout matvec reads, so that
+// the per-block product d_w * d_a * sum over 64 is formed as two halves of 32 with the same d_a.
+void orc_quantize_q8_blk(const float* x, int n, int blk, int8_t* qs, float* d) {
+    if (blk != 64) return orc_quantize_q8(x, n, qs, d);
+    for (int i = 0; i < n / 64; ++i) {
+        const float* xb = x + size_t(i) * 64;
+        float amax = 0.0f;
+        for (int j = 0; j < 64; ++j) amax = std::max(amax, std::fabs(xb[j]));
+        const float dd = amax / 127.0f;
+        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+        d[2 * i] = d[2 * i + 1] = orc_f16_to_f32(orc_f32_to_f16(dd));
+        for (int j = 0; j < 64; ++j) qs[size_t(i) * 64 + j] = int8_t(std::roundf(xb[j] * id));
+    }
+}
+
 void orc_matvec(const uint8_t* w, int rows, int cols, const int8_t* qs, const float* d, int ntok, int r0, int r1,
                 float* y, int ldy, int order) {
     const MatV m = mat_view(w, rows, cols);
@@ -232,6 +249,12 @@ void orc_matvec(const uint8_t* w, int rows, int cols, const int8_t* qs, const fl
 // expert_ffn (q2_0.cpp:164-185): gate, up, SwiGLU, Q8 of h, down
 void orc_expert_ffn(const uint8_t* blob, int n, int ff, const int8_t* xq, const float* xd, int ntok, float* out, int ldo,
                     int order) {
+    orc_expert_ffn_blk(blob, n, ff, xq, xd, ntok, out, ldo, order, kQ8);
+}
+
+// expert_ffn with h quantized in blocks of hblk = 32 or 64 (orc_quantize_q8_blk)
+void orc_expert_ffn_blk(const uint8_t* blob, int n, int ff, const int8_t* xq, const float* xd, int ntok, float* out,
+                        int ldo, int order, int hblk) {
     const ExpertV e = expert_view(blob, n, ff);
     std::vector<Act> a(ntok), ha(ntok);
     for (int t = 0; t < ntok; ++t) a[t] = Act{xq + size_t(t) * n, xd + size_t(t) * (n / kQ8)};
@@ -244,7 +267,7 @@ void orc_expert_ffn(const uint8_t* blob, int n, int ff, const int8_t* xq, const 
         float* gt = g.data() + size_t(t) * ff;
         const float* ut = u.data() + size_t(t) * ff;
         for (int i = 0; i < ff; ++i) gt[i] = swiglu(gt[i], ut[i]);
-        orc_quantize_q8(gt, ff, hq.data() + size_t(t) * ff, hd.data() + size_t(t) * (ff / kQ8));
+        orc_quantize_q8_blk(gt, ff, hblk, hq.data() + size_t(t) * ff, hd.data() + size_t(t) * (ff / kQ8));
         ha[t] = Act{hq.data() + size_t(t) * ff, hd.data() + size_t(t) * (ff / kQ8)};
     }
     matvec(e.down, ha.data(), ntok, 0, n, out, ldo, order);

@@ -32,6 +32,7 @@ int orc_planar_code(const uint8_t* blk16, int j);
 /* ---- Q8_0 activations, 32 per block (q2_0.cpp:93-117) ---- */
 /* qs [n] int8; d [n/32] = fp16-rounded amax/127 as float */
 void orc_quantize_q8(const float* x, int n, int8_t* qs, float* d);
+void orc_quantize_q8_blk(const float* x, int n, int blk, int8_t* qs, float* d);
 
 /* ---- matvec: y[t*ldy + r] for r in [r0,r1), t < ntok.
  * w: planar matrix (codes then scales), rows x cols. qs/d: ntok activation vectors back to back.
@@ -43,6 +44,8 @@ void orc_matvec(const uint8_t* w, int rows, int cols, const int8_t* qs, const fl
 /* ---- one expert, SwiGLU (q2_0.cpp:164-185): out[t*ldo + r], ntok <= 4 */
 void orc_expert_ffn(const uint8_t* blob, int n, int ff, const int8_t* xq, const float* xd, int ntok, float* out, int ldo,
                     int order);
+void orc_expert_ffn_blk(const uint8_t* blob, int n, int ff, const int8_t* xq, const float* xd, int ntok, float* out,
+                        int ldo, int order, int hblk);
 
 /* ---- router logits in the canonical order shared with the HIP kernels:
  * for each (t,e): 64 chains, chain j = fmaf over k in [j*L, (j+1)*L) ascending (L = n/64) from 0,

@@ -57,6 +57,8 @@ def lib():
         L.orc_quantize_q8.argtypes = [_f32p, C.c_int, _i8p, _f32p]
         L.orc_matvec.argtypes = [_u8p, C.c_int, C.c_int, _i8p, _f32p, C.c_int, C.c_int, C.c_int, _f32p, C.c_int, C.c_int]
         L.orc_expert_ffn.argtypes = [_u8p, C.c_int, C.c_int, _i8p, _f32p, C.c_int, _f32p, C.c_int, C.c_int]
+        L.orc_expert_ffn_blk.argtypes = [_u8p, C.c_int, C.c_int, _i8p, _f32p, C.c_int, _f32p, C.c_int, C.c_int, C.c_int]
+        L.orc_quantize_q8_blk.argtypes = [_f32p, C.c_int, C.c_int, _i8p, _f32p]
         L.orc_router_logits.argtypes = [_f32p, C.c_int, _f32p, C.c_void_p, C.c_int, C.c_int, _f32p]
         L.orc_dot_canon.restype = C.c_float
         L.orc_dot_canon.argtypes = [_f32p, _f32p, C.c_int]
@@ -139,11 +141,15 @@ def gen_zipf_bias(cfg: int, layer: int, E: int, s: float, alpha: float = 1.0, se
     return out
 
 
-def quantize_q8(x: np.ndarray):
+def quantize_q8(x: np.ndarray, blk: int = 32):
+    """Q8 codes and scales (one per 32 values; a 64-block's scale repeated when blk = 64)."""
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
     qs = np.zeros(x.size, np.int8)
     d = np.zeros(x.size // 32, np.float32)
-    lib().orc_quantize_q8(x, x.size, qs, d)
+    if blk == 32:
+        lib().orc_quantize_q8(x, x.size, qs, d)
+    else:
+        lib().orc_quantize_q8_blk(x, x.size, blk, qs, d)
     return qs, d
 
 
@@ -157,14 +163,15 @@ def matvec(w: np.ndarray, rows: int, cols: int, x: np.ndarray, order: int = 0, r
     return y
 
 
-def expert_ffn(blob: np.ndarray, n: int, ff: int, x: np.ndarray, order: int = 0) -> np.ndarray:
+def expert_ffn(blob: np.ndarray, n: int, ff: int, x: np.ndarray, order: int = 0, blk: int = 32) -> np.ndarray:
+    """blk = 64: x and h in Q8 blocks of 64 (moe_q2::run's block64)."""
     x = np.ascontiguousarray(x, np.float32).reshape(-1, n)
     out = np.zeros_like(x)
     for t0 in range(0, x.shape[0], 4):
         xs = np.ascontiguousarray(x[t0:t0 + 4])
-        qs, d = quantize_q8(xs)
+        qs, d = quantize_q8(xs, blk)
         o = np.zeros_like(xs)
-        lib().orc_expert_ffn(blob, n, ff, qs, d, xs.shape[0], o, n, order)
+        lib().orc_expert_ffn_blk(blob, n, ff, qs, d, xs.shape[0], o, n, order, blk)
         out[t0:t0 + 4] = o
     return out
 

@@ -362,19 +362,49 @@ def test_moe_q2_run(F, w0, yd_bf16):
     with pytest.raises(F.FrtError) as e:
         F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, 4096)
     assert e.value.code == -2
-    with pytest.raises(F.FrtError):
-        F.moe_q2.run(w0.arena.data_ptr(), w0.stride, E, H.N, H.FF, dev(x), dev(ids), T, K, yd, ws, nb, None, True)
+
+
+@pytest.mark.parametrize("n,ff,T,K,E", [(2048, 512, 96, 10, 24), (640, 384, 40, 3, 5)])
+def test_moe_q2_run_block64(F, n, ff, T, K, E):
+    """moe_q2::run(block64 = true): x and h quantized in Q8 blocks of 64 (kernels/cuda/moe_q2.cu:58-81,
+    AB = 64); every sampled slot against the oracle's expert_ffn with blk = 64. The block size changes
+    the result (checked), so a kernel that ignored the flag would fail."""
+    w = H.World(cfg=0, n=n, ff=ff, E=E, K=K)
+    rng = np.random.default_rng(640 + n)
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    ids = np.stack([rng.choice(E, size=K, replace=False) for _ in range(T)]).astype(np.int32)
+    nb = F.moe_q2.workspace_bytes(T, K, n, ff, E)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    yd = torch.full((T * K, n), float("nan"), dtype=torch.float32, device="cuda")
+    F.moe_q2.run(w.arena.data_ptr(), w.stride, E, n, ff, dev(x), dev(ids), T, K, yd, ws, nb, None, True)
+    torch.cuda.synchronize()
+    y = yd.cpu().numpy().reshape(T, K, n)
+    worst = 0.0
+    for t in range(0, T, 3):
+        for k in range(K):
+            blob = w.blob(int(ids[t, k]))
+            ref = O.expert_ffn(blob, n, ff, x[t], blk=64)
+            err = H.out_rel(y[t, k][None], ref)
+            worst = max(worst, err)
+            assert err <= H.OUT_REL, (t, k, err)
+    print(f"block64 n={n} ff={ff}: max out rel err {worst:.2e}")
+    ref32 = O.expert_ffn(w.blob(int(ids[0, 0])), n, ff, x[0])
+    assert H.out_rel(y[0, 0][None], ref32) > 0.0
 
 
 @pytest.mark.parametrize("n,ff,T,K,E", [(1024, 1024, 40, 4, 6), (2048, 512, 8, 2, 8), (1024, 512, 200, 3, 4),
-                                         (2560, 640, 90, 4, 6), (512, 128, 70, 2, 3), (1536, 384, 50, 3, 5)])
+                                         (2560, 640, 90, 4, 6), (512, 128, 70, 2, 3), (1536, 384, 50, 3, 5),
+                                         (640, 384, 60, 3, 5), (896, 256, 40, 2, 4), (128, 128, 30, 2, 3),
+                                         (1152, 640, 20, 4, 6)])
 def test_moe_q2_run_shapes(F, n, ff, T, K, E):
     """moe_q2::run at other shapes and tile mixes, every slot against the oracle's expert_ffn:
     ff = 1024 (four weight stretches per down row block, a 128 KB tile in LDS) with n = 1024 and about
     27 rows per expert (two-column tiles); only one-column tiles (T = 8, K = 2 over 8 experts); full
     64-row tiles next to partial ones (T = 200, K = 3 over 4 experts); ff not a multiple of 256 (the
     h rows padded to whole stretches: 640 = the reference tests' 2560 / 640 shape, with a stretch
-    count that is not a multiple of 4; 128; 384) and n = 512 and 1536."""
+    count that is not a multiple of 4; 128; 384) and n = 512 and 1536; n a multiple of 128 but not of 512
+    (moe_q2.cu:516-517 accepts those: 640, 896, 128, 1152; the activations are padded with zeros to
+    a multiple of 512 and the down GEMM's last row block is partial)."""
     w = H.World(cfg=0, n=n, ff=ff, E=E, K=K)
     rng = np.random.default_rng(n + ff + T)
     x = rng.standard_normal((T, n)).astype(np.float32)
@@ -393,14 +423,13 @@ def test_moe_q2_run_shapes(F, n, ff, T, K, E):
 
 
 def test_moe_q2_run_shape_errors(F, w0):
-    """The grouped GEMMs' shape limits (n a multiple of 512; ff a multiple of 128 up to 1024) fail
-    loudly."""
+    """The grouped GEMMs' shape limits (n and ff multiples of 128, ff up to 1024) fail loudly."""
     T, K = 4, 2
     x = torch.zeros((T, 2048), dtype=torch.float32, device="cuda")
     ids = torch.zeros((T, K), dtype=torch.int32, device="cuda")
     ids[:, 1] = 1
     yd = torch.empty((T * K, 2048), dtype=torch.float32, device="cuda")
-    for n, ff in ((2048, 704), (1280, 512), (2048, 1152), (256, 512)):
+    for n, ff in ((2048, 704), (1000, 512), (2048, 1152), (64, 512)):
         nb = F.moe_q2.workspace_bytes(T, K, n, ff, 8)
         ws = torch.empty(max(nb, 1 << 20), dtype=torch.uint8, device="cuda")
         with pytest.raises(F.FrtError) as e:

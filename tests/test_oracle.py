@@ -201,6 +201,71 @@ def test_expert_ffn_vs_float_swiglu():
         assert np.linalg.norm(y - want) / np.linalg.norm(want) < 0.05
 
 
+# ---------------------------------------------------------------- block64 (moe_q2::run's AB = 64)
+
+def q8_closed_form_blk(x: np.ndarray, blk: int):
+    """q8_closed_form over blocks of blk values; scales returned one per 32 values."""
+    xb = x.reshape(-1, blk).astype(np.float32)
+    amax = np.abs(xb).max(axis=1)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, 1), 0).astype(np.float32)
+    v = (xb * idv[:, None]).astype(np.float32)
+    q = np.sign(v) * np.floor(np.abs(v) + np.float32(0.5))
+    return q.astype(np.int8).reshape(x.shape), np.repeat(d.astype(np.float16).astype(np.float32), blk // 32)
+
+
+def test_quantize_q8_block64_closed_form():
+    """Blocks of 64: one amax, d and id for all 64 values (kernels/cuda/moe_q2.cu:58-81 with AB = 64);
+    the scale appears once per 32-value half. blk = 32 is quantize_q8 itself."""
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(64 * 40) * rng.uniform(0.1, 5, 64 * 40)).astype(np.float32)
+    x[64:128] = 0.0                     # a zero block
+    x[128:160] = 0.0                    # a block whose first half is zero (d from the second half)
+    qs, d = O.quantize_q8(x, 64)
+    cq, cd = q8_closed_form_blk(x, 64)
+    assert np.array_equal(qs, cq) and np.array_equal(d, cd)
+    assert (qs[128:160] == 0).all() and d[4] == d[5] != 0
+    q32, d32 = O.quantize_q8(x, 32)
+    c32q, c32d = q8_closed_form(x)
+    assert np.array_equal(q32, c32q) and np.array_equal(d32, c32d)
+    # a 64-block whose two halves share their amax quantizes exactly as two 32-blocks
+    y = rng.standard_normal(64 * 8).astype(np.float32)
+    y[::32] = 4.0
+    assert np.array_equal(O.quantize_q8(y, 64)[0], O.quantize_q8(y, 32)[0])
+    assert np.array_equal(O.quantize_q8(y, 64)[1], O.quantize_q8(y, 32)[1])
+
+
+def test_expert_ffn_block64_composition():
+    """expert_ffn with blk = 64 is gate/up matvecs on the 64-block Q8 of x, fp32 SwiGLU, the 64-block
+    Q8 of h and the down matvec (composed here from the oracle's matvec on the codes); and against
+    fp32 SwiGLU on dequantized weights it stays within the reference test's 0.05 (tests/test_q2_0.cpp:156-181)."""
+    n, ff = 640, 384
+    blob = O.gen_expert(98, 0, 2, n, ff)
+    mb = O.lib().orc_mat_bytes(ff, n)
+    x = np.random.default_rng(6).standard_normal((3, n)).astype(np.float32)
+    y = O.expert_ffn(blob, n, ff, x, 0, blk=64)
+
+    def mv(w, rows, cols, qs, d):
+        out = np.zeros((qs.size // cols, rows), np.float32)
+        O.lib().orc_matvec(w, rows, cols, qs, d, qs.size // cols, 0, rows, out, rows, 0)
+        return out
+    qs, d = O.quantize_q8(x, 64)
+    g = mv(blob[:mb], ff, n, qs, d)
+    u = mv(blob[mb:2 * mb], ff, n, qs, d)
+    h = (g / (np.float32(1) + np.exp(-g)) * u).astype(np.float32)
+    hq, hd = O.quantize_q8(h, 64)
+    want = mv(blob[2 * mb:3 * mb], n, ff, hq, hd)
+    assert np.max(np.abs(y - want)) <= 1e-4 * np.max(np.abs(want))   # exp in numpy vs libm: rare code flips
+    G = dequant_planar(blob[:mb], ff, n)
+    U = dequant_planar(blob[mb:2 * mb], ff, n)
+    D = dequant_planar(blob[2 * mb:3 * mb], n, ff)
+    gg, uu = x @ G.T, x @ U.T
+    ref = (gg / (1 + np.exp(-gg)) * uu) @ D.T
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 0.05
+    assert not np.array_equal(y, O.expert_ffn(blob, n, ff, x, 0, blk=32))   # the block size matters
+
+
 # ---------------------------------------------------------------- moe_cpu
 
 @pytest.mark.parametrize("tag", ["small", "cfg"])
