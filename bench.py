@@ -296,9 +296,18 @@ def run_windows(args, F, torch, st):
         idh = ids.cpu().numpy()
         distinct = float(np.mean([len(np.unique(idh[l])) for l in range(layers)]))
         need = (distinct + 1) * eb + E * N * 4 + N * 4
-        path = "decode" if T * K <= 63 and T <= 4 else "prefill"
+        # T <= 4: the grouped decode kernels; 5 .. 8: router + top-k + one moe_hits launch + combine
+        path = "decode" if T * K <= 63 and T <= 4 else ("window" if T <= 8 else "prefill")
         res[f"T{T}"] = dict(us_per_call=round(us, 2), tokens_per_s=round(T / us * 1e6, 1), path=path,
                             distinct_experts=round(distinct, 2), GBps=round(need / (us * 1e-6) / 1e9, 1))
+        if T > 1:   # per-kernel averages over an eager pass of the 48 calls, queued behind a spin kernel
+            def eager():
+                with torch.cuda.stream(stream):
+                    torch.cuda._sleep(SPIN_CYCLES)
+                    body()
+            kt = kernel_times(F, eager)
+            stream.synchronize()
+            res[f"T{T}"]["kernels_us"] = {k: round(v[0] * 1e3 / max(v[1], 1), 2) for k, v in kt.items()}
         del g
         log(f"window T={T}: {us:.2f} us/call ({path}), {distinct:.2f} distinct experts")
     return res

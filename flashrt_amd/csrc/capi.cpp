@@ -73,6 +73,7 @@ int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16
                 hipStream_t stream);
 int route_topk(hipStream_t stream, const float* logits, int T, int E, int K, int32_t* ids, float* wts, uint32_t* counts,
                uint32_t* tail_counts, int tail_from);
+bool router_fused_fits(int T, int n);
 // decode.hip
 size_t dec_scratch_bytes(int T, int K, int ff);
 int dec_moe(const float* logits, const float* gate, int T, int E, int K, const uint8_t* arena, size_t stride,
@@ -82,6 +83,11 @@ int dec_moe(const float* logits, const float* gate, int T, int E, int K, const u
 int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const int8_t* xq, const float* xd, int n,
              int ff, void* scratch, float* yh, hipStream_t stream, int T);
 int dec_check(int T, int K, int n, int ff);
+size_t dec_window_bytes(int T, int K, int n, int ff);
+int dec_window_fits(int T, int K, int ff);
+int dec_window(const int32_t* ids, const float* wts, const float* gate, int T, int K, const uint8_t* arena,
+               size_t stride, const uint8_t* shared_blob, const int8_t* xq, const float* xd, int n, int ff,
+               const float* resid, float* out, void* scratch, hipStream_t stream);
 // decode1.hip
 size_t dec1_sync_bytes();
 int dec1_eligible(int E, int K, int n, int ff);
@@ -122,16 +128,18 @@ void gen_zipf_bias(uint64_t seed, int cfg, int layer, int E, float s, float alph
 
 constexpr int kDecodeMaxT = 4;
 
-// moe_hits runs a window in chunks of at most hits_chunk(T, K) tokens (the grouped decode kernels
-// take T <= 4 and T * K <= 63); each chunk reads each of its distinct blobs once
-static int hits_chunk(int T, int K) {
-    int c = 63 / (K > 0 ? K : 1);
-    if (c > kDecodeMaxT) c = kDecodeMaxT;
+// moe_hits runs a window in launches of at most hits_chunk(T, K, ff) tokens: 8 (the reference's
+// kMaxWindow) as long as the launch has at most 128 (token, slot) items and its hidden vectors fit in
+// 96 KB of LDS (K <= 12 at ff = 512); each launch reads each of its distinct blobs once per four tokens
+static int hits_chunk(int T, int K, int ff) {
+    int c = 8;
+    const int k = K > 0 ? K : 1;
+    while (c > 1 && (c * k > 128 || size_t(c) * (k + 1) * (size_t(ff) + (ff / kQ8) * 4 + 32) > 96 * 1024)) --c;
     return T < c ? T : c;
 }
 // decode-side scratch for moe_hits: x quantized (T rows) ahead of the dec scratch of one chunk
 static size_t hits_bytes(int K, int ff, int T, int n) {
-    return up256(size_t(T) * n) + up256(size_t(T) * (n / kQ8) * 4) + dec_scratch_bytes(hits_chunk(T, K), K, ff);
+    return up256(size_t(T) * n) + up256(size_t(T) * (n / kQ8) * 4) + dec_scratch_bytes(hits_chunk(T, K, ff), K, ff);
 }
 
 struct LayerWs {
@@ -149,6 +157,15 @@ struct LayerWs {
     size_t bytes;
 };
 
+// A verify window of 5 .. 8 tokens (the reference's kMaxWindow) goes through the decode GEMV kernels
+// (router + fused Q8_0, top-k, one moe_hits launch, combine) when it fits one hits launch and the
+// router's fused quantization; larger windows take the prefill path.
+static bool window_path(const frt_moe_layer& L, int T) {
+    const int K = L.top_k, n = L.d_model;
+    if (T <= kDecodeMaxT && T * K <= 63) return false;   // the grouped decode path
+    return T <= 8 && dec_window_fits(T, K, L.d_ff) && router_fused_fits(T, n) && dec_check(1, K, n, L.d_ff) == kOk;
+}
+
 static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t total) {
     LayerWs w{};
     uint8_t* p = static_cast<uint8_t*>(base);
@@ -164,10 +181,10 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
     w.ids = reinterpret_cast<int32_t*>(take(size_t(T) * K * 4));
     w.wts = reinterpret_cast<float*>(take(size_t(T) * K * 4));
     const bool dec = T <= kDecodeMaxT && T * K <= 63;
-    if (dec) {
+    if (dec || window_path(L, T)) {
         w.xq = reinterpret_cast<int8_t*>(take(size_t(T) * n));
         w.xd = reinterpret_cast<float*>(take(size_t(T) * (n / kQ8) * 4));
-        w.rest_bytes = dec_scratch_bytes(T, K, ff);
+        w.rest_bytes = dec ? dec_scratch_bytes(T, K, ff) : dec_window_bytes(T, K, n, ff);
     } else {
         if (L.flags & FRT_LAYER_NORM_INPUT) w.u = reinterpret_cast<float*>(take(size_t(T) * n * 4));
         w.part = reinterpret_cast<float*>(take(router_gemm_ws_bytes(T, E, true)));
@@ -334,8 +351,8 @@ int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, con
                  void* scratch, float* yh, void* stream, int T) {
     if (!hit_ptr || !hit_n || !x || !scratch || !yh) return set_error(kErrNull, "moe_hits: null pointer");
     if (T < 1 || K < 1 || K > 32) return set_error(kErrShape, "moe_hits: T=%d K=%d", T, K);
-    const int tc = hits_chunk(T, K);
-    if (int rc = dec_check(tc, K, n, ff)) return rc;
+    const int tc = hits_chunk(T, K, ff);
+    if (int rc = dec_check(1, K, n, ff)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint8_t* p = static_cast<uint8_t*>(scratch);
     int8_t* xq = reinterpret_cast<int8_t*>(p);
@@ -384,6 +401,16 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
         timing_mark(s, "router_quant");
         return dec_moe(w.logits, w.gate, T, E, K, L->experts, L->stride, L->shared, w.xq, w.xd, n, ff, ids_o, wts_o,
                        counts, resid, out, w.rest, s, L->next_router_w);
+    }
+    if (window_path(*L, T)) {
+        if (int rc = router_logits(x, T, L->router_w, L->router_bias, L->gate_w, E, n, w.logits, w.gate, s, norm, w.xq,
+                                   w.xd))
+            return rc;
+        timing_mark(s, "router_quant");
+        if (int rc = route_topk(s, w.logits, T, E, K, ids_o, wts_o, counts, nullptr, 1 << 30)) return rc;
+        timing_mark(s, "route_topk");
+        return dec_window(ids_o, wts_o, w.gate, T, K, L->experts, L->stride, L->shared, w.xq, w.xd, n, ff, resid, out,
+                          w.rest, s);
     }
     if (int rc = pf_check(T, K, n, ff, E)) return rc;
     const float* xin = x;

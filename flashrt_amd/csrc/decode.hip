@@ -30,40 +30,73 @@ namespace frt {
 namespace {
 
 // ---- moe_hits grouping (moe_fast.cu:195-232): distinct blob pointers across the window's hit
-// lists, in order of first appearance; no shared expert.
-__global__ void k_hits_group(const uint8_t* const* __restrict__ hit_ptr, const int32_t* __restrict__ hit_n, int K, int T,
-                             DecEntry* __restrict__ ent, int32_t* __restrict__ n_ent) {
-    if (threadIdx.x != 0) return;
-    int U = 0, b = 0;
-    for (int t = 0; t < T; ++t) {
-        const int h = min(hit_n[t], K);
-        for (int k = 0; k < h; ++k) {
-            const uint8_t* p = hit_ptr[t * K + k];
-            int u = 0;
-            while (u < U && (ent[u].blob != p || ent[u].ntok == kDecMaxT)) ++u;   // a full entry: the repeat opens another
-            if (u == U) {
-                DecEntry d{};
-                d.blob = p;
-                d.ntok = 0;
-                for (int j = 0; j < 4; ++j) {
-                    d.tok[j] = 0;
-                    d.slot[j] = -1;
-                    d.w[j] = 0.0f;
-                }
-                ent[U++] = d;
+// lists, in order of first appearance; no shared expert. An entry holds at most kDecMaxT tokens: the
+// occurrences of a pointer beyond its entry's four slots open another entry at their place in that
+// order (a pointer met five times in the window is read twice, once per entry).
+// One workgroup, one thread per item i = t K + k (items k >= hit_n[t] take no part): the item's
+// occurrence index j among the items of its pointer decides its entry (the one opened by the
+// pointer's occurrence 4 floor(j / 4)) and its slot in it (j mod 4). Entries in the order of the
+// items that open them, so the list is what a serial pass over the items would build.
+constexpr int kHitsMaxItems = 128;
+__global__ void __launch_bounds__(kHitsMaxItems) k_hits_group(const uint8_t* const* __restrict__ hit_ptr,
+                                                              const int32_t* __restrict__ hit_n, int K, int T,
+                                                              DecEntry* __restrict__ ent, int32_t* __restrict__ n_ent) {
+    __shared__ const uint8_t* sp[kHitsMaxItems];
+    __shared__ int sj[kHitsMaxItems], sopen[kHitsMaxItems], sent[kHitsMaxItems], stot[kHitsMaxItems];
+    __shared__ int sntok[kHitsMaxItems], sbase[kHitsMaxItems + 1];
+    const int i = int(threadIdx.x), N = T * K;
+    const int t = i / K, k = i % K;
+    const bool live = i < N && k < min(hit_n[min(t, T - 1)], K);
+    sp[i] = live ? hit_ptr[i] : nullptr;
+    __syncthreads();
+    int j = 0, tot = 0;
+    if (live)
+        for (int q = 0; q < N; ++q) {
+            const bool same = sp[q] == sp[i];
+            j += int(same && q < i);
+            tot += int(same);
+        }
+    const bool opens = live && j % kDecMaxT == 0;
+    sj[i] = j;
+    stot[i] = tot;
+    sopen[i] = int(opens);
+    __syncthreads();
+    if (i == 0) {   // entry index of each opener and the entries' compact bases, in item order
+        int u = 0, b = 0;
+        for (int q = 0; q < N; ++q)
+            if (sopen[q]) {
+                const int nt = min(kDecMaxT, stot[q] - sj[q]);
+                sent[q] = u;
+                sntok[u] = nt;
+                sbase[u] = b;
+                b += nt;
+                ++u;
             }
-            DecEntry& d = ent[u];
-            d.tok[d.ntok] = t;
-            d.slot[d.ntok] = k;
-            d.w[d.ntok] = 1.0f;
-            ++d.ntok;
+        *n_ent = u;
+    }
+    __syncthreads();
+    if (!live) return;
+    int opener = i;   // the item of this pointer with occurrence index 4 floor(j / 4)
+    for (int q = 0; q <= i; ++q)
+        if (sp[q] == sp[i] && sj[q] == j - j % kDecMaxT) {
+            opener = q;
+            break;
+        }
+    const int u = sent[opener], s = j % kDecMaxT;
+    DecEntry& d = ent[u];
+    if (opens) {
+        d.blob = sp[i];
+        d.ntok = sntok[u];
+        d.base = sbase[u];
+        for (int q = sntok[u]; q < kDecMaxT; ++q) {   // the unused slots
+            d.tok[q] = 0;
+            d.slot[q] = -1;
+            d.w[q] = 0.0f;
         }
     }
-    for (int u = 0; u < U; ++u) {
-        ent[u].base = b;
-        b += ent[u].ntok;
-    }
-    *n_ent = U;
+    d.tok[s] = t;
+    d.slot[s] = k;
+    d.w[s] = 1.0f;
 }
 
 // ---- gate + up for 32 ff rows of one entry by NW waves (32 / NW rows each). NB = n / 64 blocks
@@ -386,7 +419,7 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent_g, const i
                                                   int S_max, const float* __restrict__ pf, int pf_rows) {
     constexpr int RD = 8;   // rows per workgroup
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ DecEntry s_ent[64];
+    __shared__ DecEntry s_ent[kDecMaxEnt];
     __shared__ DecComb s_comb;
     // every global load is issued before the first wait: the residual this thread adds in the
     // combine, the entry count, the LDS staging of the entry list and the quantized hidden vectors,
@@ -473,6 +506,61 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent_g, const i
 }
 
 
+// ---- a verify window of 5 .. 8 tokens through the moe_hits kernels (moe_block_fast's window path,
+// arch/qwen4exp/moe_fast.cu:1015-1108 with T <= kMaxWindow): token t's hit list is its K routed
+// experts' blobs (rank order) and the shared expert's as slot K.
+__global__ void k_win_hits(const int32_t* __restrict__ ids, int T, int K, const uint8_t* __restrict__ arena,
+                           size_t stride, const uint8_t* __restrict__ shared_blob, const uint8_t** __restrict__ hit_ptr,
+                           int32_t* __restrict__ hit_n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < T * (K + 1)) {
+        const int t = i / (K + 1), k = i % (K + 1);
+        hit_ptr[i] = k < K ? arena + size_t(ids[t * K + k]) * stride : shared_blob;
+        if (k == 0) hit_n[t] = K + 1;
+    }
+}
+// out[t] = resid[t] + (sum over the K routed slots in ascending expert id of w * y, from 0) + y_shared *
+// sigmoid(gate[t]) (moe_cpu.cpp:63-80 phase B order; moe_ref.cu:90-97); yh [T][K + 1][n]
+__global__ void __launch_bounds__(256) k_win_combine(const float* __restrict__ yh, const int32_t* __restrict__ ids,
+                                                     const float* __restrict__ wts, const float* __restrict__ gate, int T,
+                                                     int K, int n, const float* __restrict__ resid,
+                                                     float* __restrict__ out) {
+    __shared__ int order[32];
+    const int t = blockIdx.y;
+    if (int(threadIdx.x) < K) {   // rank of slot k by expert id (one token's ids are distinct)
+        const int e = ids[t * K + threadIdx.x];
+        int r = 0;
+        for (int k = 0; k < K; ++k) r += ids[t * K + k] < e ? 1 : 0;
+        order[r] = threadIdx.x;
+    }
+    __syncthreads();
+    const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= n) return;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int r = 0; r < K; ++r) {
+        const int k = order[r];
+        const float w = wts[t * K + k];
+        const float4 y = *reinterpret_cast<const float4*>(yh + (size_t(t) * (K + 1) + k) * n + i);
+        const float yv[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float p = w * yv[q];
+            acc[q] = acc[q] + p;
+        }
+    }
+    const float g = sigmoidf_(gate[t]);
+    const float4 ys = *reinterpret_cast<const float4*>(yh + (size_t(t) * (K + 1) + K) * n + i);
+    const float sv[4] = {ys.x, ys.y, ys.z, ys.w};
+    float o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float p = sv[q] * g;
+        o[q] = acc[q] + p;
+        if (resid) o[q] = resid[size_t(t) * n + i + q] + o[q];
+    }
+    *reinterpret_cast<float4*>(out + size_t(t) * n + i) = make_float4(o[0], o[1], o[2], o[3]);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- host side
@@ -513,7 +601,7 @@ static int dec_down(const DecScratch& s, int n, int ff, int T, int K, const floa
                     hipStream_t stream, const float* pf = nullptr, int pf_rows = 0) {
     const int nbf = ff / kBlock;
     const int S = T * (K + 1);                         // compact slots at most (the shared expert's included)
-    const int U_max = T * K + 1 < 64 ? T * K + 1 : 64;   // entries at most
+    const int U_max = T * K + 1 < kDecMaxEnt ? T * K + 1 : kDecMaxEnt;   // entries at most
     const size_t smem = size_t(S) * ff + size_t(S) * (ff / kQ8) * 4 + size_t(S) * 8 * 4;
 #define FRT_DN(NBFV)                                                                                           \
     case NBFV:                                                                                                 \
@@ -584,12 +672,18 @@ int dec_moe(const float* logits, const float* gate, int T, int E, int K, const u
     return dec_down(s, n, ff, T, K, resid, out, nullptr, stream, prefetch, E);
 }
 
-// moe_hits (arch/qwen4exp/moe_fast.hpp:134-142): per-slot expert outputs for the window's hit lists.
+// moe_hits (arch/qwen4exp/moe_fast.hpp:134-142): per-slot expert outputs for the window's hit lists,
+// one launch per window of up to kDecMaxHitsT tokens (the reference's kMaxWindow, moe_fast.cu:38),
+// each distinct expert's rows read once per four of its tokens.
 int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const int8_t* xq, const float* xd, int n,
              int ff, void* scratch, float* yh, hipStream_t stream, int T) {
-    if (int rc = dec_check(T, K, n, ff)) return rc;
+    if (T < 1 || T > kDecMaxHitsT || K < 1 || K > 32 || T * K > kHitsMaxItems)
+        return set_error(kErrShape, "moe_hits: T=%d K=%d (T <= %d, T*K <= %d per launch)", T, K, kDecMaxHitsT, kHitsMaxItems);
+    if (int rc = dec_check(1, K, n, ff)) return rc;
+    const size_t smem = size_t(T * (K + 1)) * (ff + (ff / kQ8) * 4 + 8 * 4);
+    if (smem > 96 * 1024) return set_error(kErrShape, "moe_hits: T=%d K=%d ff=%d needs %zu B of LDS", T, K, ff, smem);
     const DecScratch s = dec_carve(scratch, T, K, ff);
-    k_hits_group<<<1, 64, 0, stream>>>(hit_ptr, hit_n, K, T, s.ent, s.n_ent);
+    k_hits_group<<<1, kHitsMaxItems, 0, stream>>>(hit_ptr, hit_n, K, T, s.ent, s.n_ent);
     timing_mark(stream, "hits_group");
     const int nb = n / kBlock;
     dim3 g1(ff / 32, T * K);
@@ -604,5 +698,34 @@ int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const i
     return dec_down(s, n, ff, T, K, nullptr, nullptr, yh, stream);
 }
 
-}  // namespace frt
+// A verify window (T <= 8) after routing: ids / wts [T][K], gate [T], the window's Q8_0 input ->
+// out [T][n] (+ resid). One moe_hits launch reads each distinct expert once per four of its tokens
+// (arch/qwen4exp/moe_fast.cu:195-355); then the combine. Scratch: dec_window_bytes.
+size_t dec_window_bytes(int T, int K, int n, int ff) {
+    return up256(size_t(T) * (K + 1) * 8) + 256 + up256(size_t(T) * (K + 1) * n * 4) + dec_scratch_bytes(T, K + 1, ff);
+}
+int dec_window_fits(int T, int K, int ff) {
+    return T >= 1 && T <= kDecMaxHitsT && T * (K + 1) <= kHitsMaxItems &&
+           size_t(T) * (K + 2) * (size_t(ff) + (ff / kQ8) * 4 + 32) <= 96 * 1024;
+}
+int dec_window(const int32_t* ids, const float* wts, const float* gate, int T, int K, const uint8_t* arena,
+               size_t stride, const uint8_t* shared_blob, const int8_t* xq, const float* xd, int n, int ff,
+               const float* resid, float* out, void* scratch, hipStream_t stream) {
+    if (!dec_window_fits(T, K, ff)) return set_error(kErrShape, "decode window: T=%d K=%d ff=%d", T, K, ff);
+    uint8_t* p = static_cast<uint8_t*>(scratch);
+    const uint8_t** hit_ptr = reinterpret_cast<const uint8_t**>(p);
+    p += up256(size_t(T) * (K + 1) * 8);
+    int32_t* hit_n = reinterpret_cast<int32_t*>(p);
+    p += 256;
+    float* yh = reinterpret_cast<float*>(p);
+    p += up256(size_t(T) * (K + 1) * n * 4);
+    k_win_hits<<<(T * (K + 1) + 63) / 64, 64, 0, stream>>>(ids, T, K, arena, stride, shared_blob, hit_ptr, hit_n);
+    FRT_LAUNCHED("decode window hits");
+    if (int rc = dec_hits(hit_ptr, hit_n, K + 1, xq, xd, n, ff, p, yh, stream, T)) return rc;
+    launch_timed("win_combine", k_win_combine, dim3((n + 1023) / 1024, T), dim3(256), 0, stream, (const float*)yh, ids,
+                 wts, gate, T, K, n, resid, out);
+    FRT_LAUNCHED("decode window combine");
+    return kOk;
+}
 
+}  // namespace frt

@@ -18,7 +18,9 @@ struct DecEntry {
 };
 static_assert(sizeof(DecEntry) == 64, "DecEntry layout");
 
-constexpr int kDecMaxT = 4;
+constexpr int kDecMaxT = 4;        // tokens per entry, and per routed decode window
+constexpr int kDecMaxHitsT = 8;    // tokens per moe_hits launch (the reference's kMaxWindow)
+constexpr int kDecMaxEnt = 128;    // entries per launch
 
 namespace {
 

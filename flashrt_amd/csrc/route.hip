@@ -263,6 +263,15 @@ __global__ void __launch_bounds__(64) k_layer_trace(const float* __restrict__ lg
 
 // ---------------------------------------------------------------- host entry points
 
+static int router_tile_tokens(int L) { return int(98304 / (size_t(64) * (L + 1) * 4)); }
+// Whether router_logits can quantize the input of T tokens in the same launch (one token tile).
+bool router_fused_fits(int T, int n) {
+    if (n % 64 || n < 512 || n > 64 * 64 || (n / 64) % 8) return false;
+    int TT = router_tile_tokens(n / 64);
+    if (TT > 16) TT = 16;
+    return T <= TT;
+}
+
 int router_logits(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
                   float* logits, float* gate, hipStream_t stream, int norm, int8_t* xq, float* xd) {
     if (T < 1 || E < 1 || E > kMaxE || n % 64 || n < 64 || n > 64 * 64) return set_error(kErrShape, "router: shape T=%d E=%d n=%d", T, E, n);
@@ -270,8 +279,8 @@ int router_logits(const float* x, int T, const float* W, const float* bias, cons
     const int L = n / 64;
     const int rows = E + (gate_w ? 1 : 0);
     if (xq && T > 16) return set_error(kErrShape, "router: fused quantization is for T <= 16");
-    // token tile: the LDS tile stays within 64 KB, but always holds a decode window (4 tokens)
-    int TT = int(65536 / (size_t(64) * (L + 1) * 4));
+    // token tile: the LDS tile stays within 96 KB, but always holds a decode window (4 tokens)
+    int TT = router_tile_tokens(L);
     if (TT > 16) TT = 16;
     if (TT < 4) TT = 4;
     if (T < TT) TT = T;

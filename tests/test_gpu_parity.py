@@ -242,6 +242,33 @@ def test_layer_decode_config1_window(F):
         assert np.array_equal(o1[0], out[t])
 
 
+@pytest.mark.parametrize("T", [5, 8])
+def test_layer_verify_window(F, T):
+    """Verify windows of 5 and 8 tokens (the reference's kMaxWindow = 8, moe_fast.cu:38; correlated
+    tokens as in config 1) through the decode GEMV path (router with fused Q8_0, top-k, one moe_hits
+    launch over every token's routed experts and the shared expert, combine): ids bit-exact, weights
+    and outputs against the oracle; each token alone (the single-token path) gives the same ids and
+    outputs within the output bar; a window with a residual adds it exactly."""
+    w1 = H.World(cfg=1)
+    xc = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    F.gen.correlated(xc, 1, T, O.X_TENSOR, T, H.N, 0.8)
+    x = xc.cpu().numpy()
+    out, ids, wts = w1.gpu_forward(x)
+    ref, rid, rw, _ = w1.oracle_forward(x)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    err = H.out_rel(out, ref)
+    print(f"verify window T={T}: out rel err {err:.2e}, {len(set(ids.reshape(-1).tolist()))} distinct experts")
+    assert err <= H.OUT_REL
+    for t in (0, T - 1):
+        o1, i1, _ = w1.gpu_forward(x[t:t + 1])
+        assert np.array_equal(i1[0], ids[t])
+        assert H.out_rel(o1, out[t:t + 1]) <= H.OUT_REL
+    r = O.gen_normal(1, 0, O.X_TENSOR + 9, T * H.N).reshape(T, H.N)
+    out_r, _, _ = w1.gpu_forward(x, resid=r)
+    assert np.array_equal(out_r, (r + out).astype(np.float32))
+
+
 def test_layer_decode_resid(F, w0):
     x = O.gen_normal(0, 0, O.X_TENSOR + 5, 2 * H.N).reshape(2, H.N)
     r = O.gen_normal(0, 0, O.X_TENSOR + 6, 2 * H.N).reshape(2, H.N)
@@ -311,9 +338,10 @@ def test_moe_hits_repeated_blob(F, w0):
 
 @pytest.mark.parametrize("T,K", [(8, 10), (5, 32)])
 def test_moe_hits_long_windows(F, w0, T, K):
-    """Windows longer than one grouped launch takes (T = 8 = the reference's kMaxWindow,
-    moe_fast.cu:38; with K = 32 a chunk holds one token) run in chunks: every slot against the
-    oracle, pad slots untouched, and each token equal to its one-token call bit for bit."""
+    """Windows up to the reference's kMaxWindow (T = 8, moe_fast.cu:38) in one grouped launch (K = 10:
+    three experts hit by all 8 tokens, so each opens a second entry after four tokens); with K = 32 a
+    launch holds four tokens and the window runs in two. Every slot against the oracle, pad slots
+    untouched, and each token equal to its one-token call bit for bit."""
     rng = np.random.default_rng(T * K)
     x = rng.standard_normal((T, H.N)).astype(np.float32)
     hit_n = rng.integers(1, K + 1, size=T).astype(np.int32)
