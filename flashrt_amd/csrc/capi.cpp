@@ -85,9 +85,9 @@ int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const i
 int dec_check(int T, int K, int n, int ff);
 size_t dec_window_bytes(int T, int K, int n, int ff);
 int dec_window_fits(int T, int K, int ff);
-int dec_window(const int32_t* ids, const float* wts, const float* gate, int T, int K, const uint8_t* arena,
-               size_t stride, const uint8_t* shared_blob, const int8_t* xq, const float* xd, int n, int ff,
-               const float* resid, float* out, void* scratch, hipStream_t stream);
+int dec_window(const float* logits, int E, int32_t* ids, float* wts, uint32_t* counts, const float* gate, int T, int K,
+               const uint8_t* arena, size_t stride, const uint8_t* shared_blob, const int8_t* xq, const float* xd, int n,
+               int ff, const float* resid, float* out, void* scratch, hipStream_t stream);
 // decode1.hip
 size_t dec1_sync_bytes();
 int dec1_eligible(int E, int K, int n, int ff);
@@ -407,10 +407,8 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
                                    w.xd))
             return rc;
         timing_mark(s, "router_quant");
-        if (int rc = route_topk(s, w.logits, T, E, K, ids_o, wts_o, counts, nullptr, 1 << 30)) return rc;
-        timing_mark(s, "route_topk");
-        return dec_window(ids_o, wts_o, w.gate, T, K, L->experts, L->stride, L->shared, w.xq, w.xd, n, ff, resid, out,
-                          w.rest, s);
+        return dec_window(w.logits, E, ids_o, wts_o, counts, w.gate, T, K, L->experts, L->stride, L->shared, w.xq, w.xd,
+                          n, ff, resid, out, w.rest, s);
     }
     if (int rc = pf_check(T, K, n, ff, E)) return rc;
     const float* xin = x;

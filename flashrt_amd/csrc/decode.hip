@@ -29,74 +29,163 @@ namespace frt {
 
 namespace {
 
-// ---- moe_hits grouping (moe_fast.cu:195-232): distinct blob pointers across the window's hit
-// lists, in order of first appearance; no shared expert. An entry holds at most kDecMaxT tokens: the
-// occurrences of a pointer beyond its entry's four slots open another entry at their place in that
-// order (a pointer met five times in the window is read twice, once per entry).
-// One workgroup, one thread per item i = t K + k (items k >= hit_n[t] take no part): the item's
-// occurrence index j among the items of its pointer decides its entry (the one opened by the
-// pointer's occurrence 4 floor(j / 4)) and its slot in it (j mod 4). Entries in the order of the
-// items that open them, so the list is what a serial pass over the items would build.
+// ---- grouping of a window's (token, slot) items into entries (moe_fast.cu:195-232): distinct keys
+// (blob pointers, or expert ids) in order of first appearance. An entry holds at most kDecMaxT
+// tokens: the occurrences of a key beyond its entry's four slots open another entry at their place
+// in that order (a key met five times in the window is read twice, once per entry). Item i = t K + k;
+// an item's occurrence index j among the live items of its key decides its entry (the one opened by
+// the key's occurrence 4 floor(j / 4)) and its slot in it (j mod 4); entries follow the items that
+// open them, so the list is what a serial pass over the items builds. One workgroup of at least
+// kHitsMaxItems threads (thread i: item i); s_key [kHitsMaxItems] holds the keys, s_live the flags.
 constexpr int kHitsMaxItems = 128;
-__global__ void __launch_bounds__(kHitsMaxItems) k_hits_group(const uint8_t* const* __restrict__ hit_ptr,
-                                                              const int32_t* __restrict__ hit_n, int K, int T,
-                                                              DecEntry* __restrict__ ent, int32_t* __restrict__ n_ent) {
-    __shared__ const uint8_t* sp[kHitsMaxItems];
-    __shared__ int sj[kHitsMaxItems], sopen[kHitsMaxItems], sent[kHitsMaxItems], stot[kHitsMaxItems];
-    __shared__ int sntok[kHitsMaxItems], sbase[kHitsMaxItems + 1];
-    const int i = int(threadIdx.x), N = T * K;
-    const int t = i / K, k = i % K;
-    const bool live = i < N && k < min(hit_n[min(t, T - 1)], K);
-    sp[i] = live ? hit_ptr[i] : nullptr;
-    __syncthreads();
+struct GroupLds {
+    uint64_t key[kHitsMaxItems];
+    int live[kHitsMaxItems], j[kHitsMaxItems], u[kHitsMaxItems];
+    int wtot[2][kHitsMaxItems / 64];
+};
+template <class BlobOf>
+__device__ __forceinline__ void group_items(GroupLds& G, int N, int K, BlobOf blob_of, DecEntry* __restrict__ ent,
+                                            int32_t* __restrict__ n_ent) {
+    const int i = int(threadIdx.x);
+    const bool in = i < kHitsMaxItems;
+    const bool live = in && i < N && G.live[i];
+    const uint64_t key = in ? G.key[i] : 0;
     int j = 0, tot = 0;
     if (live)
         for (int q = 0; q < N; ++q) {
-            const bool same = sp[q] == sp[i];
+            const bool same = G.live[q] && G.key[q] == key;
             j += int(same && q < i);
             tot += int(same);
         }
     const bool opens = live && j % kDecMaxT == 0;
-    sj[i] = j;
-    stot[i] = tot;
-    sopen[i] = int(opens);
+    const int nt = opens ? min(kDecMaxT, tot - j) : 0;
+    // exclusive scans over the items in order: entry index and compact base of each opener
+    const int wave = i >> 6;
+    int tu = 0, tb = 0;
+    const int su = wave_excl_scan(int(opens), &tu), sb = wave_excl_scan(nt, &tb);
+    if (in && (i & 63) == 0) {
+        G.wtot[0][wave] = tu;
+        G.wtot[1][wave] = tb;
+    }
+    if (in) G.j[i] = live ? j : -1;
     __syncthreads();
-    if (i == 0) {   // entry index of each opener and the entries' compact bases, in item order
-        int u = 0, b = 0;
-        for (int q = 0; q < N; ++q)
-            if (sopen[q]) {
-                const int nt = min(kDecMaxT, stot[q] - sj[q]);
-                sent[q] = u;
-                sntok[u] = nt;
-                sbase[u] = b;
-                b += nt;
-                ++u;
-            }
-        *n_ent = u;
+    int u0 = 0, b0 = 0;
+    for (int w = 0; w < wave && w < kHitsMaxItems / 64; ++w) {
+        u0 += G.wtot[0][w];
+        b0 += G.wtot[1][w];
+    }
+    if (in) G.u[i] = u0 + su;
+    if (i == 0) {
+        int U = 0;
+        for (int w = 0; w < kHitsMaxItems / 64; ++w) U += G.wtot[0][w];
+        *n_ent = U;
     }
     __syncthreads();
     if (!live) return;
-    int opener = i;   // the item of this pointer with occurrence index 4 floor(j / 4)
+    int opener = i;   // the item of this key with occurrence index 4 floor(j / 4)
     for (int q = 0; q <= i; ++q)
-        if (sp[q] == sp[i] && sj[q] == j - j % kDecMaxT) {
+        if (G.j[q] == j - j % kDecMaxT && G.key[q] == key) {
             opener = q;
             break;
         }
-    const int u = sent[opener], s = j % kDecMaxT;
+    const int u = G.u[opener], sl = j % kDecMaxT, t = i / K, k = i % K;
     DecEntry& d = ent[u];
     if (opens) {
-        d.blob = sp[i];
-        d.ntok = sntok[u];
-        d.base = sbase[u];
-        for (int q = sntok[u]; q < kDecMaxT; ++q) {   // the unused slots
+        d.blob = blob_of(key);
+        d.ntok = nt;
+        d.base = b0 + sb;
+        for (int q = nt; q < kDecMaxT; ++q) {   // the unused slots
             d.tok[q] = 0;
             d.slot[q] = -1;
             d.w[q] = 0.0f;
         }
     }
-    d.tok[s] = t;
-    d.slot[s] = k;
-    d.w[s] = 1.0f;
+    d.tok[sl] = t;
+    d.slot[sl] = k;
+    d.w[sl] = 1.0f;
+}
+
+// moe_hits: the keys are the blob pointers; items k >= hit_n[t] take no part; no shared expert.
+__global__ void __launch_bounds__(kHitsMaxItems) k_hits_group(const uint8_t* const* __restrict__ hit_ptr,
+                                                              const int32_t* __restrict__ hit_n, int K, int T,
+                                                              DecEntry* __restrict__ ent, int32_t* __restrict__ n_ent) {
+    __shared__ GroupLds G;
+    const int i = int(threadIdx.x), N = T * K;
+    const int t = i / K, k = i % K;
+    const bool live = i < N && k < min(hit_n[min(t, T - 1)], K);
+    G.key[i] = live ? reinterpret_cast<uint64_t>(hit_ptr[i]) : 0;
+    G.live[i] = int(live);
+    __syncthreads();
+    group_items(G, N, K, [](uint64_t key) { return reinterpret_cast<const uint8_t*>(key); }, ent, n_ent);
+}
+
+// A verify window's routing and grouping in one workgroup: wave t < T routes token t (topk.hpp, the
+// k_route_topk selection: ids and renormalised weights, and the counts), then the (token, slot)
+// items, the K routed experts of each token and the shared expert as slot K, are grouped into
+// entries keyed by expert id (E: the shared expert), as group_items would: a token's ids are
+// distinct, so an item's occurrence index is the number of earlier tokens that chose its expert,
+// read off a per-expert mask of the tokens that chose it.
+template <int V>
+__global__ void __launch_bounds__(512) k_win_route(const float* __restrict__ logits, int T, int E, int K,
+                                                   int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                   uint32_t* __restrict__ counts, const uint8_t* __restrict__ arena,
+                                                   size_t stride, const uint8_t* __restrict__ shared_blob,
+                                                   DecEntry* __restrict__ ent, int32_t* __restrict__ n_ent) {
+    __shared__ float cand_v[8][64];
+    __shared__ int cand_id[8][64];
+    __shared__ int s_ids[8][32];
+    __shared__ uint32_t s_mask[1025];   // per expert (and E: the shared one), the tokens that chose it
+    __shared__ int s_ent[1025][2];      // per expert, its entries (tokens 0-3 and 4-7 of its list)
+    __shared__ int s_wtot[2][2];
+    const int wave = int(threadIdx.x) >> 6, lane = int(threadIdx.x) & 63, i = int(threadIdx.x);
+    for (int e = i; e <= E; e += 512) s_mask[e] = e == E ? (1u << T) - 1u : 0u;
+    __syncthreads();
+    if (wave < T) {
+        const int id = topk_wave<V>(logits + size_t(wave) * E, E, K, ids + size_t(wave) * K, wts + size_t(wave) * K,
+                                    cand_v[wave], cand_id[wave]);
+        if (lane < K) {
+            s_ids[wave][lane] = id;
+            atomicOr(&s_mask[id], 1u << wave);
+            if (counts) atomicAdd(counts + id, 1u);
+        }
+    }
+    __syncthreads();
+    const int K1 = K + 1, N = T * K1;
+    const bool live = i < N;   // N <= kHitsMaxItems <= 128: waves 0 and 1
+    const int t = i / K1, k = i % K1;
+    const int key = live ? (k < K ? s_ids[t][k] : E) : 0;
+    const uint32_t m = live ? s_mask[key] : 0u;
+    const int j = __popc(m & ((1u << t) - 1u)), tot = __popc(m);
+    const bool opens = live && j % kDecMaxT == 0;
+    const int nt = opens ? min(kDecMaxT, tot - j) : 0;
+    int tu = 0, tb = 0;
+    const int su = wave_excl_scan(int(opens), &tu), sb = wave_excl_scan(nt, &tb);
+    if (lane == 0 && wave < 2) {
+        s_wtot[0][wave] = tu;
+        s_wtot[1][wave] = tb;
+    }
+    __syncthreads();
+    const int u0 = wave == 1 ? s_wtot[0][0] : 0, b0 = wave == 1 ? s_wtot[1][0] : 0;
+    const int u = u0 + su;
+    if (opens) s_ent[key][j / kDecMaxT] = u;
+    if (i == 0) *n_ent = s_wtot[0][0] + (N > 64 ? s_wtot[0][1] : 0);
+    __syncthreads();
+    if (!live) return;
+    DecEntry& d = ent[s_ent[key][j / kDecMaxT]];
+    const int sl = j % kDecMaxT;
+    if (opens) {
+        d.blob = key < E ? arena + size_t(key) * stride : shared_blob;
+        d.ntok = nt;
+        d.base = b0 + sb;
+        for (int q = nt; q < kDecMaxT; ++q) {   // the unused slots
+            d.tok[q] = 0;
+            d.slot[q] = -1;
+            d.w[q] = 0.0f;
+        }
+    }
+    d.tok[sl] = t;
+    d.slot[sl] = k;
+    d.w[sl] = 1.0f;
 }
 
 // ---- gate + up for 32 ff rows of one entry by NW waves (32 / NW rows each). NB = n / 64 blocks
@@ -509,16 +598,6 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent_g, const i
 // ---- a verify window of 5 .. 8 tokens through the moe_hits kernels (moe_block_fast's window path,
 // arch/qwen4exp/moe_fast.cu:1015-1108 with T <= kMaxWindow): token t's hit list is its K routed
 // experts' blobs (rank order) and the shared expert's as slot K.
-__global__ void k_win_hits(const int32_t* __restrict__ ids, int T, int K, const uint8_t* __restrict__ arena,
-                           size_t stride, const uint8_t* __restrict__ shared_blob, const uint8_t** __restrict__ hit_ptr,
-                           int32_t* __restrict__ hit_n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < T * (K + 1)) {
-        const int t = i / (K + 1), k = i % (K + 1);
-        hit_ptr[i] = k < K ? arena + size_t(ids[t * K + k]) * stride : shared_blob;
-        if (k == 0) hit_n[t] = K + 1;
-    }
-}
 // out[t] = resid[t] + (sum over the K routed slots in ascending expert id of w * y, from 0) + y_shared *
 // sigmoid(gate[t]) (moe_cpu.cpp:63-80 phase B order; moe_ref.cu:90-97); yh [T][K + 1][n]
 __global__ void __launch_bounds__(256) k_win_combine(const float* __restrict__ yh, const int32_t* __restrict__ ids,
@@ -683,8 +762,10 @@ int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const i
     const size_t smem = size_t(T * (K + 1)) * (ff + (ff / kQ8) * 4 + 8 * 4);
     if (smem > 96 * 1024) return set_error(kErrShape, "moe_hits: T=%d K=%d ff=%d needs %zu B of LDS", T, K, ff, smem);
     const DecScratch s = dec_carve(scratch, T, K, ff);
-    k_hits_group<<<1, kHitsMaxItems, 0, stream>>>(hit_ptr, hit_n, K, T, s.ent, s.n_ent);
-    timing_mark(stream, "hits_group");
+    if (hit_ptr) {   // (null: the caller has filled the entry list, dec_window)
+        k_hits_group<<<1, kHitsMaxItems, 0, stream>>>(hit_ptr, hit_n, K, T, s.ent, s.n_ent);
+        timing_mark(stream, "hits_group");
+    }
     const int nb = n / kBlock;
     dim3 g1(ff / 32, T * K);
 #define FRT_GU(NBV) \
@@ -708,20 +789,23 @@ int dec_window_fits(int T, int K, int ff) {
     return T >= 1 && T <= kDecMaxHitsT && T * (K + 1) <= kHitsMaxItems &&
            size_t(T) * (K + 2) * (size_t(ff) + (ff / kQ8) * 4 + 32) <= 96 * 1024;
 }
-int dec_window(const int32_t* ids, const float* wts, const float* gate, int T, int K, const uint8_t* arena,
-               size_t stride, const uint8_t* shared_blob, const int8_t* xq, const float* xd, int n, int ff,
-               const float* resid, float* out, void* scratch, hipStream_t stream) {
-    if (!dec_window_fits(T, K, ff)) return set_error(kErrShape, "decode window: T=%d K=%d ff=%d", T, K, ff);
+int dec_window(const float* logits, int E, int32_t* ids, float* wts, uint32_t* counts, const float* gate, int T, int K,
+               const uint8_t* arena, size_t stride, const uint8_t* shared_blob, const int8_t* xq, const float* xd, int n,
+               int ff, const float* resid, float* out, void* scratch, hipStream_t stream) {
+    if (!dec_window_fits(T, K, ff) || E < 1 || E > 1024) return set_error(kErrShape, "decode window: T=%d K=%d ff=%d E=%d", T, K, ff, E);
     uint8_t* p = static_cast<uint8_t*>(scratch);
-    const uint8_t** hit_ptr = reinterpret_cast<const uint8_t**>(p);
-    p += up256(size_t(T) * (K + 1) * 8);
-    int32_t* hit_n = reinterpret_cast<int32_t*>(p);
-    p += 256;
+    p += up256(size_t(T) * (K + 1) * 8) + 256;
     float* yh = reinterpret_cast<float*>(p);
     p += up256(size_t(T) * (K + 1) * n * 4);
-    k_win_hits<<<(T * (K + 1) + 63) / 64, 64, 0, stream>>>(ids, T, K, arena, stride, shared_blob, hit_ptr, hit_n);
-    FRT_LAUNCHED("decode window hits");
-    if (int rc = dec_hits(hit_ptr, hit_n, K + 1, xq, xd, n, ff, p, yh, stream, T)) return rc;
+    const DecScratch s = dec_carve(p, T, K + 1, ff);
+    if (E <= 512)
+        launch_timed("win_route", k_win_route<8>, dim3(1), dim3(512), 0, stream, logits, T, E, K, ids, wts, counts,
+                     arena, stride, shared_blob, s.ent, s.n_ent);
+    else
+        launch_timed("win_route", k_win_route<16>, dim3(1), dim3(512), 0, stream, logits, T, E, K, ids, wts, counts,
+                     arena, stride, shared_blob, s.ent, s.n_ent);
+    FRT_LAUNCHED("decode window routing");
+    if (int rc = dec_hits(nullptr, nullptr, K + 1, xq, xd, n, ff, p, yh, stream, T)) return rc;
     launch_timed("win_combine", k_win_combine, dim3((n + 1023) / 1024, T), dim3(256), 0, stream, (const float*)yh, ids,
                  wts, gate, T, K, n, resid, out);
     FRT_LAUNCHED("decode window combine");
