@@ -297,7 +297,7 @@ def run_windows(args, F, torch, st):
         distinct = float(np.mean([len(np.unique(idh[l])) for l in range(layers)]))
         need = (distinct + 1) * eb + E * N * 4 + N * 4
         # T <= 4: the grouped decode kernels; 5 .. 8: router + top-k + one moe_hits launch + combine
-        path = "decode" if T * K <= 63 and T <= 4 else ("window" if T <= 8 else "prefill")
+        path = "decode" if T * K <= 63 and T < args.window_min_t else ("window" if T <= 8 else "prefill")
         res[f"T{T}"] = dict(us_per_call=round(us, 2), tokens_per_s=round(T / us * 1e6, 1), path=path,
                             distinct_experts=round(distinct, 2), GBps=round(need / (us * 1e-6) / 1e9, 1))
         if T > 1:   # per-kernel averages over an eager pass of the 48 calls, queued behind a spin kernel
@@ -467,6 +467,9 @@ def main():
     ap.add_argument("--decode-path", choices=["stack", "fused", "three"], default="stack",
                     help="the 48 layers as one persistent launch (stack, default), one persistent launch per layer "
                          "(fused), or three kernels per layer (three)")
+    ap.add_argument("--window-min-t", type=int, default=2,
+                    help="windows of at least this many tokens (2..8) take the window path (router, top-k and "
+                         "grouping in one workgroup, one moe_hits launch, combine); 9: none")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -487,6 +490,7 @@ def main():
         del src, dst
 
     F.set_option("decode_fused", 0 if args.decode_path == "three" else 1)
+    F.set_option("window_min_t", args.window_min_t)
     F.set_option("decode_grid", args.decode_grid)
     st = run_stack(args, F, torch)
     if st["sync_error"]:

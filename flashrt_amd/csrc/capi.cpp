@@ -160,9 +160,10 @@ struct LayerWs {
 // A verify window of 5 .. 8 tokens (the reference's kMaxWindow) goes through the decode GEMV kernels
 // (router + fused Q8_0, top-k, one moe_hits launch, combine) when it fits one hits launch and the
 // router's fused quantization; larger windows take the prefill path.
+int g_window_min_t = 2;   // windows of at least this many tokens take the window path (measured faster from 2)
 static bool window_path(const frt_moe_layer& L, int T) {
     const int K = L.top_k, n = L.d_model;
-    if (T <= kDecodeMaxT && T * K <= 63) return false;   // the grouped decode path
+    if (T < g_window_min_t && T <= kDecodeMaxT && T * K <= 63) return false;   // the grouped decode path
     return T <= 8 && dec_window_fits(T, K, L.d_ff) && router_fused_fits(T, n) && dec_check(1, K, n, L.d_ff) == kOk;
 }
 
@@ -180,8 +181,9 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
     w.gate = reinterpret_cast<float*>(take(size_t(T) * 4));
     w.ids = reinterpret_cast<int32_t*>(take(size_t(T) * K * 4));
     w.wts = reinterpret_cast<float*>(take(size_t(T) * K * 4));
-    const bool dec = T <= kDecodeMaxT && T * K <= 63;
-    if (dec || window_path(L, T)) {
+    const bool win = window_path(L, T);
+    const bool dec = !win && T <= kDecodeMaxT && T * K <= 63;
+    if (dec || win) {
         w.xq = reinterpret_cast<int8_t*>(take(size_t(T) * n));
         w.xd = reinterpret_cast<float*>(take(size_t(T) * (n / kQ8) * 4));
         w.rest_bytes = dec ? dec_scratch_bytes(T, K, ff) : dec_window_bytes(T, K, n, ff);
@@ -199,7 +201,7 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
 // ---- the allocation-free decode entry point's workspace: a file-scope device array, one copy per
 // GPU, held until the process ends. Host code never passes the array's name to a kernel or a copy:
 // it uses the device address hipGetSymbolAddress returns, looked up once per device.
-constexpr size_t kNoAllocScratchBytes = size_t(1) << 20;
+constexpr size_t kNoAllocScratchBytes = size_t(2) << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 namespace {
 constexpr int kMaxDevices = 64;
@@ -392,7 +394,7 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     if (T == 1 && g_dec1_on && dec1_support(E, K, n, ff) >= 1)   // the whole layer in one persistent launch
         return dec1_layer(x, L->router_w, L->router_bias, L->gate_w, E, K, L->experts, L->stride, L->shared, n, ff,
                           norm, resid, out, ids_o, wts_o, counts, w.sync, L->next_router_w, s);
-    if (T <= kDecodeMaxT && T * K <= 63) {
+    if (!window_path(*L, T) && T <= kDecodeMaxT && T * K <= 63) {
         if (int rc = dec_check(T, K, n, ff)) return rc;
         // router logits, the shared gate, the RMS scale and Q8_0 of the input in one launch
         if (int rc = router_logits(x, T, L->router_w, L->router_bias, L->gate_w, E, n, w.logits, w.gate, s, norm, w.xq,
@@ -503,6 +505,11 @@ int frt_set_option(const char* name, int64_t value) {
     if (!std::strcmp(name, "decode_grid")) {
         if (value < 0 || value > 1024) return set_error(kErrShape, "set_option: decode_grid %lld", (long long)value);
         g_dec1_grid_cap = int(value);
+        return kOk;
+    }
+    if (!std::strcmp(name, "window_min_t")) {   // (2 .. 9; 9: no window path)
+        if (value < 2 || value > 9) return set_error(kErrShape, "set_option: window_min_t %lld", (long long)value);
+        g_window_min_t = int(value);
         return kOk;
     }
     if (!std::strcmp(name, "sync_ticks")) {

@@ -235,11 +235,14 @@ def test_layer_decode_config1_window(F):
     assert H.out_rel(out, ref) <= H.OUT_REL
     # overlapping routes: the window reads fewer than 3 * 10 distinct experts
     assert len(set(ids.reshape(-1).tolist())) < 30
-    # each token alone gives the same outputs as the window (moe_fast.cu:195-355 exactness)
+    # each token alone (the single-token path) selects the same experts and gives the same outputs
+    # within the output bar (the window path forms the routing weights with the top-k kernel's
+    # formula, so they can differ from the single-token path's in the last bits; the moe_hits
+    # window itself equals its one-token calls bit for bit, test_moe_hits)
     for t in range(3):
         o1, i1, _ = w1.gpu_forward(x[t:t + 1])
         assert np.array_equal(i1[0], ids[t])
-        assert np.array_equal(o1[0], out[t])
+        assert H.out_rel(o1, out[t:t + 1]) <= H.OUT_REL
 
 
 @pytest.mark.parametrize("T", [5, 8])

@@ -57,4 +57,4 @@ def test_noalloc_refuses_prefill_sizes():
         w.layer_obj.forward_noalloc(x, out, T=8)
     assert e.value.code == -1
     assert "decode windows only" in str(e.value)
-    assert F.noalloc_scratch_bytes() == 1 << 20
+    assert F.noalloc_scratch_bytes() == 2 << 20
