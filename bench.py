@@ -525,7 +525,7 @@ def main():
     tf = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tf):
         with open(tf) as f:
-            traffic = (json.load(f).get(dom) or {}).get("bytes")   # HBM bytes per launch, from rocprofv3 PMC
+            traffic = (json.load(f).get("kernels", {}).get(dom) or {}).get("bytes")   # HBM bytes per launch, rocprofv3 PMC
 
     line = {
         "metric": METRIC,
