@@ -95,6 +95,12 @@ __device__ __forceinline__ uint4 gld_u4(const void* p) {
     const u32x4_t v = gld<u32x4_t>(p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// the same as a non-temporal (streaming) load, for expert weights read once per token (measured on
+// the decode stack: 0.5% faster than cached loads, same box, alternating runs)
+__device__ __forceinline__ uint4 gld_u4_nt(const void* p) {
+    const u32x4_t v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 __device__ __forceinline__ float h2f(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 

@@ -374,8 +374,8 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
             const int rl = p * RPW + rsub;
             if (live && rl < ROWS) okm |= 1u << p;
             const int row = rb * 32 + wave * ROWS + min(rl, ROWS - 1);
-            cg[p] = gld_u4(gcodes + (size_t(row) * NB + bl) * 16);
-            cu[p] = gld_u4(ucodes + (size_t(row) * NB + bl) * 16);
+            cg[p] = gld_u4_nt(gcodes + (size_t(row) * NB + bl) * 16);
+            cu[p] = gld_u4_nt(ucodes + (size_t(row) * NB + bl) * 16);
             sg[p] = gld<uint16_t>(gscal + size_t(row) * NB + bl);
             su[p] = gld<uint16_t>(uscal + size_t(row) * NB + bl);
         }

@@ -360,7 +360,7 @@ __device__ __forceinline__ void down_load(const DecEntry* ent, int U, int u0, in
             if (u0 + US * i < U && live && rl < D::RD) R.ok |= 1u << (i * D::PASSES + p);
             const int r = r0 + min(rl, D::RD - 1);
             const int bb = live ? b : 0;
-            R.cd[i][p] = gld_u4(db[i] + (size_t(r) * NBF + bb) * 16);
+            R.cd[i][p] = gld_u4_nt(db[i] + (size_t(r) * NBF + bb) * 16);
             R.sd[i][p] = gld<uint16_t>(db[i] + size_t(n) * NBF * 16 + (size_t(r) * NBF + bb) * 2);
         }
     }
