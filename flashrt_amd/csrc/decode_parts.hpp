@@ -96,18 +96,13 @@ __device__ __forceinline__ void route1_wave(const float (&v)[V], int E, int K, f
     const bool cl = lane < C;
     const float cv = cl ? S.cand_v[lane] : 0.0f;
     const int ci = cl ? S.cand_id[lane] : 0x7fffffff;
-    // rank among the candidates: those ahead by logit, or equal and lower id (= lower slot); the
-    // candidates' logits are read four at a time (the same address in every lane); float order
-    // with -0 == +0 is the keys' order
+    // rank among the candidates: those ahead by logit, or equal and lower id (= lower slot); each
+    // candidate's logit broadcast from its lane (no LDS round trip per step); float order with
+    // -0 == +0 is the keys' order
     int rank = 0;
-    for (int j0 = 0; j0 < C; j0 += 4) {
-        const float4 q = *reinterpret_cast<const float4*>(S.cand_v + j0);
-        const float qv[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int j = j0 + u;
-            rank += int(j < C && (qv[u] > cv || (qv[u] == cv && j < lane)));
-        }
+    for (int j = 0; j < C; ++j) {
+        const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), j));
+        rank += int(o > cv || (o == cv && j < lane));
     }
     const bool sel = cl && rank < K;
     const int u = lanes_below(__ballot(sel));   // entry index: ascending expert id
