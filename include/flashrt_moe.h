@@ -124,15 +124,17 @@ int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, 
 /* ---- decode expert GEMVs (arch/qwen4exp/moe_fast.hpp:134-142 moe_hits_scratch_bytes, moe_hits).
  * yh [T][K][n]: entry (t, k) for k < hit_n[t] = down(silu(gate x) * up x) of the blob at
  * hit_ptr[t*K + k] (device array of device pointers); entries k >= hit_n[t] are not written.
- * x [T][n] fp32, any T >= 1: windows of up to min(4, 63 / K) tokens read each distinct blob once
- * (moe_fast.cu:195-355); a longer window runs in such chunks, one after the other on the stream.
+ * x [T][n] fp32, any T >= 1: one launch takes up to 8 tokens (the reference's kMaxWindow,
+ * moe_fast.cu:38) and 128 (token, slot) items, and reads each distinct blob once per four of its
+ * tokens (moe_fast.cu:195-355); a longer window runs in such launches, one after the other.
  * Activations are quantized to Q8_0 per 32 (the reference quantizes per 64 here). */
 size_t frt_moe_hits_scratch_bytes(int K, int ff, int T, int n);
 int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const float* x, int n, int ff,
                  void* scratch, float* yh, void* stream, int T);
 
 /* ---- one whole MoE layer on an HBM-resident arena: router logits -> route_topk -> routed experts
- * + shared expert * sigmoid(gate) (moe_block_fast, arch/qwen4exp/moe_fast.hpp:144-147, for T <= 4;
+ * + shared expert * sigmoid(gate) (moe_block_fast, arch/qwen4exp/moe_fast.hpp:144-147, for T <= 8:
+ * T = 1 as one persistent launch, 2..8 through the moe_hits kernels;
  * moe_block_stream, arch/qwen4exp/moe_stream.hpp:35, for prefill chunks; same math as moe_block,
  * arch/qwen4exp/blocks.hpp:286). out [T][n] = (resid ? resid : 0) + moe(u), with u = x, or with
  * flags & FRT_LAYER_NORM_INPUT u = x / rms(x) (the unweighted RMS norm that precedes the MoE in the
