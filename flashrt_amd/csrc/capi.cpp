@@ -62,6 +62,8 @@ void timing_mark(hipStream_t stream, const char* kernel) {
     t.marks.emplace_back(kernel, e);
 }
 
+// gen.hip
+int router_widen(const void* src, int type, size_t count, float* dst, hipStream_t stream);
 // route.hip
 int router_logits(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
                   float* logits, float* gate, hipStream_t stream, int norm, int8_t* xq, float* xd);
@@ -325,6 +327,10 @@ int frt_moe_route_topk(void* stream, const float* logits, int T, int E, int k, i
 int frt_router_logits(void* stream, const float* x, int T, const float* W, const float* bias, const float* gate_w,
                       int E, int n, float* logits, float* gate) {
     return router_logits(x, T, W, bias, gate_w, E, n, logits, gate, static_cast<hipStream_t>(stream), 0, nullptr, nullptr);
+}
+
+int frt_router_widen(void* stream, const void* src, int type, size_t count, float* dst) {
+    return router_widen(src, type, count, dst, static_cast<hipStream_t>(stream));
 }
 
 int frt_quantize_q8(void* stream, const float* x, int rows, int n, int8_t* xq, float* xd) {

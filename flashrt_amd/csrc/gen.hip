@@ -175,4 +175,42 @@ void gen_zipf_bias(uint64_t seed, int cfg, int layer, int E, float s, float alph
     for (int e = 0; e < E; ++e) bias[e] = float(-double(s) * double(alpha) * std::log(1.0 + double(perm[e])));
 }
 
+// ---- router / gate tensors of a GGUF file widened to fp32 (exact for every type taken)
+namespace {
+__global__ void k_widen_f16(const uint16_t* __restrict__ s, size_t n, float* __restrict__ d) {
+    for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+        d[i] = h2f(s[i]);
+}
+__global__ void k_widen_bf16(const uint16_t* __restrict__ s, size_t n, float* __restrict__ d) {
+    for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+        d[i] = __uint_as_float(uint32_t(s[i]) << 16);
+}
+// ggml block_q8_0: {fp16 d; int8 qs[32]} (34 bytes); value j of block b = d * qs[j] (exact in fp32)
+__global__ void k_widen_q8_0(const uint8_t* __restrict__ s, size_t n, float* __restrict__ d) {
+    for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+        const uint8_t* blk = s + (i / 32) * 34;
+        const uint16_t dh = uint16_t(blk[0]) | (uint16_t(blk[1]) << 8);
+        d[i] = h2f(dh) * float(int8_t(blk[2 + i % 32]));
+    }
+}
+}  // namespace
+
+int router_widen(const void* src, int type, size_t count, float* dst, hipStream_t stream) {
+    if (!src || !dst) return set_error(kErrNull, "router_widen: null pointer");
+    if (count == 0) return kOk;
+    const int grid = int(std::min<size_t>((count + 255) / 256, 4096));
+    switch (type) {
+        case 0: FRT_HIP(hipMemcpyAsync(dst, src, count * 4, hipMemcpyDeviceToDevice, stream)); return kOk;
+        case 1: k_widen_f16<<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(src), count, dst); break;
+        case 30: k_widen_bf16<<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(src), count, dst); break;
+        case 8:
+            if (count % 32) return set_error(kErrShape, "router_widen: Q8_0 count %zu not a multiple of 32", count);
+            k_widen_q8_0<<<grid, 256, 0, stream>>>(static_cast<const uint8_t*>(src), count, dst);
+            break;
+        default: return set_error(kErrShape, "router_widen: ggml type %d (F32, F16, BF16 or Q8_0)", type);
+    }
+    FRT_LAUNCHED("router_widen");
+    return kOk;
+}
+
 }  // namespace frt

@@ -238,6 +238,17 @@ class MoeStack:
                                           ws.numel(), _s(stream)))
 
 
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_BF16 = 0, 1, 8, 30
+
+
+def router_widen(src: torch.Tensor, gguf_type: int, count: int, dst: torch.Tensor, stream=None) -> None:
+    """frt_router_widen: a router or gate tensor in its GGUF type (ggml type id F32, F16, BF16 or
+    Q8_0, raw bytes on the device) widened exactly to the fp32 layout the router kernels take."""
+    if dst.dtype != torch.float32 or dst.numel() < count:
+        raise ValueError("router_widen: dst must be float32 with at least count values")
+    check(lib().frt_router_widen(_s(stream), _p(src), int(gguf_type), int(count), _p(dst)))
+
+
 def set_option(name: str, value: int) -> None:
     """frt_set_option: "decode_fused" (1: single-token layers in one persistent launch, 0: three
     kernels) or "sync_ticks" (bound of the persistent launch's waits, 100 MHz ticks)."""

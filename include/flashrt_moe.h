@@ -102,6 +102,18 @@ int frt_moe_route_topk(void* stream, const float* logits, int T, int E, int k, i
 int frt_router_logits(void* stream, const float* x, int T, const float* W, const float* bias, const float* gate_w,
                       int E, int n, float* logits, float* gate);
 
+/* ---- router / gate tensors in the model's GGUF types, widened to the fp32 layout the router
+ * kernels take (the reference reads ffn_gate_inp and ffn_gate_inp_shexp through ggml's linear(),
+ * arch/qwen4exp/blocks.hpp:85, in whatever type the file ships). type is the ggml type id:
+ * FRT_GGML_F32 (copy), FRT_GGML_F16, FRT_GGML_BF16 or FRT_GGML_Q8_0 (blocks {fp16 d; int8 q[32]},
+ * value d * q). Every one widens to fp32 exactly, so the router's canonical order then runs on the
+ * model's own values. count values (a multiple of 32 for Q8_0); src and dst device pointers. */
+#define FRT_GGML_F32 0
+#define FRT_GGML_F16 1
+#define FRT_GGML_Q8_0 8
+#define FRT_GGML_BF16 30
+int frt_router_widen(void* stream, const void* src, int type, size_t count, float* dst);
+
 /* ---- Q8_0 activation quantization (quant/q2_0/q2_0.hpp:66-70 quantize_q8): per 32 values
  * d = fp16(amax/127), q = roundf(x * 127/amax). xq [rows][n] int8, xd [rows][n/32] float. */
 int frt_quantize_q8(void* stream, const float* x, int rows, int n, int8_t* xq, float* xd);

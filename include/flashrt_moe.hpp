@@ -169,6 +169,13 @@ LoadStats load_experts(const GgufT& g, const SpecT& s, ExpertArena& arena, int t
 // The arena is device memory already: its device address.
 inline const uint8_t* arena_register(const ExpertArena& arena) { return static_cast<const uint8_t*>(arena.buf.ptr); }
 
+// A router or gate tensor in the GGUF type the model ships (ggml F32, F16, BF16, Q8_0) widened
+// exactly to the fp32 layout the router takes (the reference reads it through ggml's linear(),
+// arch/qwen4exp/blocks.hpp:85). Throws on an unsupported type.
+inline void router_widen(hipStream_t stream, const void* src, int ggml_type, size_t count, float* dst) {
+    detail::check(frt_router_widen(stream, src, ggml_type, count, dst), "router_widen");
+}
+
 inline void moe_route_topk(hipStream_t stream, const float* logits, int T, int E, int k, int32_t* ids, float* wts,
                            uint32_t* counts, uint32_t* tail_counts = nullptr, int tail_from = 1 << 30) {
     detail::check(frt_moe_route_topk(stream, logits, T, E, k, ids, wts, counts, tail_counts, tail_from),

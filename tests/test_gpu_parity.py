@@ -368,6 +368,42 @@ def test_moe_hits_long_windows(F, w0, T, K):
         assert np.array_equal(y1.cpu().numpy()[0, :hit_n[t]], y[t, :hit_n[t]]), t
 
 
+def test_router_widen_gguf_types(F):
+    """Router / gate tensors in the GGUF types a model ships (ggml F32, F16, BF16, Q8_0 blocks
+    {fp16 d; int8 q[32]}) widen to fp32 exactly: against numpy's exact conversions; an unsupported
+    type and a Q8_0 count off the block size fail loudly."""
+    rng = np.random.default_rng(30)
+    n = 512 * 64
+    ref = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    out = torch.full((n,), float("nan"), dtype=torch.float32, device="cuda")
+    h16 = ref.astype(np.float16)
+    F.router_widen(torch.from_numpy(h16.view(np.uint8).copy()).cuda(), F.GGML_F16, n, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), h16.astype(np.float32))
+    b16 = (ref.view(np.uint32) >> 16).astype(np.uint16)   # truncation: any bf16 bit pattern
+    F.router_widen(torch.from_numpy(b16.view(np.uint8).copy()).cuda(), F.GGML_BF16, n, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), b16.astype(np.uint32) << 16)
+    nb = n // 32
+    d = (np.abs(rng.standard_normal(nb)) * 1e-3).astype(np.float16)
+    q = rng.integers(-127, 128, size=(nb, 32)).astype(np.int8)
+    blocks = np.zeros((nb, 34), np.uint8)
+    blocks[:, :2] = d.view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:] = q.view(np.uint8)
+    F.router_widen(torch.from_numpy(blocks.reshape(-1)).cuda(), F.GGML_Q8_0, n, out)
+    torch.cuda.synchronize()
+    want = (d.astype(np.float32)[:, None] * q.astype(np.float32)).reshape(-1)
+    assert np.array_equal(out.cpu().numpy(), want)
+    src32 = torch.from_numpy(ref).cuda()
+    F.router_widen(src32, F.GGML_F32, n, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, src32)
+    with pytest.raises(F.FrtError):
+        F.router_widen(src32, 2, n, out)          # Q4_0: not a router type here
+    with pytest.raises(F.FrtError):
+        F.router_widen(src32, F.GGML_Q8_0, 33, out)
+
+
 # ---------------------------------------------------------------- prefill path
 
 @pytest.mark.parametrize("yd_bf16", [False, True])
