@@ -595,6 +595,66 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent_g, const i
 }
 
 
+// ---- moe_hits down with per-slot outputs: workgroup (x, y) takes output rows 8x .. 8x + 7 of entries
+// 16y .. 16y + 15 (4 waves x 4 entries), staging only those entries' hidden vectors (their compact
+// slots are contiguous); no sum across entries, so the entry chunks are independent workgroups.
+constexpr int kHitsDownEnt = 16;
+template <int NBF>
+__global__ void __launch_bounds__(256) k_hits_down(const DecEntry* __restrict__ ent_g, const int32_t* __restrict__ n_ent,
+                                                   const int8_t* __restrict__ hq, const float* __restrict__ hd, int n,
+                                                   int ff, int K, float* __restrict__ yh) {
+    constexpr int RD = 8;
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ DecEntry s_ent[kHitsDownEnt];
+    const int U = *n_ent, u_lo = int(blockIdx.y) * kHitsDownEnt;
+    if (u_lo >= U) return;
+    const int nu = min(U - u_lo, kHitsDownEnt);
+    const int r0 = blockIdx.x * RD, tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const DecEntry* eg = ent_g + u_lo;
+    const int c_lo = eg[0].base, c_hi = eg[nu - 1].base + eg[nu - 1].ntok;   // this chunk's compact slots
+    const int nc = c_hi - c_lo;
+    int8_t* sh_q = reinterpret_cast<int8_t*>(smem);                       // [nc][ff]
+    float* sh_d = reinterpret_cast<float*>(smem + size_t(kHitsDownEnt * kDecMaxT) * ff);   // [nc][ff/32]
+    float* sh_y = sh_d + size_t(kHitsDownEnt * kDecMaxT) * (ff / kQ8);                     // [nc][RD]
+    // staging loads first (waits count in issue order), then the down rows, then the LDS stores
+    const int nq = nc * ff / 16, nd = nc * (ff / kQ8);
+    const int4* srcq = reinterpret_cast<const int4*>(hq + size_t(c_lo) * ff);
+    const float* srcd = hd + size_t(c_lo) * (ff / kQ8);
+    int4 vq[4];
+    float vd[2];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) vq[k] = srcq[min(tid + 256 * k, nq - 1)];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) vd[k] = srcd[min(tid + 256 * k, nd - 1)];
+    DownRegs<NBF, 4> R;
+    down_load<NBF, 4>(eg, nu, wave, r0, n, ff, R);
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < nu * int(sizeof(DecEntry) / 4))
+        reinterpret_cast<int32_t*>(s_ent)[tid] = reinterpret_cast<const int32_t*>(eg)[tid];
+    int4* dq = reinterpret_cast<int4*>(sh_q);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (tid + 256 * k < nq) dq[tid + 256 * k] = vq[k];
+    for (int i = tid + 1024; i < nq; i += 256) dq[i] = srcq[i];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        if (tid + 256 * k < nd) sh_d[tid + 256 * k] = vd[k];
+    for (int i = tid + 512; i < nd; i += 256) sh_d[i] = srcd[i];
+    __syncthreads();
+    // entries indexed locally, slots globally: the LDS arrays are offset by the chunk's first slot
+    down_compute<NBF, 4>(s_ent, nu, wave, R, sh_q - size_t(c_lo) * ff, sh_d - size_t(c_lo) * (ff / kQ8),
+                         sh_y - size_t(c_lo) * RD, ff);
+    __syncthreads();
+    for (int i = tid; i < nc * RD; i += 256) {
+        const int c = c_lo + i / RD, rl = i % RD;
+        int u = 0;
+        while (s_ent[u].base + s_ent[u].ntok <= c) ++u;
+        const int j = c - s_ent[u].base;
+        yh[(size_t(s_ent[u].tok[j]) * K + s_ent[u].slot[j]) * n + r0 + rl] = sh_y[(c - c_lo) * RD + rl];
+    }
+}
+
 // ---- a verify window of 5 .. 8 tokens through the moe_hits kernels (moe_block_fast's window path,
 // arch/qwen4exp/moe_fast.cu:1015-1108 with T <= kMaxWindow): token t's hit list is its K routed
 // experts' blobs (rank order) and the shared expert's as slot K.
@@ -682,11 +742,12 @@ static int dec_down(const DecScratch& s, int n, int ff, int T, int K, const floa
     const int S = T * (K + 1);                         // compact slots at most (the shared expert's included)
     const int U_max = T * K + 1 < kDecMaxEnt ? T * K + 1 : kDecMaxEnt;   // entries at most
     const size_t smem = size_t(S) * ff + size_t(S) * (ff / kQ8) * 4 + size_t(S) * 8 * 4;
+    const size_t hits_smem = size_t(kHitsDownEnt * kDecMaxT) * (ff + (ff / kQ8) * 4 + 8 * 4);
 #define FRT_DN(NBFV)                                                                                           \
     case NBFV:                                                                                                 \
         if (yh)                                                                                                \
-            launch_timed("dec_down", k_dec_down<NBFV, true, false>, dim3(n / 8), dim3(256), smem, stream, s.ent,  \
-                         s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid, out, yh, U_max, S, pf, pf_rows);          \
+            launch_timed("dec_down", k_hits_down<NBFV>, dim3(n / 8, (U_max + kHitsDownEnt - 1) / kHitsDownEnt),   \
+                         dim3(256), hits_smem, stream, s.ent, s.n_ent, s.hq, s.hd, n, ff, K, yh);                   \
         else if (T == 1)                                                                                       \
             launch_timed("dec_down", k_dec_down<NBFV, false, true>, dim3(n / 8), dim3(256), smem, stream, s.ent,  \
                          s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid, out, yh, U_max, S, pf, pf_rows);          \
