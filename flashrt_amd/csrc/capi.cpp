@@ -162,6 +162,7 @@ struct LayerWs {
 // A verify window of 5 .. 8 tokens (the reference's kMaxWindow) goes through the decode GEMV kernels
 // (router + fused Q8_0, top-k, one moe_hits launch, combine) when it fits one hits launch and the
 // router's fused quantization; larger windows take the prefill path.
+extern int g_router_mfma;
 int g_window_min_t = 2;   // windows of at least this many tokens take the window path (measured faster from 2)
 static bool window_path(const frt_moe_layer& L, int T) {
     const int K = L.top_k, n = L.d_model;
@@ -327,6 +328,20 @@ int frt_moe_route_topk(void* stream, const float* logits, int T, int E, int k, i
 int frt_router_logits(void* stream, const float* x, int T, const float* W, const float* bias, const float* gate_w,
                       int E, int n, float* logits, float* gate) {
     return router_logits(x, T, W, bias, gate_w, E, n, logits, gate, static_cast<hipStream_t>(stream), 0, nullptr, nullptr);
+}
+
+size_t frt_router_gemm_workspace_bytes(int T, int E, int has_gate) {
+    return T < 1 || E < 1 ? 0 : router_gemm_ws_bytes(T, E, has_gate != 0);
+}
+
+int frt_router_logits_gemm(void* stream, const float* x, int T, const float* W, const float* bias, const float* gate_w,
+                           int E, int n, float* logits, float* gate, void* ws, size_t ws_bytes) {
+    if (!x || !W || !logits || !ws) return set_error(kErrNull, "router_logits_gemm: null pointer");
+    if (T < 1 || E < 1 || E > 4096) return set_error(kErrShape, "router_logits_gemm: T=%d E=%d", T, E);
+    if (ws_bytes < router_gemm_ws_bytes(T, E, gate_w != nullptr))
+        return set_error(kErrWorkspace, "router_logits_gemm: workspace %zu < %zu", ws_bytes,
+                         router_gemm_ws_bytes(T, E, gate_w != nullptr));
+    return router_gemm(x, T, W, bias, gate_w, E, n, logits, gate, static_cast<float*>(ws), static_cast<hipStream_t>(stream));
 }
 
 int frt_router_widen(void* stream, const void* src, int type, size_t count, float* dst) {
@@ -516,6 +531,10 @@ int frt_set_option(const char* name, int64_t value) {
     if (!std::strcmp(name, "window_min_t")) {   // (2 .. 9; 9: no window path)
         if (value < 2 || value > 9) return set_error(kErrShape, "set_option: window_min_t %lld", (long long)value);
         g_window_min_t = int(value);
+        return kOk;
+    }
+    if (!std::strcmp(name, "router_mfma")) {
+        g_router_mfma = value ? 1 : 0;
         return kOk;
     }
     if (!std::strcmp(name, "sync_ticks")) {

@@ -479,6 +479,113 @@ k_router_gemm(const float* __restrict__ x, int T, const float* __restrict__ W, c
 
 // top of the tree: v = ((S0 + S1) + (S2 + S3)) + ((S4 + S5) + (S6 + S7)); logits [T][E] = v + bias,
 // gate [T] = row E's v
+// The same split GEMM on the matrix cores. v_mfma_f32_16x16x4f32 accumulates its four products in
+// K order as a chain of fused multiply-adds (d = fma(a3, b3, fma(a2, b2, fma(a1, b1, fma(a0, b0, c)))),
+// bit for bit; checked on the MI355X over 5.12M random operands with exponents spread over 2^-12 ..
+// 2^12), so a chain of L = n / 64 values is L / 4 MFMA steps from a zero accumulator in natural K
+// order: the canonical chain exactly. The chains then join the same pending-subtree tree as above.
+// Workgroup: 64 router rows x 64 tokens, 4 waves of 2 x 2 tiles of 16 x 16; per chain the W and x
+// tiles are staged in LDS (row stride L + 4 floats: the 16 rows x 4 K of an operand read fall in
+// distinct banks), the next chain's tiles loaded into registers during the current one's steps.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+template <int L>
+__global__ void __launch_bounds__(256) k_router_mfma(const float* __restrict__ x, int T, const float* __restrict__ W,
+                                                     const float* __restrict__ gate_w, int E, float* __restrict__ part) {
+    constexpr int LS = L + 4;                  // LDS row stride (floats)
+    constexpr int F4 = L / 4;                  // float4 per row and chain
+    constexpr int NP = (64 * F4 + 255) / 256;  // staging passes
+    __shared__ __align__(16) float sx[2][64 * LS];
+    __shared__ __align__(16) float sw[2][64 * LS];
+    const int E1 = E + (gate_w ? 1 : 0);
+    const int t0 = blockIdx.y * 64, e0 = blockIdx.x * 64, c0 = blockIdx.z * kRgChains;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+    const int wr = (wave & 1) * 32, wc = (wave >> 1) * 32;   // this wave's rows and tokens in the tile
+    const int n = 64 * L;
+    float4 rx[NP], rw[NP];
+    auto load = [&](int c) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const int idx = p * 256 + tid;
+            const int row = idx / F4, q = idx % F4;
+            const int t = min(t0 + row, T - 1), e = e0 + row;
+            const float* wrow = e < E ? W + size_t(e) * n : gate_w;   // row E: the gate vector
+            const bool in = idx < 64 * F4;
+            rx[p] = in ? *reinterpret_cast<const float4*>(x + size_t(t) * n + c * L + q * 4) : make_float4(0, 0, 0, 0);
+            rw[p] = in && e < E1 ? *reinterpret_cast<const float4*>(wrow + c * L + q * 4) : make_float4(0, 0, 0, 0);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const int idx = p * 256 + tid;
+            if (idx >= 64 * F4) continue;
+            const int row = idx / F4, q = idx % F4;
+            *reinterpret_cast<float4*>(&sx[buf][row * LS + q * 4]) = rx[p];
+            *reinterpret_cast<float4*>(&sw[buf][row * LS + q * 4]) = rw[p];
+        }
+    };
+    load(c0);
+    store(0);
+    __syncthreads();
+    f32x4v lv[2][2][kRgLevels];   // pending subtrees of the levels below the split's root
+    f32x4v total[2][2];
+    for (int c = 0; c < kRgChains; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < kRgChains) load(c0 + c + 1);
+        f32x4v ch[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) ch[i][j] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+        const float* aw = &sw[buf][(wr + li) * LS + lg];
+        const float* ax = &sx[buf][(wc + li) * LS + lg];
+#pragma unroll
+        for (int s = 0; s < L / 4; ++s) {
+            const float a0 = aw[4 * s], a1 = aw[16 * LS + 4 * s];
+            const float b0 = ax[4 * s], b1 = ax[16 * LS + 4 * s];
+            ch[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, ch[0][0], 0, 0, 0);
+            ch[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, ch[0][1], 0, 0, 0);
+            ch[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, ch[1][0], 0, 0, 0);
+            ch[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, ch[1][1], 0, 0, 0);
+        }
+        // chain c joins the tree (the same rule as k_router_gemm)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                f32x4v v = ch[i][j];
+                bool parked = false;
+#pragma unroll
+                for (int m = 0; m < kRgLevels; ++m) {
+                    if (parked) continue;
+                    if (((c >> m) & 1) == 0) {
+                        lv[i][j][m] = v;
+                        parked = true;
+                    } else {
+                        v = lv[i][j][m] + v;
+                    }
+                }
+                if (!parked) total[i][j] = v;
+            }
+        if (c + 1 < kRgChains) {
+            store(buf ^ 1);
+            __syncthreads();
+        }
+    }
+    // lane: router rows 4 lg + v of row tile i, token li of token tile j
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int t = t0 + wc + 16 * j + li;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int e = e0 + wr + 16 * i + 4 * lg + v;
+                if (t < T && e < E1) part[(size_t(blockIdx.z) * T + t) * E1 + e] = total[i][j][v];
+            }
+        }
+}
+
 __global__ void __launch_bounds__(256) k_router_combine(const float* __restrict__ part, int T, int E, int E1,
                                                         const float* __restrict__ bias, float* __restrict__ logits,
                                                         float* __restrict__ gate) {
@@ -493,6 +600,8 @@ __global__ void __launch_bounds__(256) k_router_combine(const float* __restrict_
 
 }  // namespace
 
+int g_router_mfma = 1;   // the prefill router GEMM on the matrix cores (0: the VALU kernel)
+
 size_t router_gemm_ws_bytes(int T, int E, bool gate) { return size_t(kRgSplit) * T * (E + (gate ? 1 : 0)) * 4; }
 
 int router_gemm(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
@@ -502,13 +611,24 @@ int router_gemm(const float* x, int T, const float* W, const float* bias, const 
     if (T < 1 || E < 1 || !part || (gate_w && !gate)) return set_error(kErrShape, "router_gemm: T=%d E=%d", T, E);
     const int E1 = E + (gate_w ? 1 : 0);
     dim3 grid((E1 + 63) / 64, (T + 63) / 64, kRgSplit);
-    switch (n / 64) {
-        case 16: k_router_gemm<16><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-        case 32: k_router_gemm<32><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-        case 40: k_router_gemm<40><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-        case 48: k_router_gemm<48><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-        case 64: k_router_gemm<64><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-        default: return set_error(kErrShape, "router_gemm: n=%d", n);
+    if (g_router_mfma) {
+        switch (n / 64) {
+            case 16: k_router_mfma<16><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 32: k_router_mfma<32><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 40: k_router_mfma<40><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 48: k_router_mfma<48><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 64: k_router_mfma<64><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            default: return set_error(kErrShape, "router_gemm: n=%d", n);
+        }
+    } else {
+        switch (n / 64) {
+            case 16: k_router_gemm<16><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 32: k_router_gemm<32><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 40: k_router_gemm<40><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 48: k_router_gemm<48><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 64: k_router_gemm<64><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            default: return set_error(kErrShape, "router_gemm: n=%d", n);
+        }
     }
     FRT_LAUNCHED("router_gemm");
     const size_t N = size_t(T) * E1;

@@ -121,6 +121,15 @@ def router_logits(x, T: int, W, E: int, n: int, logits, bias=None, gate_w=None, 
     check(lib().frt_router_logits(_s(stream), _p(x), T, _p(W), _p(bias), _p(gate_w), E, n, _p(logits), _p(gate)))
 
 
+def router_logits_gemm(x, T: int, W, E: int, n: int, logits, bias=None, gate_w=None, gate=None, stream=None) -> None:
+    """The prefill router (many tokens) as the K-split GEMM on the matrix cores: the same canonical
+    order, bit for bit, as router_logits."""
+    nb = int(lib().frt_router_gemm_workspace_bytes(T, E, 1 if gate_w is not None else 0))
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+    check(lib().frt_router_logits_gemm(_s(stream), _p(x), T, _p(W), _p(bias), _p(gate_w), E, n, _p(logits), _p(gate),
+                                       _p(ws), nb))
+
+
 def quantize_q8(x, rows: int, n: int, xq, xd, stream=None) -> None:
     check(lib().frt_quantize_q8(_s(stream), _p(x), rows, n, _p(xq), _p(xd)))
 

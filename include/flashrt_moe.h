@@ -102,6 +102,13 @@ int frt_moe_route_topk(void* stream, const float* logits, int T, int E, int k, i
 int frt_router_logits(void* stream, const float* x, int T, const float* W, const float* bias, const float* gate_w,
                       int E, int n, float* logits, float* gate);
 
+/* ---- the same router logits for many tokens (a prefill chunk) as a K-split GEMM on the matrix
+ * cores, bit for bit the canonical order of frt_router_logits. n in {1024, 2048, 2560, 3072, 4096};
+ * ws of frt_router_gemm_workspace_bytes(T, E, gate_w != NULL). */
+size_t frt_router_gemm_workspace_bytes(int T, int E, int has_gate);
+int frt_router_logits_gemm(void* stream, const float* x, int T, const float* W, const float* bias, const float* gate_w,
+                           int E, int n, float* logits, float* gate, void* ws, size_t ws_bytes);
+
 /* ---- router / gate tensors in the model's GGUF types, widened to the fp32 layout the router
  * kernels take (the reference reads ffn_gate_inp and ffn_gate_inp_shexp through ggml's linear(),
  * arch/qwen4exp/blocks.hpp:85, in whatever type the file ships). type is the ggml type id:

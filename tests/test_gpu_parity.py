@@ -96,6 +96,32 @@ def test_router_logits_bit_exact(F, T, n, with_bias):
     assert np.array_equal(gt.cpu().numpy(), gref)
 
 
+@pytest.mark.parametrize("T,n,with_bias", [(300, 2048, True), (2048, 2048, False), (70, 2560, True), (64, 1024, False)])
+def test_router_logits_gemm_bit_exact(F, T, n, with_bias):
+    """The prefill router GEMM (K split along the canonical tree; the chains on the matrix cores,
+    whose f32 MFMA accumulates its four products as a chain of fmas in K order) equals the oracle's
+    canonical order bit for bit, and the VALU kernel of the same GEMM equals it too."""
+    E = 512
+    rng = np.random.default_rng(T + n)
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    W = (rng.standard_normal((E, n)) * 0.02).astype(np.float32)
+    g = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    bias = (rng.standard_normal(E)).astype(np.float32) if with_bias else None
+    ref = O.router_logits(x, W, bias)
+    gref = np.array([O.dot_canon(g, x[t]) for t in range(T)], np.float32)
+    for mfma in (1, 0):
+        F.set_option("router_mfma", mfma)
+        try:
+            lg = torch.full((T, E), float("nan"), dtype=torch.float32, device="cuda")
+            gt = torch.full((T,), float("nan"), dtype=torch.float32, device="cuda")
+            F.router_logits_gemm(dev(x), T, dev(W), E, n, lg, bias=None if bias is None else dev(bias), gate_w=dev(g), gate=gt)
+            torch.cuda.synchronize()
+        finally:
+            F.set_option("router_mfma", 1)
+        assert np.array_equal(lg.cpu().numpy(), ref), mfma
+        assert np.array_equal(gt.cpu().numpy(), gref), mfma
+
+
 # ---------------------------------------------------------------- routing
 
 def _route_gpu(F, lg, K, tail_from=1 << 30):
