@@ -46,6 +46,31 @@ __global__ void __launch_bounds__(256) k_pf_hist(const int32_t* __restrict__ ids
     for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[size_t(blockIdx.x) * E + e] = h[e];
 }
 
+// Per expert (a wave each): cnt[b][e] becomes the exclusive prefix over the chunks b' < b (the
+// chunk's first row within the expert's group), rows[e] the group's size. Lane l takes the chunks
+// l P .. l P + P - 1 in order; the lanes' sums are scanned across the wave.
+__global__ void __launch_bounds__(256) k_pf_colscan(int32_t* __restrict__ cnt, int nchunk, int E,
+                                                    int32_t* __restrict__ rows) {
+    const int e = int(blockIdx.x) * 4 + int(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (e >= E) return;   // whole waves
+    const int P = (nchunk + 63) / 64, b0 = lane * P, b1 = min(nchunk, b0 + P);
+    int sum = 0;
+    for (int b = b0; b < b1; ++b) sum += cnt[size_t(b) * E + e];
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    int run = incl - sum;
+    for (int b = b0; b < b1; ++b) {
+        const int v = cnt[size_t(b) * E + e];
+        cnt[size_t(b) * E + e] = run;
+        run += v;
+    }
+    if (lane == 63) rows[e] = incl;
+}
+
 // Exclusive prefix sums over the workgroup of N ints per thread at once (and the totals): a shuffle
 // scan within each wave, then wave 0 scans the wave totals in parallel. ws: (nwaves + 1) * N ints.
 template <int N>
@@ -88,7 +113,7 @@ __device__ __forceinline__ void block_excl_scan_v(const int (&v)[N], int (&r)[N]
     __syncthreads();
 }
 
-// 1024 threads. cnt [nchunk][E] becomes each chunk's first row per expert (absolute).
+// 1024 threads. bounds[e] holds each group's rows (k_pf_colscan) and becomes its first row.
 // Tiles are listed longest first (4 token columns of 16, then 3, 2, 1; by expert within a class),
 // so that the grouped GEMMs start the long tiles first and finish on short ones.
 __device__ __forceinline__ int tile_class(int rows) { return (rows + 15) / 16; }   // 1..4
@@ -105,12 +130,7 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
         n[4] = c / kTN;
         if (c % kTN) ++n[tile_class(c % kTN)];
     };
-    auto group_rows = [&](int e) {
-        int c = 0;
-#pragma unroll 8
-        for (int b = 0; b < nchunk; ++b) c += cnt[size_t(b) * E + e];   // independent loads, 8 in flight
-        return c;
-    };
+    auto group_rows = [&](int e) { return bounds[e]; };   // (k_pf_colscan's group sizes)
     // pass 1: tiles per class over all groups (the shared group E included)
     int total[5] = {0, 0, 0, 0, 0};
     for (int e0 = 0; e0 < E; e0 += blockDim.x) {
@@ -148,23 +168,11 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
             base[k] += tot[k];
         }
         if (e < E) {
-            bounds[e] = off;
+            bounds[e] = off;   // (each thread reads and then writes only its own groups' entries)
             for (int i = 0; i < c / kTN; ++i) tiles[at[4] + i] = make_int2(e, i * kTN);
             if (c % kTN) {
                 const int k = tile_class(c % kTN);
                 tiles[at[k] + (k == 4 ? n[4] - 1 : 0)] = make_int2(e, (c / kTN) * kTN);
-            }
-            int run = off;
-            for (int b0 = 0; b0 < nchunk; b0 += 8) {   // 8 loads in flight, then their prefix
-                int xv[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) xv[u] = b0 + u < nchunk ? cnt[size_t(b0 + u) * E + e] : 0;
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (b0 + u < nchunk) {
-                        cnt[size_t(b0 + u) * E + e] = run;
-                        run += xv[u];
-                    }
             }
         }
         run_rows += tot_rows;
@@ -186,8 +194,8 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
 
 // one wave per chunk; stable ranks from a ballot match-any over the expert id bits
 __global__ void __launch_bounds__(64) k_pf_place(const int32_t* __restrict__ ids, int S, int K, int E, int id_bits,
-                                                 const int32_t* __restrict__ cnt, int32_t* __restrict__ tok_of,
-                                                 int32_t* __restrict__ slot_of, int shared_T) {
+                                                 const int32_t* __restrict__ cnt, const int32_t* __restrict__ bounds,
+                                                 int32_t* __restrict__ tok_of, int32_t* __restrict__ slot_of, int shared_T) {
     extern __shared__ int32_t next[];
     const int lane = threadIdx.x;
     const int nchunk = (S + kChunk - 1) / kChunk;
@@ -199,7 +207,7 @@ __global__ void __launch_bounds__(64) k_pf_place(const int32_t* __restrict__ ids
         }
         return;
     }
-    for (int e = lane; e < E; e += 64) next[e] = cnt[size_t(blockIdx.x) * E + e];
+    for (int e = lane; e < E; e += 64) next[e] = bounds[e] + cnt[size_t(blockIdx.x) * E + e];
     __syncthreads();
     const int s0 = blockIdx.x * kChunk, s1 = min(S, s0 + kChunk);
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -945,10 +953,12 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
     if (int rc = quantize_pairs(x, T, n, pf_np(n), blk, w.xhi, w.xlo, stream)) return rc;
     timing_mark(stream, "pf_quant_x");
     launch_timed("pf_hist", k_pf_hist, dim3(nchunk), dim3(256), size_t(E) * 4, stream, ids, T * K, E, w.cnt);
+    launch_timed("pf_colscan", k_pf_colscan, dim3((E + 3) / 4), dim3(256), 0, stream, w.cnt, nchunk, E, w.bounds);
     launch_timed("pf_scan", k_pf_scan, dim3(1), dim3(1024), 0, stream, w.cnt, nchunk, E, T, K, shared ? 1 : 0, w.bounds,
                  w.tiles, w.n_tiles);
     launch_timed("pf_place", k_pf_place, dim3(nchunk + (shared ? (T + 63) / 64 : 0)), dim3(64), size_t(E) * 4, stream,
-                 ids, T * K, K, E, id_bits, w.cnt, w.tok_of, w.slot_of, shared ? T : 0);
+                 ids, T * K, K, E, id_bits, (const int32_t*)w.cnt, (const int32_t*)w.bounds, w.tok_of, w.slot_of,
+                 shared ? T : 0);
     timing_mark(stream, "pf_dispatch");
     const int mt = pf_max_tiles(S, G);
     int rc = kOk;
@@ -1003,8 +1013,9 @@ int pf_dispatch(const int32_t* ids, int T, int K, int E, int32_t* bounds, int32_
     int id_bits = 1;
     while ((1 << id_bits) < E) ++id_bits;
     k_pf_hist<<<nchunk, 256, size_t(E) * 4, stream>>>(ids, T * K, E, cnt);
+    k_pf_colscan<<<(E + 3) / 4, 256, 0, stream>>>(cnt, nchunk, E, bounds);
     k_pf_scan<<<1, 1024, 0, stream>>>(cnt, nchunk, E, T, K, 0, bounds, tiles, n_tiles);
-    k_pf_place<<<nchunk, 64, size_t(E) * 4, stream>>>(ids, T * K, K, E, id_bits, cnt, tok_of, slot_of, 0);
+    k_pf_place<<<nchunk, 64, size_t(E) * 4, stream>>>(ids, T * K, K, E, id_bits, cnt, bounds, tok_of, slot_of, 0);
     FRT_LAUNCHED("dispatch");
     return kOk;
 }
