@@ -222,7 +222,7 @@ def test_layer_decode_other_expert_counts(F, E, T):
     """Decode routing with other expert counts. Each lane holds V consecutive logits (V = 8 for
     E <= 512, 16 above): E = 128 fills 16 lanes, 300 ends inside a lane (clamped loads, tail past
     E), 1000 and 1024 take the V = 16 selection. T = 1 runs the single-token selection, T = 2 the
-    four-wave one. Ids, weights and output against the oracle (the reference routes any E up to
+    window path's per-token selection (k_win_route). Ids, weights and output against the oracle (the reference routes any E up to
     its kernel's bound, blocks.hpp:130-135)."""
     w = H.World(cfg=0, E=E)
     rng = np.random.default_rng(E + T)
@@ -249,12 +249,20 @@ def test_layer_reference_test_shape(F):
         assert H.out_rel(out, ref) <= H.OUT_REL, T
 
 
-def test_layer_decode_config1_window(F):
+@pytest.mark.parametrize("min_t", [2, 9])
+def test_layer_decode_config1_window(F, min_t):
+    """Config 1 (3 correlated tokens) through the window path (the default) and, with the window
+    path switched off (window_min_t = 9), through the grouped decode kernels (four-wave routing in
+    every gate/up workgroup, the combine lists in k_dec_down)."""
     w1 = H.World(cfg=1)
     xc = torch.empty((3, H.N), dtype=torch.float32, device="cuda")
     F.gen.correlated(xc, 1, 0, O.X_TENSOR, 3, H.N, 0.8)
     x = xc.cpu().numpy()
-    out, ids, wts = w1.gpu_forward(x)
+    F.set_option("window_min_t", min_t)
+    try:
+        out, ids, wts = w1.gpu_forward(x)
+    finally:
+        F.set_option("window_min_t", 2)
     ref, rid, rw, _ = w1.oracle_forward(x)
     assert np.array_equal(ids, rid)
     assert H.w_rel(wts, rw) <= H.W_REL
