@@ -131,12 +131,13 @@ void gen_zipf_bias(uint64_t seed, int cfg, int layer, int E, float s, float alph
 constexpr int kDecodeMaxT = 4;
 
 // moe_hits runs a window in launches of at most hits_chunk(T, K, ff) tokens: 8 (the reference's
-// kMaxWindow) as long as the launch has at most 128 (token, slot) items and its hidden vectors fit in
-// 96 KB of LDS (K <= 12 at ff = 512); each launch reads each of its distinct blobs once per four tokens
+// kMaxWindow) as long as the launch has at most 128 (token, slot) items (K <= 16 for 8 tokens); each
+// launch reads each of its distinct blobs once per four of its tokens
 static int hits_chunk(int T, int K, int ff) {
+    (void)ff;
     int c = 8;
     const int k = K > 0 ? K : 1;
-    while (c > 1 && (c * k > 128 || size_t(c) * (k + 1) * (size_t(ff) + (ff / kQ8) * 4 + 32) > 96 * 1024)) --c;
+    while (c > 1 && c * k > 128) --c;
     return T < c ? T : c;
 }
 // decode-side scratch for moe_hits: x quantized (T rows) ahead of the dec scratch of one chunk
