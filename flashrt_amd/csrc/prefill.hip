@@ -259,7 +259,7 @@ __global__ void __launch_bounds__(64) k_pf_place(const int32_t* __restrict__ ids
 //                  48 KB ring), so two workgroups share a CU and one computes while the other waits
 //                  for its loads; the tile classes of 2-4 token columns (one branch-free variant per
 //                  column count).
-//   SMALL = true:  256 threads, 16 tokens x 128 ff rows, stages of K = 128, for the tiles of one
+//   SMALL = true:  256 threads, 16 tokens x 128 ff rows, stages of K = 256 in a ring of 2, for the tiles of one
 //                  token column (half of them under skewed routing): a quarter of the LDS and of the
 //                  registers, so 4 workgroups share a CU.
 // Every activation fragment read from LDS feeds 4 MFMAs, every dequantized weight fragment NC NP.
@@ -316,12 +316,12 @@ struct GuShape {
     static constexpr int threads = 256;
     static constexpr int tokens = SMALL ? 16 : kTN;       // activation rows in LDS
     static constexpr int ff_rows = threads / 2;           // ff rows per workgroup (32 per wave)
-    static constexpr int stage_k = SMALL ? 128 : 64;      // K per activation stage
+    static constexpr int stage_k = SMALL ? 256 : 64;      // K per activation stage
     static constexpr int sps = 256 / stage_k;             // stages per weight stretch
     static constexpr int ksps = stage_k / 32;             // MFMA K-steps per stage
     static constexpr int cpt = stage_k / 8;               // 16-byte chunks per token per stage
     static constexpr int slot_b = tokens * stage_k * 2;   // bytes per part per slot
-    static constexpr int stages = 3;                      // activation ring slots
+    static constexpr int stages = SMALL ? 2 : 3;          // activation ring slots
     static constexpr int ahead = stages - 1;              // stages issued ahead
     static constexpr int smem = stages * 2 * slot_b;
     static constexpr int dma = tokens * cpt / threads;    // activation loads per lane per part
