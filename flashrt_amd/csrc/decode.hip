@@ -130,7 +130,8 @@ __global__ void __launch_bounds__(512) k_win_route(const float* __restrict__ log
                                                    int32_t* __restrict__ ids, float* __restrict__ wts,
                                                    uint32_t* __restrict__ counts, const uint8_t* __restrict__ arena,
                                                    size_t stride, const uint8_t* __restrict__ shared_blob,
-                                                   DecEntry* __restrict__ ent, int32_t* __restrict__ n_ent) {
+                                                   DecEntry* __restrict__ ent, int32_t* __restrict__ n_ent,
+                                                   int32_t* __restrict__ arrive, int n_groups) {
     __shared__ float cand_v[8][64];
     __shared__ int cand_id[8][64];
     __shared__ int s_ids[8][32];
@@ -139,6 +140,8 @@ __global__ void __launch_bounds__(512) k_win_route(const float* __restrict__ log
     __shared__ int s_wtot[2][2];
     const int wave = int(threadIdx.x) >> 6, lane = int(threadIdx.x) & 63, i = int(threadIdx.x);
     for (int e = i; e <= E; e += 512) s_mask[e] = e == E ? (1u << T) - 1u : 0u;
+    for (int g = i; g < n_groups; g += 512)   // the down kernel's row-group counters
+        __hip_atomic_store(arrive + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (wave < T) {
         const int id = topk_wave<V>(logits + size_t(wave) * E, E, K, ids + size_t(wave) * K, wts + size_t(wave) * K,
@@ -599,10 +602,21 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent_g, const i
 // 16y .. 16y + 15 (4 waves x 4 entries), staging only those entries' hidden vectors (their compact
 // slots are contiguous); no sum across entries, so the entry chunks are independent workgroups.
 constexpr int kHitsDownEnt = 16;
+// A verify window's combine, fused into the down kernel: the last workgroup of a row group to
+// finish (a counter per row group, zeroed by k_win_route) sums that group's rows for every token.
+struct WinComb {
+    int32_t* arrive;        // [n / 8]; null: no combine (moe_hits)
+    const int32_t* ids;     // [T][K] rank order
+    const float* wts;       // [T][K]
+    const float* gate;      // [T] shared-expert gate logits
+    const float* resid;     // [T][n] or null
+    float* out;             // [T][n]
+    int T, K;               // K routed slots per token (the shared expert is slot K)
+};
 template <int NBF>
 __global__ void __launch_bounds__(256) k_hits_down(const DecEntry* __restrict__ ent_g, const int32_t* __restrict__ n_ent,
                                                    const int8_t* __restrict__ hq, const float* __restrict__ hd, int n,
-                                                   int ff, int K, float* __restrict__ yh) {
+                                                   int ff, int K, float* __restrict__ yh, WinComb wc) {
     constexpr int RD = 8;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ DecEntry s_ent[kHitsDownEnt];
@@ -651,53 +665,57 @@ __global__ void __launch_bounds__(256) k_hits_down(const DecEntry* __restrict__ 
         int u = 0;
         while (s_ent[u].base + s_ent[u].ntok <= c) ++u;
         const int j = c - s_ent[u].base;
-        yh[(size_t(s_ent[u].tok[j]) * K + s_ent[u].slot[j]) * n + r0 + rl] = sh_y[(c - c_lo) * RD + rl];
+        float* dst = yh + (size_t(s_ent[u].tok[j]) * K + s_ent[u].slot[j]) * n + r0 + rl;
+        if (wc.arrive) __hip_atomic_store(dst, sh_y[(c - c_lo) * RD + rl], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else *dst = sh_y[(c - c_lo) * RD + rl];
     }
-}
-
-// ---- a verify window of 5 .. 8 tokens through the moe_hits kernels (moe_block_fast's window path,
-// arch/qwen4exp/moe_fast.cu:1015-1108 with T <= kMaxWindow): token t's hit list is its K routed
-// experts' blobs (rank order) and the shared expert's as slot K.
-// out[t] = resid[t] + (sum over the K routed slots in ascending expert id of w * y, from 0) + y_shared *
-// sigmoid(gate[t]) (moe_cpu.cpp:63-80 phase B order; moe_ref.cu:90-97); yh [T][K + 1][n]
-__global__ void __launch_bounds__(256) k_win_combine(const float* __restrict__ yh, const int32_t* __restrict__ ids,
-                                                     const float* __restrict__ wts, const float* __restrict__ gate, int T,
-                                                     int K, int n, const float* __restrict__ resid,
-                                                     float* __restrict__ out) {
-    __shared__ int order[32];
-    const int t = blockIdx.y;
-    if (int(threadIdx.x) < K) {   // rank of slot k by expert id (one token's ids are distinct)
-        const int e = ids[t * K + threadIdx.x];
-        int r = 0;
-        for (int k = 0; k < K; ++k) r += ids[t * K + k] < e ? 1 : 0;
-        order[r] = threadIdx.x;
+    if (!wc.arrive) return;
+    // out[t] = resid[t] + (sum over the routed slots in ascending expert id of w * y, from 0) +
+    // y_shared * sigmoid(gate[t]) (moe_cpu.cpp:63-80 phase B order; moe_ref.cu:90-97), by the row
+    // group's last workgroup. The rows go out as agent-scope stores (to the memory side, past this
+    // XCD's L2), each wave waits for their completion, and only then is the workgroup counted in;
+    // the last one reads the rows with agent-scope loads. (A release / acquire fence pair would write
+    // back and invalidate whole L2s, which costs the following kernels their cached weights.)
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's stores are complete
+    __syncthreads();
+    if (tid == 0) {
+        const int ny = (U + kHitsDownEnt - 1) / kHitsDownEnt;
+        s_last = __hip_atomic_fetch_add(wc.arrive + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ny - 1;
     }
     __syncthreads();
-    const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
-    if (i >= n) return;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int r = 0; r < K; ++r) {
-        const int k = order[r];
-        const float w = wts[t * K + k];
-        const float4 y = *reinterpret_cast<const float4*>(yh + (size_t(t) * (K + 1) + k) * n + i);
-        const float yv[4] = {y.x, y.y, y.z, y.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float p = w * yv[q];
-            acc[q] = acc[q] + p;
+    if (!s_last) return;
+    // (the staging area is free again: every wave has passed the barrier above)
+    float(*s_yc)[33] = reinterpret_cast<float(*)[33]>(smem);   // [token, row][slot]
+    int(*s_order)[32] = reinterpret_cast<int(*)[32]>(smem + sizeof(float) * kDecMaxHitsT * RD * 33);
+    const int Kr = wc.K;
+    // every slot row of the group at once (one memory round trip), parked in LDS
+    for (int i = tid; i < wc.T * RD * (Kr + 1); i += 256) {
+        const int tr = i % (wc.T * RD), k = i / (wc.T * RD), t = tr / RD;
+        s_yc[tr][k] = __hip_atomic_load(yh + (size_t(t) * K + k) * n + r0 + tr % RD, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid < wc.T * Kr) {   // rank of slot k by expert id (one token's ids are distinct)
+        const int t = tid / Kr, k = tid % Kr, e = wc.ids[t * Kr + k];
+        int r = 0;
+        for (int q = 0; q < Kr; ++q) r += wc.ids[t * Kr + q] < e ? 1 : 0;
+        s_order[t][r] = k;
+    }
+    __syncthreads();
+    if (tid < wc.T * RD) {
+        const int t = tid / RD, row = r0 + tid % RD;
+        const float* yc = s_yc[tid];
+        float acc = 0.0f;
+        for (int r = 0; r < Kr; ++r) {
+            const int k = s_order[t][r];
+            const float p = wc.wts[t * Kr + k] * yc[k];
+            acc = acc + p;
         }
+        const float p = yc[Kr] * sigmoidf_(wc.gate[t]);
+        float o = acc + p;
+        if (wc.resid) o = wc.resid[size_t(t) * n + row] + o;
+        wc.out[size_t(t) * n + row] = o;
     }
-    const float g = sigmoidf_(gate[t]);
-    const float4 ys = *reinterpret_cast<const float4*>(yh + (size_t(t) * (K + 1) + K) * n + i);
-    const float sv[4] = {ys.x, ys.y, ys.z, ys.w};
-    float o[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const float p = sv[q] * g;
-        o[q] = acc[q] + p;
-        if (resid) o[q] = resid[size_t(t) * n + i + q] + o[q];
-    }
-    *reinterpret_cast<float4*>(out + size_t(t) * n + i) = make_float4(o[0], o[1], o[2], o[3]);
 }
 
 }  // namespace
@@ -737,17 +755,18 @@ static DecScratch dec_carve(void* base, int T, int K, int ff) {
 }
 
 static int dec_down(const DecScratch& s, int n, int ff, int T, int K, const float* resid, float* out, float* yh,
-                    hipStream_t stream, const float* pf = nullptr, int pf_rows = 0) {
+                    hipStream_t stream, const float* pf = nullptr, int pf_rows = 0, const WinComb& wc = WinComb{}) {
     const int nbf = ff / kBlock;
     const int S = T * (K + 1);                         // compact slots at most (the shared expert's included)
     const int U_max = T * K + 1 < kDecMaxEnt ? T * K + 1 : kDecMaxEnt;   // entries at most
     const size_t smem = size_t(S) * ff + size_t(S) * (ff / kQ8) * 4 + size_t(S) * 8 * 4;
-    const size_t hits_smem = size_t(kHitsDownEnt * kDecMaxT) * (ff + (ff / kQ8) * 4 + 8 * 4);
+    const size_t hits_smem = std::max(size_t(kHitsDownEnt * kDecMaxT) * (ff + (ff / kQ8) * 4 + 8 * 4),
+                                      size_t(kDecMaxHitsT * 8) * 33 * 4 + size_t(kDecMaxHitsT) * 32 * 4);   // (+ the combine's)
 #define FRT_DN(NBFV)                                                                                           \
     case NBFV:                                                                                                 \
         if (yh)                                                                                                \
             launch_timed("dec_down", k_hits_down<NBFV>, dim3(n / 8, (U_max + kHitsDownEnt - 1) / kHitsDownEnt),   \
-                         dim3(256), hits_smem, stream, s.ent, s.n_ent, s.hq, s.hd, n, ff, K, yh);                   \
+                         dim3(256), hits_smem, stream, s.ent, s.n_ent, s.hq, s.hd, n, ff, K, yh, wc);               \
         else if (T == 1)                                                                                       \
             launch_timed("dec_down", k_dec_down<NBFV, false, true>, dim3(n / 8), dim3(256), smem, stream, s.ent,  \
                          s.n_ent, s.comb, s.hq, s.hd, n, ff, T, K, resid, out, yh, U_max, S, pf, pf_rows);          \
@@ -815,8 +834,8 @@ int dec_moe(const float* logits, const float* gate, int T, int E, int K, const u
 // moe_hits (arch/qwen4exp/moe_fast.hpp:134-142): per-slot expert outputs for the window's hit lists,
 // one launch per window of up to kDecMaxHitsT tokens (the reference's kMaxWindow, moe_fast.cu:38),
 // each distinct expert's rows read once per four of its tokens.
-int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const int8_t* xq, const float* xd, int n,
-             int ff, void* scratch, float* yh, hipStream_t stream, int T) {
+static int hits_run(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const int8_t* xq, const float* xd,
+                    int n, int ff, void* scratch, float* yh, hipStream_t stream, int T, const WinComb& wc) {
     if (T < 1 || T > kDecMaxHitsT || K < 1 || K > 32 || T * K > kHitsMaxItems)
         return set_error(kErrShape, "moe_hits: T=%d K=%d (T <= %d, T*K <= %d per launch)", T, K, kDecMaxHitsT, kHitsMaxItems);
     if (int rc = dec_check(1, K, n, ff)) return rc;   // (k_hits_down stages 64 slots: at most 75 KB of LDS)
@@ -835,14 +854,20 @@ int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const i
     }
 #undef FRT_GU
     timing_mark(stream, "dec_gateup");
-    return dec_down(s, n, ff, T, K, nullptr, nullptr, yh, stream);
+    return dec_down(s, n, ff, T, K, nullptr, nullptr, yh, stream, nullptr, 0, wc);
+}
+int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const int8_t* xq, const float* xd, int n,
+             int ff, void* scratch, float* yh, hipStream_t stream, int T) {
+    return hits_run(hit_ptr, hit_n, K, xq, xd, n, ff, scratch, yh, stream, T, WinComb{});
 }
 
 // A verify window (T <= 8) after routing: ids / wts [T][K], gate [T], the window's Q8_0 input ->
 // out [T][n] (+ resid). One moe_hits launch reads each distinct expert once per four of its tokens
-// (arch/qwen4exp/moe_fast.cu:195-355); then the combine. Scratch: dec_window_bytes.
+// (arch/qwen4exp/moe_fast.cu:195-355), and its down kernel's last workgroup per row group combines.
+// Scratch: dec_window_bytes.
 size_t dec_window_bytes(int T, int K, int n, int ff) {
-    return up256(size_t(T) * (K + 1) * 8) + 256 + up256(size_t(T) * (K + 1) * n * 4) + dec_scratch_bytes(T, K + 1, ff);
+    return up256(size_t(T) * (K + 1) * 8) + 256 + up256(size_t(n / 8) * 4) + up256(size_t(T) * (K + 1) * n * 4) +
+           dec_scratch_bytes(T, K + 1, ff);
 }
 int dec_window_fits(int T, int K, int ff) {
     (void)ff;
@@ -854,21 +879,20 @@ int dec_window(const float* logits, int E, int32_t* ids, float* wts, uint32_t* c
     if (!dec_window_fits(T, K, ff) || E < 1 || E > 1024) return set_error(kErrShape, "decode window: T=%d K=%d ff=%d E=%d", T, K, ff, E);
     uint8_t* p = static_cast<uint8_t*>(scratch);
     p += up256(size_t(T) * (K + 1) * 8) + 256;
+    int32_t* arrive = reinterpret_cast<int32_t*>(p);
+    p += up256(size_t(n / 8) * 4);
     float* yh = reinterpret_cast<float*>(p);
     p += up256(size_t(T) * (K + 1) * n * 4);
     const DecScratch s = dec_carve(p, T, K + 1, ff);
     if (E <= 512)
         launch_timed("win_route", k_win_route<8>, dim3(1), dim3(512), 0, stream, logits, T, E, K, ids, wts, counts,
-                     arena, stride, shared_blob, s.ent, s.n_ent);
+                     arena, stride, shared_blob, s.ent, s.n_ent, arrive, n / 8);
     else
         launch_timed("win_route", k_win_route<16>, dim3(1), dim3(512), 0, stream, logits, T, E, K, ids, wts, counts,
-                     arena, stride, shared_blob, s.ent, s.n_ent);
+                     arena, stride, shared_blob, s.ent, s.n_ent, arrive, n / 8);
     FRT_LAUNCHED("decode window routing");
-    if (int rc = dec_hits(nullptr, nullptr, K + 1, xq, xd, n, ff, p, yh, stream, T)) return rc;
-    launch_timed("win_combine", k_win_combine, dim3((n + 1023) / 1024, T), dim3(256), 0, stream, (const float*)yh, ids,
-                 wts, gate, T, K, n, resid, out);
-    FRT_LAUNCHED("decode window combine");
-    return kOk;
+    const WinComb wc{arrive, ids, wts, gate, resid, out, T, K};
+    return hits_run(nullptr, nullptr, K + 1, xq, xd, n, ff, p, yh, stream, T, wc);
 }
 
 }  // namespace frt
