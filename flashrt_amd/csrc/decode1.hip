@@ -99,6 +99,10 @@ __device__ __forceinline__ void wait_words(const uint64_t* base, int count, uint
                 put(int(threadIdx.x) + k * kNT1, uint32_t(v[k]));
                 pend &= ~(1u << k);
             }
+        // a short back-off between polls: the polls of 256 workgroups share the fabric with the weight
+        // loads (measured per token: none 710 us, 2 x 64 cycles 707.5, 8 x 64 cycles 725; two polls
+        // in flight instead of one: 838)
+        if (pend) __builtin_amdgcn_s_sleep(2);
         if (pend && wall_clock64() > deadline) {
             __hip_atomic_store(err, err_val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
