@@ -613,6 +613,41 @@ def test_layer_prefill_graph_replays(F):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("T", [3, 8])
+def test_layer_window_graph_replays(F, T):
+    """A verify window (router, routing and grouping, moe_hits gate/up, the down kernel whose last
+    workgroup per row group combines on a counter that the routing kernel zeroes) captured in a HIP
+    graph replays to the eager result, bit for bit, on three replays with eager work of another
+    window size and synchronizations between them; the eager result meets the oracle's bar."""
+    w1 = H.World(cfg=1)
+    xc = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    F.gen.correlated(xc, 1, 40 + T, O.X_TENSOR, T, H.N, 0.8)
+    x2 = torch.empty((2, H.N), dtype=torch.float32, device="cuda")
+    F.gen.correlated(x2, 1, 50 + T, O.X_TENSOR, 2, H.N, 0.8)
+    lo = w1.layer_obj
+    ws = lo.workspace(T)
+    ref = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    lo.forward(xc, ref, T=T, ws=ws)
+    torch.cuda.synchronize()
+    r, rid, _, _ = w1.oracle_forward(xc.cpu().numpy())
+    assert H.out_rel(ref.cpu().numpy(), r) <= H.OUT_REL
+    out = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    o2 = torch.empty((2, H.N), dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        lo.forward(xc, out, T=T, ws=ws, stream=s)
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), i
+        lo.forward(x2, o2, T=2, ws=ws)   # eager work between the replays, on the same workspace
+        torch.cuda.synchronize()
+
+
 def test_decode_stack_graph_replays(F):
     """Four config 2 decode layers (single token, RMS-normalised input, residual, the next layer's
     router warming) captured in a HIP graph, as the bench runs them: three replays, with eager work
