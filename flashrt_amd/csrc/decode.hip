@@ -398,7 +398,7 @@ __device__ __forceinline__ void gateup_body(const DecEntry& e, int rb, const int
 }
 
 template <int NB>
-__global__ void __launch_bounds__(512, 4) k_dec_gateup(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
+__global__ void __launch_bounds__(512, 2) k_dec_gateup(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
                                                     const int8_t* __restrict__ xq, const float* __restrict__ xd, int n,
                                                     int ff, int8_t* __restrict__ hq, float* __restrict__ hd) {
     __shared__ float hrow[kDecMaxT][32];
