@@ -216,13 +216,13 @@ def test_layer_decode_config0(F, w0):
     assert H.out_rel(out, ref) <= H.OUT_REL
 
 
-@pytest.mark.parametrize("T", [1, 2])
+@pytest.mark.parametrize("T", [1, 2, 8])
 @pytest.mark.parametrize("E", [300, 128, 1000, 1024])
 def test_layer_decode_other_expert_counts(F, E, T):
     """Decode routing with other expert counts. Each lane holds V consecutive logits (V = 8 for
     E <= 512, 16 above): E = 128 fills 16 lanes, 300 ends inside a lane (clamped loads, tail past
-    E), 1000 and 1024 take the V = 16 selection. T = 1 runs the single-token selection, T = 2 the
-    window path's per-token selection (k_win_route). Ids, weights and output against the oracle (the reference routes any E up to
+    E), 1000 and 1024 take the V = 16 selection. T = 1 runs the single-token selection, T = 2 and 8
+    the window path's per-token selection (k_win_route) and its combine in the down kernel. Ids, weights and output against the oracle (the reference routes any E up to
     its kernel's bound, blocks.hpp:130-135)."""
     w = H.World(cfg=0, E=E)
     rng = np.random.default_rng(E + T)
