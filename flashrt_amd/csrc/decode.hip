@@ -397,14 +397,16 @@ __device__ __forceinline__ void gateup_body(const DecEntry& e, int rb, const int
         hd[0] = float(wv[0].x ^ wv[0].y ^ wv[0].z ^ wv[0].w ^ wv[1].x ^ wv[1].y ^ wv[1].z ^ wv[1].w);
 }
 
+// Four waves per workgroup (8 ff rows each): at n <= 2048 three workgroups fit per CU without
+// register spills (12 waves, against 8 for one 8-wave workgroup); wider rows fit two.
 template <int NB>
-__global__ void __launch_bounds__(512, 2) k_dec_gateup(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
+__global__ void __launch_bounds__(256, NB > 32 ? 2 : 3) k_dec_gateup(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
                                                     const int8_t* __restrict__ xq, const float* __restrict__ xd, int n,
                                                     int ff, int8_t* __restrict__ hq, float* __restrict__ hd) {
     __shared__ float hrow[kDecMaxT][32];
     if (int(blockIdx.y) >= *n_ent) return;
     const DecEntry e = ent[blockIdx.y];
-    gateup_body<NB, 8>(e, blockIdx.x, xq, xd, n, ff, hq, hd, hrow);
+    gateup_body<NB, 4>(e, blockIdx.x, xq, xd, n, ff, hq, hd, hrow);
 }
 
 template <int NB, int V, int MT>
@@ -847,7 +849,7 @@ static int hits_run(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, 
     const int nb = n / kBlock;
     dim3 g1(ff / 32, T * K);
 #define FRT_GU(NBV) \
-    case NBV: k_dec_gateup<NBV><<<g1, 512, 0, stream>>>(s.ent, s.n_ent, xq, xd, n, ff, s.hq, s.hd); break;
+    case NBV: k_dec_gateup<NBV><<<g1, 256, 0, stream>>>(s.ent, s.n_ent, xq, xd, n, ff, s.hq, s.hd); break;
     switch (nb) {
         FRT_GU(16) FRT_GU(32) FRT_GU(40) FRT_GU(48) FRT_GU(64)
         default: return set_error(kErrShape, "decode: n=%d unsupported (n/64 in {16,32,40,48,64})", n);
