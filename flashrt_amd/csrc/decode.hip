@@ -132,8 +132,8 @@ __global__ void __launch_bounds__(512) k_win_route(const float* __restrict__ log
                                                    size_t stride, const uint8_t* __restrict__ shared_blob,
                                                    DecEntry* __restrict__ ent, int32_t* __restrict__ n_ent,
                                                    int32_t* __restrict__ arrive, int n_groups) {
-    __shared__ float cand_v[8][64];
-    __shared__ int cand_id[8][64];
+    __shared__ float cand_v[8][128];
+    __shared__ int cand_id[8][128];
     __shared__ int s_ids[8][32];
     __shared__ uint32_t s_mask[1025];   // per expert (and E: the shared one), the tokens that chose it
     __shared__ int s_ent[1025][2];      // per expert, its entries (tokens 0-3 and 4-7 of its list)
@@ -144,8 +144,8 @@ __global__ void __launch_bounds__(512) k_win_route(const float* __restrict__ log
         __hip_atomic_store(arrive + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (wave < T) {
-        const int id = topk_wave<V>(logits + size_t(wave) * E, E, K, ids + size_t(wave) * K, wts + size_t(wave) * K,
-                                    cand_v[wave], cand_id[wave]);
+        const int id = topk_wave_fast<V>(logits + size_t(wave) * E, E, K, ids + size_t(wave) * K,
+                                         wts + size_t(wave) * K, cand_v[wave], cand_id[wave]);
         if (lane < K) {
             s_ids[wave][lane] = id;
             atomicOr(&s_mask[id], 1u << wave);

@@ -287,6 +287,81 @@ __device__ __forceinline__ int topk_wave(const float* __restrict__ l, int E, int
     return sel_id;
 }
 
+// The same selection as topk_wave by ballots in place of the bitonic sort (route1_wave's method):
+// a lower bound on the K-th largest lane maximum (ballot counts over the keys' upper 12 bits) makes
+// every member of the top K a candidate; the candidates, compacted in ascending id, are ranked by
+// logit (ties: lower id first) and scattered by rank. The weights are topk_weight_sel's (the max is
+// the rank-0 logit). More than 64 candidates (heavily tied logits) falls back to topk_wave.
+// cand_v / cand_id: 128 entries each (64 candidates and one junk slot per lane).
+template <int V>
+__device__ __forceinline__ int topk_wave_fast(const float* __restrict__ l, int E, int K, int32_t* ids, float* wts,
+                                              float* cand_v, int* cand_id) {
+    const int lane = threadIdx.x & 63;
+    float v[V];
+    if (E == 64 * V) {
+        const float4* l4 = reinterpret_cast<const float4*>(l + V * lane);
+#pragma unroll
+        for (int i = 0; i < V / 4; ++i) {
+            const float4 q = l4[i];
+            v[4 * i] = q.x;
+            v[4 * i + 1] = q.y;
+            v[4 * i + 2] = q.z;
+            v[4 * i + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = l[min(V * lane + i, E - 1)];   // past E: masked by the keys
+    }
+    uint32_t key[V], mk = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        key[i] = V * lane + i < E ? logit_key(v[i]) : 0u;
+        mk = max(mk, key[i]);
+    }
+    const uint32_t t1 = wave_kth_key_hi(mk, K) << 20;
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) c += int(key[i] != 0u && key[i] >= t1);
+    int C;
+    int pos = wave_excl_scan(c, &C);
+    if (C > 64) return topk_wave<V>(l, E, K, ids, wts, cand_v, cand_id);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {   // branch-free compaction: a non-candidate goes to junk slot 64 + lane
+        const bool is_c = key[i] != 0u && key[i] >= t1;
+        const int slot = is_c ? pos : 64 + lane;
+        cand_v[slot] = v[i];
+        cand_id[slot] = V * lane + i;
+        pos += int(is_c);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    const bool cl = lane < C;
+    const float cv = cl ? cand_v[lane] : 0.0f;
+    const int ci = cl ? cand_id[lane] : 0x7fffffff;
+    int rank = 0;   // candidates ahead: higher logit, or equal and lower id (= lower slot)
+    for (int j = 0; j < C; ++j) {
+        const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), j));
+        rank += int(o > cv || (o == cv && j < lane));
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    if (cl && rank < K) {
+        cand_v[rank] = cv;
+        cand_id[rank] = ci;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    const float sel_l = lane < K ? cand_v[lane] : 0.0f;
+    const int sel_id = lane < K ? cand_id[lane] : 0;
+    const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sel_l), 0));
+    const float w = topk_weight_sel(sel_l, mx, K);
+    if (lane < K) {
+        ids[lane] = sel_id;
+        wts[lane] = w;
+    }
+    return sel_id;
+}
+
 // ---- Top-K of one token by a group of 4 waves (q = 0..3 the wave's index in the group), for
 // latency: the same selection and order as topk_select, with the two ranking passes split over the
 // group. Lane l of every wave loads experts V l .. V l + V - 1 (the same data in all 4 waves).
