@@ -603,7 +603,8 @@ __global__ void __launch_bounds__(256) k_dec_down(const DecEntry* ent_g, const i
 // ---- moe_hits down with per-slot outputs: workgroup (x, y) takes output rows 8x .. 8x + 7 of entries
 // 16y .. 16y + 15 (4 waves x 4 entries), staging only those entries' hidden vectors (their compact
 // slots are contiguous); no sum across entries, so the entry chunks are independent workgroups.
-constexpr int kHitsDownEnt = 16;
+constexpr int kHitsDownEnt = 8;
+constexpr int kHitsBatch = kHitsDownEnt / 4;   // entries per wave
 // A verify window's combine, fused into the down kernel: the last workgroup of a row group to
 // finish (a counter per row group, zeroed by k_win_route) sums that group's rows for every token.
 struct WinComb {
@@ -643,8 +644,8 @@ __global__ void __launch_bounds__(256) k_hits_down(const DecEntry* __restrict__ 
     for (int k = 0; k < 4; ++k) vq[k] = srcq[min(tid + 256 * k, nq - 1)];
 #pragma unroll
     for (int k = 0; k < 2; ++k) vd[k] = srcd[min(tid + 256 * k, nd - 1)];
-    DownRegs<NBF, 4> R;
-    down_load<NBF, 4>(eg, nu, wave, r0, n, ff, R);
+    DownRegs<NBF, kHitsBatch> R;
+    down_load<NBF, kHitsBatch>(eg, nu, wave, r0, n, ff, R);
     __builtin_amdgcn_sched_barrier(0);
     if (tid < nu * int(sizeof(DecEntry) / 4))
         reinterpret_cast<int32_t*>(s_ent)[tid] = reinterpret_cast<const int32_t*>(eg)[tid];
@@ -659,7 +660,7 @@ __global__ void __launch_bounds__(256) k_hits_down(const DecEntry* __restrict__ 
     for (int i = tid + 512; i < nd; i += 256) sh_d[i] = srcd[i];
     __syncthreads();
     // entries indexed locally, slots globally: the LDS arrays are offset by the chunk's first slot
-    down_compute<NBF, 4>(s_ent, nu, wave, R, sh_q - size_t(c_lo) * ff, sh_d - size_t(c_lo) * (ff / kQ8),
+    down_compute<NBF, kHitsBatch>(s_ent, nu, wave, R, sh_q - size_t(c_lo) * ff, sh_d - size_t(c_lo) * (ff / kQ8),
                          sh_y - size_t(c_lo) * RD, ff);
     __syncthreads();
     for (int i = tid; i < nc * RD; i += 256) {
