@@ -316,15 +316,17 @@ def run_windows(args, F, torch, st):
 # ---------------------------------------------------------------- CPU baseline
 
 def _host_cpus():
-    """(CPUs in this process's affinity mask, physical cores among them, the CPU model name)."""
+    """(CPUs in this process's affinity mask, one logical CPU per physical core among them, the
+    CPU model name)."""
     cpus = sorted(os.sched_getaffinity(0))
-    cores = set()
+    cores = {}
     for c in cpus:
         try:
             with open(f"/sys/devices/system/cpu/cpu{c}/topology/thread_siblings_list") as f:
-                cores.add(f.read().strip())
+                key = f.read().strip()
         except OSError:
-            cores.add(str(c))
+            key = str(c)
+        cores.setdefault(key, c)
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -334,7 +336,7 @@ def _host_cpus():
                     break
     except OSError:
         pass
-    return len(cpus), len(cores), model
+    return len(cpus), sorted(cores.values()), model
 
 
 def cpu_baseline(args, F, torch, stack):
@@ -360,7 +362,8 @@ def cpu_baseline(args, F, torch, stack):
     gw = gate[:nl].cpu().numpy()
     bh = bias[:nl].cpu().numpy()
     host_np = host.numpy()
-    n_aff, n_phys, model = _host_cpus()
+    n_aff, phys, model = _host_cpus()
+    n_phys = len(phys)
     kind = "reference" if O.have_ref() else "port"
     R = O.ref() if O.have_ref() else None
     rng_x = O.gen_normal(2, 0, O.X_TENSOR, 64 * N).reshape(64, N)
@@ -371,7 +374,11 @@ def cpu_baseline(args, F, torch, stack):
         threadpool_limits = None
 
     def sample(workers, seconds):
-        pool = R.ref_pool_create(workers, 0) if R else None
+        # the pool pinned to one logical CPU per physical core, as the reference's bench pins it
+        # (to the cores this process may use); the caller thread is pinned too and restored after
+        saved_aff = os.sched_getaffinity(0)
+        pin = (C.c_int * len(phys))(*phys)
+        pool = R.ref_pool_create_cpus(workers, pin, len(phys)) if R else None
         # numpy's BLAS threads stay at one: idle BLAS workers spinning beside the pool's would steal its cores
         limiter = threadpool_limits(1) if threadpool_limits else None
         route_times, moe_times = [], []
@@ -418,22 +425,26 @@ def cpu_baseline(args, F, torch, stack):
                 limiter.unregister()
             if pool:
                 R.ref_pool_destroy(pool)
+            os.sched_setaffinity(0, saved_aff)
         t_layer = float(np.median([a + b for a, b in zip(route_times, moe_times)]))
         return dict(workers=workers, tokens=steps, us_per_layer=round(t_layer * 1e6, 1),
                     route_us=round(float(np.median(route_times)) * 1e6, 1),
                     moe_cpu_us=round(float(np.median(moe_times)) * 1e6, 1),
                     moe_cpu_GBps=round(11 * F.expert_bytes(N, FF) / float(np.median(moe_times)) / 1e9, 2),
-                    tokens_per_s=round(1.0 / (LAYERS * t_layer), 2))
+                    tokens_per_s=round(1.0 / (LAYERS * t_layer), 2),
+                    moe_cpu_tokens_per_s=round(1.0 / (LAYERS * float(np.median(moe_times))), 2))
 
     full = sample(n_phys, args.cpu_seconds)
     eight = sample(8, args.cpu_seconds / 2)
     what = "the reference moe_cpu (AVX-512 VNNI) on its CpuPool" if R else "the oracle's moe_cpu restatement"
     return dict(value=full["tokens_per_s"], unit="tokens/s", cores=n_phys, kind=kind, cpu_model=model,
+                moe_cpu_only_tokens_per_s=full["moe_cpu_tokens_per_s"], pinned=bool(R),
                 sample=(f"{full['tokens']} tokens x {nl} of {LAYERS} layers of configs[2] on the host CPU "
                         f"({model}; {n_aff} CPUs in this process's affinity mask, {n_phys} physical cores): RMS norm "
                         f"+ numpy fp32 router + top-10 on one thread (median {full['route_us']:.0f} us), then {what} with "
-                        f"{n_phys} workers over the 10 routed + shared experts (median {full['moe_cpu_us']:.0f} us); "
-                        f"median {full['us_per_layer']:.0f} us/layer x {LAYERS} layers"),
+                        f"{n_phys} workers pinned one per physical core over the 10 routed + shared experts (median "
+                        f"{full['moe_cpu_us']:.0f} us); median {full['us_per_layer']:.0f} us/layer x {LAYERS} layers; "
+                        f"moe_cpu alone {full['moe_cpu_tokens_per_s']:.1f} tokens/s"),
                 all_cores=full, workers_8=eight)
 
 
@@ -464,6 +475,9 @@ def main():
     ap.add_argument("--window-reps", type=int, default=8, help="replays of the 48-call graph per window size")
     ap.add_argument("--no-mixed", action="store_true", help="skip configs[4]")
     ap.add_argument("--decode-grid", type=int, default=0, help="workgroups of a persistent decode call (0: one per CU)")
+    ap.add_argument("--decode-xcd", type=int, default=0,
+                    help="1: persistent single-token calls split each layer by XCD (decode2.hip) where the shape "
+                         "fits; 0: the single-grid persistent kernel (decode1.hip)")
     ap.add_argument("--decode-path", choices=["stack", "fused", "three"], default="stack",
                     help="the 48 layers as one persistent launch (stack, default), one persistent launch per layer "
                          "(fused), or three kernels per layer (three)")
@@ -492,6 +506,7 @@ def main():
     F.set_option("decode_fused", 0 if args.decode_path == "three" else 1)
     F.set_option("window_min_t", args.window_min_t)
     F.set_option("decode_grid", args.decode_grid)
+    F.set_option("decode_xcd", args.decode_xcd)
     st = run_stack(args, F, torch)
     if st["sync_error"]:
         sys.exit("bench.py: a persistent decode call ran out of time waiting for another workgroup")
@@ -503,17 +518,25 @@ def main():
 
     # roofline of the dominant decode kernel
     kt = st["kernels"]
-    per_launch_bytes = {   # algorithmic HBM bytes per launch (weights read once; activations are KB)
-        "dec1_stack": args.layers * ((K + 1) * F.expert_bytes(N, FF) + E * N * 4 + N * 4),
-        "dec1_layer": (K + 1) * F.expert_bytes(N, FF) + E * N * 4 + N * 4,
+    # algorithmic bytes per launch: the expert weights each launch reads once ((K + 1) blobs per
+    # token and layer); the router matrices are reported beside them (frac_with_router), not in them
+    router_layer = E * N * 4 + N * 4
+    per_launch_bytes = {
+        "dec1_stack": args.layers * (K + 1) * F.expert_bytes(N, FF),
+        "dec2_stack": args.layers * (K + 1) * F.expert_bytes(N, FF),
+        "dec1_layer": (K + 1) * F.expert_bytes(N, FF),
+        "dec2_layer": (K + 1) * F.expert_bytes(N, FF),
         "dec_route_gateup": (K + 1) * 2 * F.lib().frt_q2_mat_bytes(FF, N),
         "dec_down": (K + 1) * F.lib().frt_q2_mat_bytes(N, FF),
-        "router_quant": E * N * 4 + N * 4,
+        "router_quant": 0,
     }
+    router_bytes = {"dec1_stack": args.layers * router_layer, "dec2_stack": args.layers * router_layer,
+                    "dec1_layer": router_layer, "dec2_layer": router_layer, "router_quant": router_layer}
     dom = max(kt, key=lambda k: kt[k][0])
     dom_avg_ms = kt[dom][0] / kt[dom][1]
     dom_bytes = per_launch_bytes.get(dom)
     achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9 if dom_bytes else None
+    achieved_wr = (dom_bytes + router_bytes.get(dom, 0)) / (dom_avg_ms * 1e-3) / 1e9 if dom_bytes else None
     kernels = {k: dict(avg_us=round(v[0] / v[1] * 1e3, 2), launches=v[1],
                        share=round(v[0] / sum(x[0] for x in kt.values()), 3)) for k, v in kt.items()}
     for k, b in per_launch_bytes.items():
@@ -546,7 +569,9 @@ def main():
                    "global_batch": 1, "seq_len": 1, "parallelism": "none (one GPU)"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1) if achieved else None,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None, "traffic": traffic},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None, "traffic": traffic,
+                     "algo_bytes": dom_bytes, "avg_us": round(dom_avg_ms * 1e3, 2),
+                     "frac_with_router": round(achieved_wr / HBM_PEAK_GBS, 4) if achieved_wr else None},
         "stack": {"expert_bytes_per_token": expert_bytes_tok, "router_bytes_per_token": router_bytes_tok,
                   "expert_TBps": round(stack_tbs, 3), "expert_hbm_frac": round(stack_tbs * 1e3 / HBM_PEAK_GBS, 4),
                   "expert_plus_router_hbm_frac": round((expert_bytes_tok + router_bytes_tok) / (ms * 1e-3) / 1e9
@@ -561,7 +586,18 @@ def main():
                 "mfma": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                          for k, v in pf.util.items()}}
     if not args.no_prefill:
-        line["prefill_2k"] = pf_entry(run_prefill(args, F, torch))
+        pf = run_prefill(args, F, torch)
+        line["prefill_2k"] = pf_entry(pf)
+        # the prefill roofline: expert flops over the grouped GEMM kernels' summed average durations
+        parts = [p for p in ("pf_gateup", "pf_gateup1", "pf_down") if p in pf.kernels]
+        if parts:
+            gemm_ms = sum(pf.kernels[p][0] / pf.kernels[p][1] for p in parts)
+            tf = pf.flops / (gemm_ms * 1e-3) / 1e12
+            line["roofline_prefill"] = {"bound": "mfma", "kernels": parts, "achieved": round(tf, 1),
+                                        "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                        "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "avg_us": round(gemm_ms * 1e3, 2),
+                                        "flops": pf.flops, "frac_layer": round(pf.flops / (pf.ms * 1e-3) / 1e12
+                                                                               / MFMA_F16_PEAK_TFLOPS, 4)}
     if not args.no_mixed:
         line["mixed_cfg4"] = pf_entry(run_mixed(args, F, torch))
     if not args.no_windows:

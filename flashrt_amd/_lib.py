@@ -51,6 +51,7 @@ SIGNATURES = {
     "frt_moe_stack_workspace_bytes": (_sz, [_vp, _i]),
     "frt_moe_stack_forward": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "frt_moe_layer_sync_error": (_i, [_vp, _vp]),
+    "frt_noalloc_sync_error": (_i, [_vp]),
     "frt_gen_experts": (_i, [_u64, _i, _i, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
     "frt_gen_normal": (_i, [_u64, _i, _i, _i, _f, _vp, _sz, _i, _vp]),
     "frt_gen_correlated": (_i, [_u64, _i, _i, _i, _i, _i, _f, _vp, _vp]),

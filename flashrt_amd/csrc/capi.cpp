@@ -105,6 +105,18 @@ int layer_trace(const float* lg, int ls, const int32_t* ids, int T, int E, int K
                 float* probs, hipStream_t stream);
 int dec1_stack(const frt_moe_layer* L, int n_layer, const float* x, float* out, int32_t* ids, float* wts,
                void* sync_ws, hipStream_t stream);
+int dec1_take_timeout();
+// decode2.hip
+int dec2_support(int E, int K, int n, int ff, int n_layer);
+int dec2_layer(const float* x, const float* W, const float* bias, const float* gate_w, int E, int K,
+               const uint8_t* arena, size_t stride, const uint8_t* shared, int n, int ff, int norm, const float* resid,
+               float* out, int32_t* ids, float* wts, uint32_t* counts, void* sync_ws, const float* next_w,
+               hipStream_t stream);
+int dec2_stack(const frt_moe_layer* L, int n_layer, const float* x, float* out, int32_t* ids, float* wts,
+               void* sync_ws, hipStream_t stream);
+extern int g_dec2_on;
+extern uint64_t* g_dec2_stamps;
+extern thread_local bool g_dec1_no_alloc;
 extern int g_dec1_on;
 extern uint64_t g_dec1_ticks;
 extern int g_dec1_grid_cap;
@@ -185,12 +197,16 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
     w.gate = reinterpret_cast<float*>(take(size_t(T) * 4));
     w.ids = reinterpret_cast<int32_t*>(take(size_t(T) * K * 4));
     w.wts = reinterpret_cast<float*>(take(size_t(T) * K * 4));
-    const bool win = window_path(L, T);
-    const bool dec = !win && T <= kDecodeMaxT && T * K <= 63;
-    if (dec || win) {
+    // the decode window paths a call of T tokens can take, whatever "window_min_t" is set to: the
+    // workspace holds the larger of their layouts, so a size queried once stays valid after the option
+    // changes (both carve xq and xd first, then their own scratch)
+    const bool dec_ok = T <= kDecodeMaxT && T * K <= 63;
+    const bool win_ok = T <= 8 && dec_window_fits(T, K, ff) && router_fused_fits(T, n) && dec_check(1, K, n, ff) == kOk;
+    if (dec_ok || win_ok) {
         w.xq = reinterpret_cast<int8_t*>(take(size_t(T) * n));
         w.xd = reinterpret_cast<float*>(take(size_t(T) * (n / kQ8) * 4));
-        w.rest_bytes = dec ? dec_scratch_bytes(T, K, ff) : dec_window_bytes(T, K, n, ff);
+        const size_t db = dec_ok ? dec_scratch_bytes(T, K, ff) : 0, wb = win_ok ? dec_window_bytes(T, K, n, ff) : 0;
+        w.rest_bytes = db > wb ? db : wb;
     } else {
         if (L.flags & FRT_LAYER_NORM_INPUT) w.u = reinterpret_cast<float*>(take(size_t(T) * n * 4));
         w.part = reinterpret_cast<float*>(take(router_gemm_ws_bytes(T, E, true)));
@@ -403,6 +419,7 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     if (!L || !x || !out || !ws) return set_error(kErrNull, "moe_layer: null pointer");
     if (!L->experts || !L->shared || !L->router_w || !L->gate_w) return set_error(kErrNull, "moe_layer: layer weights missing");
     if (T < 1) return set_error(kErrShape, "moe_layer: T=%d", T);
+    if (int rc = dec1_take_timeout()) return rc;
     const int E = L->n_expert, K = L->top_k, n = L->d_model, ff = L->d_ff;
     if (E < 1 || E > 1024 || K < 1 || K > 32 || K > E) return set_error(kErrShape, "moe_layer: E=%d K=%d", E, K);
     if (L->stride < expert_bytes(n, ff)) return set_error(kErrShape, "moe_layer: stride %zu < blob %zu", L->stride, expert_bytes(n, ff));
@@ -413,6 +430,9 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     float* wts_o = wts ? wts : w.wts;
     const int norm = (L->flags & FRT_LAYER_NORM_INPUT) ? 1 : 0;
     timing_mark(s, "begin");
+    if (T == 1 && g_dec1_on && dec2_support(E, K, n, ff, 1))   // one persistent launch, joins split by XCD
+        return dec2_layer(x, L->router_w, L->router_bias, L->gate_w, E, K, L->experts, L->stride, L->shared, n, ff,
+                          norm, resid, out, ids_o, wts_o, counts, w.sync, L->next_router_w, s);
     if (T == 1 && g_dec1_on && dec1_support(E, K, n, ff) >= 1)   // the whole layer in one persistent launch
         return dec1_layer(x, L->router_w, L->router_bias, L->gate_w, E, K, L->experts, L->stride, L->shared, n, ff,
                           norm, resid, out, ids_o, wts_o, counts, w.sync, L->next_router_w, s);
@@ -465,7 +485,19 @@ int frt_moe_layer_forward_noalloc(const frt_moe_layer* L, const float* x, int T,
                                         "scratch holds %zu", need, kNoAllocScratchBytes);
     void* p = nullptr;
     if (int rc = scratch_ptr(&p)) return rc;
+    struct NoAllocScope {   // the persistent path then allocates nothing (no host time-out flag)
+        NoAllocScope() { g_dec1_no_alloc = true; }
+        ~NoAllocScope() { g_dec1_no_alloc = false; }
+    } scope;
     return frt_moe_layer_forward(L, x, T, resid, out, ids, wts, counts, p, kNoAllocScratchBytes, stream);
+}
+
+int frt_noalloc_sync_error(void* stream) {
+    void* p = nullptr;
+    if (int rc = scratch_ptr(&p)) return rc;
+    uint32_t err = 0;
+    if (int rc = dec1_status(p, static_cast<hipStream_t>(stream), &err)) return rc;
+    return err ? 1 : 0;
 }
 
 size_t frt_moe_stack_workspace_bytes(const frt_moe_layer* layers, int n_layer) {
@@ -477,6 +509,7 @@ int frt_moe_stack_forward(const frt_moe_layer* layers, int n_layer, const float*
                           float* wts, void* ws, size_t ws_bytes, void* stream) {
     if (!layers || !x || !out || !ws) return set_error(kErrNull, "moe_stack: null pointer");
     if (n_layer < 1) return set_error(kErrShape, "moe_stack: n_layer=%d", n_layer);
+    if (int rc = dec1_take_timeout()) return rc;
     const frt_moe_layer& L0 = layers[0];
     for (int l = 0; l < n_layer; ++l) {
         const frt_moe_layer& Ll = layers[l];
@@ -496,6 +529,18 @@ int frt_moe_stack_forward(const frt_moe_layer* layers, int n_layer, const float*
                      reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + lw + up256(size_t(n) * 4))};
     constexpr int kChunk = 64;   // layers of one persistent launch
     const float* cur = x;
+    if (g_dec1_on && dec2_support(E, K, n, ff, 2)) {
+        const LayerWs w = layer_carve(ws, L0, 1, ws_bytes);
+        for (int l0 = 0, c = 0; l0 < n_layer; l0 += kChunk, ++c) {
+            const int nl = n_layer - l0 < kChunk ? n_layer - l0 : kChunk;
+            float* dst = l0 + nl == n_layer ? out : buf[c % 2];
+            if (int rc = dec2_stack(layers + l0, nl, cur, dst, ids ? ids + size_t(l0) * K : nullptr,
+                                    wts ? wts + size_t(l0) * K : nullptr, w.sync, s))
+                return rc;
+            cur = dst;
+        }
+        return kOk;
+    }
     if (g_dec1_on && dec1_support(E, K, n, ff) == 2) {
         const LayerWs w = layer_carve(ws, L0, 1, ws_bytes);
         for (int l0 = 0, c = 0; l0 < n_layer; l0 += kChunk, ++c) {
@@ -522,6 +567,14 @@ int frt_set_option(const char* name, int64_t value) {
     if (!name) return set_error(kErrNull, "set_option: null name");
     if (!std::strcmp(name, "decode_fused")) {
         g_dec1_on = value ? 1 : 0;
+        return kOk;
+    }
+    if (!std::strcmp(name, "decode_stamps")) {   // (a device buffer of 64 x 12 x 1024 words, or 0)
+        g_dec2_stamps = reinterpret_cast<uint64_t*>(uintptr_t(value));
+        return kOk;
+    }
+    if (!std::strcmp(name, "decode_xcd")) {
+        g_dec2_on = value ? 1 : 0;
         return kOk;
     }
     if (!std::strcmp(name, "decode_grid")) {
@@ -562,7 +615,8 @@ int frt_moe_layer_forward_ex(const frt_moe_layer* L, const float* x, int T, cons
     const LayerWs w = layer_carve(ws, *L, T, ws_bytes);
     const float* lg = w.logits;
     int ls = 1;
-    if (T == 1 && g_dec1_on && dec1_support(E, K, n, ff) >= 1) lg = dec1_logits(w.sync, &ls);   // the persistent call's
+    if (T == 1 && g_dec1_on && (dec2_support(E, K, n, ff, 1) || dec1_support(E, K, n, ff) >= 1))
+        lg = dec1_logits(w.sync, &ls);   // the persistent call's (both kernels keep them in the same words)
     return layer_trace(lg, ls, ids ? ids : w.ids, T, E, K, tail_counts, tail_from, probs, static_cast<hipStream_t>(stream));
 }
 

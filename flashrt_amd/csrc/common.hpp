@@ -43,6 +43,7 @@ enum Status : int {
     kErrHip = -3,         // a HIP call failed
     kErrNull = -4,        // required pointer missing
     kErrIo = -5,          // a file could not be read
+    kErrSync = -6,        // an earlier persistent call ran out of time waiting for another workgroup
 };
 
 // Records the message of the last failure (thread-local) and returns code.

@@ -876,7 +876,8 @@ size_t dec_window_bytes(int T, int K, int n, int ff) {
 }
 int dec_window_fits(int T, int K, int ff) {
     (void)ff;
-    return T >= 1 && T <= kDecMaxHitsT && T * (K + 1) <= kHitsMaxItems;
+    // (the window path runs moe_hits over K + 1 slots per token, the shared expert last: K + 1 <= 32)
+    return T >= 1 && T <= kDecMaxHitsT && K + 1 <= 32 && T * (K + 1) <= kHitsMaxItems;
 }
 int dec_window(const float* logits, int E, int32_t* ids, float* wts, uint32_t* counts, const float* gate, int T, int K,
                const uint8_t* arena, size_t stride, const uint8_t* shared_blob, const int8_t* xq, const float* xd, int n,

@@ -42,6 +42,7 @@ struct FrtOpaqueTid {
 };
 #define threadIdx (FrtOpaqueTid{})
 #include "decode_parts.hpp"
+#include "persist.hpp"
 
 #include "../../include/flashrt_moe.h"
 
@@ -52,77 +53,17 @@ struct FrtOpaqueTid {
 
 namespace frt {
 
-constexpr int kMaxGrid = 1024;
 // Words between two published words of the logits, h blocks and x: every workgroup polls every
 // word, pollers of one line queue on it, and more lines mean more requests (measured: 4 / 1 / 1).
 constexpr int kLgStride = 4;
 constexpr int kHbStride = 1;
 constexpr int kXbStride = 1;
-constexpr uint32_t kErrMagic = 0x5E7C0DE5u;   // upper half of a set error word (garbage rarely matches)
-struct Dec1Sync {
-    uint64_t err;                // (kErrMagic << 32) | epoch of a call whose wait ran out of time; else anything
-    uint32_t pad[62];
-    uint32_t epoch[kMaxGrid];    // per workgroup: its last call's epoch
-};
 
 namespace {
 
-constexpr int kNT1 = 512;          // threads per workgroup
+constexpr int kNT1 = kNTP;         // threads per workgroup
 constexpr int kNW1 = kNT1 / 64;    // waves per workgroup
 constexpr int kMaxHWords = 8 * kNT1;   // h words one call can publish (8 per thread to wait for)
-
-__device__ __forceinline__ uint32_t sync_tag(uint32_t e) { return (e * 0x9E3779B1u) ^ 0x7F4A7C15u; }
-__device__ __forceinline__ void pub(uint64_t* p, uint32_t tag, uint32_t v) {
-    __hip_atomic_store(p, (uint64_t(tag) << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t peek(const uint64_t* p) {
-    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Waits for the tagged words i = threadIdx.x + k kNT1 < count (k < MAXK), word i at base + i STRIDE,
-// and hands each payload to put(i, payload). Out of time: sets the error word (err_val) and hands
-// over what it last read.
-template <int MAXK, int STRIDE = 1, class F>
-__device__ __forceinline__ void wait_words(const uint64_t* base, int count, uint32_t tag, uint64_t deadline,
-                                           uint64_t* err, uint64_t err_val, F put) {
-    uint32_t pend = 0;
-#pragma unroll
-    for (int k = 0; k < MAXK; ++k)
-        if (int(threadIdx.x) + k * kNT1 < count) pend |= 1u << k;
-    while (pend) {
-        uint64_t v[MAXK];
-#pragma unroll
-        for (int k = 0; k < MAXK; ++k) v[k] = ((pend >> k) & 1u) ? peek(base + size_t(threadIdx.x + k * kNT1) * STRIDE) : 0ull;
-#pragma unroll
-        for (int k = 0; k < MAXK; ++k)
-            if (((pend >> k) & 1u) && uint32_t(v[k] >> 32) == tag) {
-                put(int(threadIdx.x) + k * kNT1, uint32_t(v[k]));
-                pend &= ~(1u << k);
-            }
-        // a short back-off between polls: the polls of 256 workgroups share the fabric with the weight
-        // loads (measured per token: none 710 us, 2 x 64 cycles 707.5, 8 x 64 cycles 725; two polls
-        // in flight instead of one: 838)
-        if (pend) __builtin_amdgcn_s_sleep(2);
-        if (pend && wall_clock64() > deadline) {
-            __hip_atomic_store(err, err_val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-            for (int k = 0; k < MAXK; ++k)
-                if ((pend >> k) & 1u) put(int(threadIdx.x) + k * kNT1, uint32_t(v[k]));
-            break;
-        }
-    }
-}
-
-
-constexpr int kMaxStack = 64;   // layers of one stack call (their table travels in the kernel arguments)
-
-struct Dec1Layer {
-    const float* W;        // [E][n] router
-    const float* bias;     // [E] or null
-    const float* gate_w;   // [n] shared-expert gate
-    const uint8_t* arena;  // routed expert 0 of the layer
-    const uint8_t* shared;
-};
 
 struct Dec1Args {
     Dec1Layer lay[kMaxStack];
@@ -140,6 +81,7 @@ struct Dec1Args {
     uint64_t* hb;          // [U * ff/32][9] tagged h blocks: 8 words of 4 codes, then the scale
     const float* next_w;   // the next layer's router [E][n] (cache warming) or null
     uint64_t ticks;        // bound of the call's waits, in ticks of the 100 MHz constant clock
+    uint32_t* host_err;    // host-visible flag set with the error word (pinned host memory), or null
     int E, K, ff, norm;
 };
 
@@ -236,7 +178,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
     if (l > 0) {   // x_l from the previous layer's down rows
         load_router(LY);   // rows warmed into this XCD's L2 by the previous layer: they land during the wait
         __syncthreads();   // the previous combine has read xs
-        wait_words<(64 * 64 + kNT1 - 1) / kNT1, kXbStride>(a.xb, n, tag, deadline, &a.sync->err, err_val,
+        wait_words<(64 * 64 + kNT1 - 1) / kNT1, kXbStride>(a.xb, n, tag, deadline, &a.sync->err, err_val, a.host_err,
                                                 [&](int i, uint32_t p) { xs[(i / L) * (L + 1) + i % L] = __uint_as_float(p); });
         __syncthreads();
     }
@@ -299,7 +241,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
     }
 
     // ---- 2. all logits, the routing, gate/up
-    wait_words<(1024 + 1 + kNT1 - 1) / kNT1, kLgStride>(a.lg, E + 1, tag, deadline, &a.sync->err, err_val,
+    wait_words<(1024 + 1 + kNT1 - 1) / kNT1, kLgStride>(a.lg, E + 1, tag, deadline, &a.sync->err, err_val, a.host_err,
                                             [&](int i, uint32_t p) { s_lg[i] = __uint_as_float(p); });
     __syncthreads();
     if (wave == 0) {
@@ -500,7 +442,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
 #pragma unroll
         for (int i = 0; i < L / 4; ++i) nv[i] = w4[i];
     }
-    wait_words<kMaxHWords / kNT1, kHbStride>(a.hb, NU * 9, tag, deadline, &a.sync->err, err_val, [&](int i, uint32_t p) {
+    wait_words<kMaxHWords / kNT1, kHbStride>(a.hb, NU * 9, tag, deadline, &a.sync->err, err_val, a.host_err, [&](int i, uint32_t p) {
         const int q = i / 9, part = i % 9, u = q / RB, rb = q % RB;
         if (part < 8) *reinterpret_cast<uint32_t*>(sh_q + size_t(u) * ff + rb * 32 + 4 * part) = p;
         else sh_d[u * (ff / kQ8) + rb] = __uint_as_float(p);
@@ -566,11 +508,12 @@ __global__ void k_dec1_zero(uint64_t* p, size_t words) {
 
 // The sync region at the front of every layer workspace: the error word and the epoch cells, then
 // the tagged words (sized for the largest eligible call: E <= 1024, 4096 h words).
-constexpr size_t kDec1Head = (sizeof(Dec1Sync) + 255) / 256 * 256;
-constexpr size_t kDec1Lg = size_t(1024 + 1 + 31) / 32 * 32 * 8 * 16;   // room for any logit stride up to 16
+constexpr size_t kDec1Head = kSyncHead;
+constexpr size_t kDec1Lg = kSyncLg;   // room for any logit stride up to 16
 constexpr size_t kDec1Hb = size_t(kMaxHWords) * 8 * kHbStride;
 constexpr size_t kDec1Xb = size_t(64 * 64) * 8 * kXbStride;   // a stack's next-layer input, n <= 4096
-size_t dec1_sync_bytes() { return kDec1Head + kDec1Lg + kDec1Hb + kDec1Xb; }
+// (decode2.hip's words follow the logits in the same region; both kernels share the epoch cells)
+size_t dec1_sync_bytes() { return kDec1Head + kDec1Lg + (kDec1Hb + kDec1Xb > kD2Tail ? kDec1Hb + kDec1Xb : kD2Tail); }
 
 int dec1_eligible(int E, int K, int n, int ff) {
     const int nb = n / 64, nbf = ff / 64;
@@ -588,6 +531,60 @@ std::mutex g_dec1_mu;
 std::set<std::pair<int, const void*>> g_dec1_init;   // (device, sync region) already zeroed
 std::map<std::pair<int, const void*>, int> g_dec1_grid;   // (device, kernel) -> grid size
 }  // namespace
+
+// The host-visible time-out flag of each device: pinned, mapped host memory that a persistent call
+// whose wait ran out of time sets (a system-scope store) beside the workspace's error word, so that
+// the next call through the C ABI reports it without synchronising (kErrSync). Allocated at the
+// first persistent launch on a device; an allocation-free call only uses it once it exists.
+namespace {
+constexpr int kMaxDev = 64;
+std::mutex g_herr_mu;
+uint32_t* g_herr_host[kMaxDev] = {};
+uint32_t* g_herr_dev[kMaxDev] = {};
+}  // namespace
+
+int host_err_flag(int dev, bool may_alloc, uint32_t** dptr) {
+    *dptr = nullptr;
+    if (dev < 0 || dev >= kMaxDev) return kOk;
+    std::lock_guard<std::mutex> lk(g_herr_mu);
+    if (!g_herr_host[dev] && may_alloc) {
+        void* h = nullptr;
+        FRT_HIP(hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent));
+        void* d = nullptr;
+        FRT_HIP(hipHostGetDevicePointer(&d, h, 0));
+        *static_cast<volatile uint32_t*>(h) = 0u;
+        g_herr_host[dev] = static_cast<uint32_t*>(h);
+        g_herr_dev[dev] = static_cast<uint32_t*>(d);
+    }
+    *dptr = g_herr_dev[dev];
+    return kOk;
+}
+
+// kErrSync (and clears the flag) if a persistent call on the current device ran out of time since the
+// last check; no synchronisation (the flag is read where the GPU wrote it, in host memory).
+int dec1_take_timeout() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return kOk;
+    uint32_t* h;
+    {
+        std::lock_guard<std::mutex> lk(g_herr_mu);
+        h = g_herr_host[dev];
+    }
+    if (!h) return kOk;
+    volatile uint32_t* v = h;
+    if (*v == 0u) return kOk;
+    *v = 0u;
+    return set_error(kErrSync, "a persistent decode call on device %d ran out of time waiting for another workgroup; "
+                               "its outputs are undefined", dev);
+}
+static void host_err_clear() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return;
+    std::lock_guard<std::mutex> lk(g_herr_mu);
+    if (g_herr_host[dev]) *static_cast<volatile uint32_t*>(g_herr_host[dev]) = 0u;
+}
+// set by the allocation-free entry point around its call: no allocation of the flag then
+thread_local bool g_dec1_no_alloc = false;
 
 // Whether the next decode calls take this path (1, the default) or the three-kernel one (0), and
 // the bound of a call's waits (200 ms of the 100 MHz constant clock by default).
@@ -610,6 +607,8 @@ static int dec1_launch(Dec1Args& a, int E, int K, int n, int ff, int norm, void*
     a.xb = reinterpret_cast<uint64_t*>(base + kDec1Head + kDec1Lg + kDec1Hb);
     a.next_w = next_w;
     a.ticks = g_dec1_ticks;
+    if (!probe_only)
+        if (int rc = host_err_flag(dev, !g_dec1_no_alloc, &a.host_err)) return rc;
     a.E = E;
     a.K = K;
     a.ff = ff;
@@ -743,6 +742,7 @@ int dec1_status(void* sync_ws, hipStream_t stream, uint32_t* err) {
                            stream));
     FRT_HIP(hipStreamSynchronize(stream));
     *err = uint32_t(e >> 32) == kErrMagic ? 1u : 0u;
+    host_err_clear();   // reported here: the next call need not report it again
     if (e) {
         const uint64_t z = 0;
         FRT_HIP(hipMemcpyAsync(static_cast<uint8_t*>(sync_ws) + offsetof(Dec1Sync, err), &z, 8, hipMemcpyHostToDevice,

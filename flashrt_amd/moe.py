@@ -195,7 +195,8 @@ class MoeLayer:
     def workspace(self, T: int) -> torch.Tensor:
         need = self.workspace_bytes(T)
         if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+            # zeroed: a new allocation may reuse an address the library has seen, with leftover bytes
+            self._ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
         return self._ws
 
     def forward(self, x, out, T: int | None = None, resid=None, ids=None, wts=None, counts=None, ws=None,
@@ -238,7 +239,7 @@ class MoeStack:
     def workspace(self) -> torch.Tensor:
         need = self.workspace_bytes()
         if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+            self._ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
         return self._ws
 
     def forward(self, x, out, ids=None, wts=None, ws=None, stream=None) -> None:
@@ -267,6 +268,14 @@ def set_option(name: str, value: int) -> None:
 def layer_sync_error(ws, stream=None) -> bool:
     """True if a persistent single-token call on this workspace ran out of time since the last check."""
     rc = lib().frt_moe_layer_sync_error(_p(ws), _s(stream))
+    if rc < 0:
+        check(rc)
+    return rc == 1
+
+
+def noalloc_sync_error(stream=None) -> bool:
+    """True if an allocation-free single-token call ran out of time since the last check."""
+    rc = lib().frt_noalloc_sync_error(_s(stream))
     if rc < 0:
         check(rc)
     return rc == 1

@@ -29,6 +29,9 @@ extern "C" {
 #define FRT_ERR_HIP -3        /* a HIP call failed */
 #define FRT_ERR_NULL -4       /* a required pointer is missing */
 #define FRT_ERR_IO -5         /* a file could not be opened or read */
+#define FRT_ERR_SYNC -6       /* an earlier persistent decode call on this device ran out of time waiting
+                                 for another workgroup (its outputs are undefined); reported once, by the
+                                 next layer or stack call, which then launches nothing */
 
 /* Message of the last failure on this thread (static storage; "" when none). */
 const char* frt_last_error(void);
@@ -184,7 +187,10 @@ int frt_moe_layer_forward_ex(const frt_moe_layer* L, const float* x, int T, cons
                              int32_t* ids, float* wts, uint32_t* counts, uint32_t* tail_counts, int tail_from,
                              float* probs, void* ws, size_t ws_bytes, void* stream);
 /* The workspace's first bytes hold the single-token path's synchronisation words: they are zeroed by
- * the first call that sees the workspace and must not be written by the caller between calls. */
+ * the first call that sees a workspace address and must not be written by the caller between calls.
+ * A workspace newly allocated at an address used before (a caching allocator hands freed memory out
+ * again) must be zeroed by the caller before its first call: its leftover bytes could by chance carry
+ * a word the next call waits for. The size depends only on the shapes and T, not on frt_set_option. */
 size_t frt_moe_layer_workspace_bytes(const frt_moe_layer* L, int T);
 int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out, int32_t* ids,
                           float* wts, uint32_t* counts, void* ws, size_t ws_bytes, void* stream);
@@ -193,6 +199,12 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
  *   "decode_fused" (default 1): single-token layer calls run as one persistent launch (router, then
  *       routing + gate/up, then down, joined inside the kernel); 0 selects the three-kernel path
  *       (router kernel, routing + gate/up kernel, down kernel). Both give identical results.
+ *   "decode_xcd" (default 0): 1 runs persistent single-token calls in the kernel that splits each layer
+ *       by XCD (router logits relayed into each XCD's L2, each XCD a share of the experts' ff rows,
+ *       XCD partials summed last) where the shape fits; outputs within the layer bar of the default
+ *       kernel's, not bit-equal to them.
+ *   "decode_stamps" (default 0): a device buffer of 64 x 12 x 1024 uint64 that the XCD-split kernel
+ *       fills with per-layer phase times (100 MHz ticks; measurement only), or 0 for none.
  *   "decode_grid" (default 0): workgroups of a persistent single-token call, at most one per CU (0:
  *       one per CU).
  *   "sync_ticks" (default 20000000): bound of a persistent call's waits for other workgroups, in
@@ -202,7 +214,9 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
 int frt_set_option(const char* name, int64_t value);
 /* Reads and clears the error word of a layer workspace (synchronises the stream): 1 if a persistent
  * single-token call on this workspace ran out of time waiting for another workgroup since the last
- * check, 0 if not, negative on a HIP error. No reference counterpart. */
+ * check, 0 if not, negative on a HIP error. Also clears the device's pending FRT_ERR_SYNC. Without this
+ * call, the next frt_moe_layer_forward(_ex) / frt_moe_stack_forward on the device returns FRT_ERR_SYNC
+ * (no synchronisation needed: the kernel sets a flag in pinned host memory). No reference counterpart. */
 int frt_moe_layer_sync_error(void* ws, void* stream);
 
 /* ---- allocation-free decode: frt_moe_layer_forward for decode windows (1 <= T <= 4, T * K <= 63)
@@ -215,6 +229,10 @@ int frt_moe_layer_sync_error(void* ws, void* stream);
 size_t frt_noalloc_scratch_bytes(void);
 int frt_moe_layer_forward_noalloc(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out,
                                   int32_t* ids, float* wts, uint32_t* counts, void* stream);
+/* frt_moe_layer_sync_error for the static array of the current device (synchronises the stream): 1 if
+ * an allocation-free single-token call ran out of time waiting for another workgroup since the last
+ * check, else 0. No reference counterpart; for the same callers as frt_moe_layer_forward_noalloc. */
+int frt_noalloc_sync_error(void* stream);
 
 /* ---- a stack of single-token MoE layers (no reference counterpart as one call: the engine calls
  * moe_block_fast once per layer, arch/qwen4exp/forward.cu:214-217; BASELINE config 2 is a stack of

@@ -304,6 +304,8 @@ struct MoeFastHost {
             ws = nullptr;
             ws_bytes = 0;
             detail::hip_check(hipMalloc(&ws, need), "MoeFastHost workspace");
+            // zeroed: the address may have held a workspace the library has seen before
+            detail::hip_check(hipMemset(ws, 0, need), "MoeFastHost workspace");
             ws_bytes = need;
         }
     }
@@ -398,6 +400,8 @@ struct ExpertStream {
             ws = nullptr;
             ws_bytes = 0;
             detail::hip_check(hipMalloc(&ws, need), "ExpertStream workspace");
+            // zeroed: the address may have held a workspace the library has seen before
+            detail::hip_check(hipMemset(ws, 0, need), "ExpertStream workspace");
             ws_bytes = need;
         }
     }

@@ -106,6 +106,8 @@ def ref():
         R.ref_expert_ffn.argtypes = [_u8p, C.c_int, C.c_int, _f32p, C.c_int, _f32p, C.c_int, C.c_int]
         R.ref_pool_create.restype = C.c_void_p
         R.ref_pool_create.argtypes = [C.c_int, C.c_int]
+        R.ref_pool_create_cpus.restype = C.c_void_p
+        R.ref_pool_create_cpus.argtypes = [C.c_int, C.c_void_p, C.c_int]
         R.ref_pool_destroy.argtypes = [C.c_void_p]
         R.ref_physical_cpus.restype = C.c_int
         R.ref_moe_prepare.restype = C.c_void_p

@@ -81,6 +81,12 @@ void ref_expert_ffn(const void* blob, int n, int ff, const float* x, int ntok, f
 
 // A CpuPool pinned to the physical CPUs (as tools/bench_moe_cpu.cpp:77 does), or unpinned.
 void* ref_pool_create(int n_workers, int pin) { return new CpuPool(n_workers, pin ? physical_cpus() : std::vector<int>{}); }
+// A pool pinned to the given CPUs (the reference's bench pins its pool to physical_cpus(),
+// tools/bench_moe_cpu.cpp:76-77; a caller confined to part of the machine passes the physical cores
+// it may use, one logical CPU each).
+void* ref_pool_create_cpus(int n_workers, const int* cpus, int n_cpus) {
+    return new CpuPool(n_workers, std::vector<int>(cpus, cpus + n_cpus));
+}
 void ref_pool_destroy(void* p) { delete static_cast<CpuPool*>(p); }
 int ref_physical_cpus() { return int(physical_cpus().size()); }
 

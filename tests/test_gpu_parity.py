@@ -860,12 +860,13 @@ def test_cpp_mirror_gpu():
 # ---------------------------------------------------------------- the persistent single-token layer
 
 def _fused_vs_three(F, w, x, resid=None, reps=3):
-    """The single-token layer through the persistent launch (several calls on one workspace, so the
-    epochs advance) and through the three-kernel path: identical ids, weights and outputs, and no
-    wait ran out of time."""
+    """The single-token layer through the persistent launch of decode1.hip (several calls on one
+    workspace, so the epochs advance) and through the three-kernel path: identical ids, weights and
+    outputs, and no wait ran out of time."""
     ws = w.layer_obj.workspace(1)
     outs = []
     try:
+        F.set_option("decode_xcd", 0)
         F.set_option("decode_fused", 0)
         ref = w.gpu_forward(x, resid=resid)
         F.set_option("decode_fused", 1)
@@ -873,6 +874,7 @@ def _fused_vs_three(F, w, x, resid=None, reps=3):
             outs.append(w.gpu_forward(x, resid=resid))
     finally:
         F.set_option("decode_fused", 1)
+        F.set_option("decode_xcd", 1)
     assert not F.layer_sync_error(ws)
     for o in outs:
         for a, b in zip(o, ref):
@@ -914,18 +916,51 @@ def test_decode_fused_matches_three_kernel(F, case):
     assert H.out_rel(out - (x if resid is not None else 0), ref) <= H.OUT_REL
 
 
-def test_decode_fused_router_logits_bit_exact(F):
+@pytest.mark.parametrize("T", [2, 3])
+def test_layer_k32_short_windows(F, T):
+    """K = 32 windows of 2 and 3 tokens: 33 slots per token exceed the window path's moe_hits launch
+    (at most 32 slots), so the layer takes another path and must still match the oracle (ids
+    bit-exact, weights 1e-6, outputs 2e-3), with the workspace the size query gives."""
+    w = H.World(cfg=0, K=32)
+    x = (np.random.default_rng(70 + T).standard_normal((T, H.N))).astype(np.float32)
+    out, ids, wts = w.gpu_forward(x)
+    ref, rid, rw, _ = w.oracle_forward(x)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    assert H.out_rel(out, ref) <= H.OUT_REL
+
+
+def test_layer_workspace_size_independent_of_window_option(F):
+    """The layer workspace size for T <= 8 does not change with "window_min_t": a workspace sized
+    once serves calls after the option changes."""
+    w = H.World(cfg=0)
+    sizes = {}
+    try:
+        for mt in (2, 5, 9):
+            F.set_option("window_min_t", mt)
+            sizes[mt] = [w.layer_obj.workspace_bytes(T) for T in range(1, 9)]
+    finally:
+        F.set_option("window_min_t", 2)
+    assert sizes[2] == sizes[5] == sizes[9]
+
+
+@pytest.mark.parametrize("xcd", [0, 1])
+def test_decode_fused_router_logits_bit_exact(F, xcd):
     """The persistent layer's router logits with the stack's RMS norm (read back from the
     workspace's tagged logit words) equal the oracle's canonical router on rmsnorm(x) bit for bit,
-    the shared gate logit included."""
+    the shared gate logit included (both persistent kernels)."""
     bias = O.gen_zipf_bias(2, 3, H.E, H.ZIPF_S_STACK)
     w = H.World(cfg=2, layer=3, bias=bias, norm_input=True)
     x = (np.random.default_rng(3).standard_normal((1, H.N)) * 4).astype(np.float32)
     ws = w.layer_obj.workspace(1)
     xd = dev(x)
     out = torch.empty((1, H.N), dtype=torch.float32, device="cuda")
-    w.layer_obj.forward(xd, out, T=1, ws=ws)
-    torch.cuda.synchronize()
+    try:
+        F.set_option("decode_xcd", xcd)
+        w.layer_obj.forward(xd, out, T=1, ws=ws)
+        torch.cuda.synchronize()
+    finally:
+        F.set_option("decode_xcd", 0)
     # the logit words follow the 4352-byte header, one every 4 words (32 bytes)
     words = ws[4352:4352 + 32 * (H.E + 1)].cpu().numpy().view(np.uint64)[::4]
     got = (words & np.uint64(0xFFFFFFFF)).astype(np.uint32).view(np.float32)
@@ -936,25 +971,120 @@ def test_decode_fused_router_logits_bit_exact(F):
     assert got[H.E] == gate
 
 
-def test_decode_fused_timeout_path(F, w0):
+@pytest.mark.parametrize("xcd", [0, 1])
+def test_decode_fused_timeout_path(F, w0, xcd):
     """With a zero wait bound the persistent layer cannot wait for the other workgroups: every call
-    still completes (no hang), the error word reports it, and the next call with the normal bound
-    returns the right answer again."""
+    still completes (no hang), the next call reports it (FRT_ERR_SYNC, without a synchronisation),
+    the error word reports it, and the next call with the normal bound returns the right answer
+    again (both persistent kernels)."""
+    F.set_option("decode_xcd", xcd)
+    try:
+        _timeout_path(F, w0)
+    finally:
+        F.set_option("decode_xcd", 0)
+
+
+def _timeout_path(F, w0):
     x = O.gen_normal(0, 0, O.X_TENSOR, H.N).reshape(1, H.N)
     ws = w0.layer_obj.workspace(1)
     good = w0.gpu_forward(x)
     assert not F.layer_sync_error(ws)
     try:
         F.set_option("sync_ticks", 0)
-        w0.gpu_forward(x)
-        flagged = F.layer_sync_error(ws)
+        w0.gpu_forward(x)   # completes (a 256-workgroup join cannot finish within zero ticks)
     finally:
         F.set_option("sync_ticks", 20000000)
+    # the next call reports the time-out without a synchronisation and launches nothing
+    with pytest.raises(F.FrtError) as e:
+        w0.gpu_forward(x)
+    assert e.value.code == -6, e.value
+    assert "ran out of time" in str(e.value)
+    # the workspace's error word still tells (and is cleared by the check)
+    assert F.layer_sync_error(ws)
     again = w0.gpu_forward(x)
     assert not F.layer_sync_error(ws)
     for a, b in zip(again, good):
         assert np.array_equal(a, b)
-    print(f"zero bound flagged: {flagged}")
+    # a time-out reported by layer_sync_error is not reported again by the next call
+    try:
+        F.set_option("sync_ticks", 0)
+        w0.gpu_forward(x)
+    finally:
+        F.set_option("sync_ticks", 20000000)
+    assert F.layer_sync_error(ws)
+    again = w0.gpu_forward(x)
+    for a, b in zip(again, good):
+        assert np.array_equal(a, b)
+
+
+def _kernels(F, fn):
+    """The library kernels fn() launches (names of its per-kernel timing)."""
+    import ctypes as C
+    L = F.lib()
+    L.frt_timing_begin()
+    fn()
+    names = C.create_string_buffer(64 * 32)
+    ms = (C.c_double * 32)()
+    cnt = (C.c_int * 32)()
+    n = L.frt_timing_end(names, 32, ms, cnt, 32)
+    return {names.raw[i * 32:(i + 1) * 32].split(b"\0")[0].decode() for i in range(n)}
+
+
+@pytest.mark.parametrize("case", ["cfg0", "stack", "E128", "E1000", "n1024_ff1024", "n4096_ff256", "K32", "K4",
+                                  "K7", "n3072"])
+def test_decode_xcd_layer_matches_oracle(F, case):
+    """The single-token layer through decode2.hip (joins split by XCD): ids bit-exact, weights 1e-6,
+    outputs within 2e-3 of the oracle, over shapes: config 0; a config 2 layer (RMS norm, Zipf
+    bias, residual); E = 128 and 1000; n = 1024 / ff = 1024 (4 blocks per XCD); n = 4096 / ff = 256
+    (one 32-row block per XCD, 128 down rows per workgroup); K = 32 (4 owned entries per XCD and one
+    split), K = 4 (no owned entry: every entry split over the XCDs), K = 7 (one owned entry per XCD, none
+    split); n = 3072. Repeated calls
+    on one workspace give the same bits, and no wait runs out of time."""
+    rng = np.random.default_rng(abs(hash(case)) % 1000 + 5)
+    kw = dict(cfg=0)
+    resid = None
+    if case == "stack":
+        kw = dict(cfg=2, layer=11, bias=O.gen_zipf_bias(2, 11, H.E, H.ZIPF_S_STACK), norm_input=True)
+    elif case == "E128":
+        kw = dict(cfg=0, E=128)
+    elif case == "E1000":
+        kw = dict(cfg=0, E=1000)
+    elif case == "n1024_ff1024":
+        kw = dict(cfg=0, n=1024, ff=1024)
+    elif case == "n4096_ff256":
+        kw = dict(cfg=0, n=4096, ff=256)
+    elif case == "K32":
+        kw = dict(cfg=0, K=32)
+    elif case == "K4":
+        kw = dict(cfg=0, K=4)
+    elif case == "K7":
+        kw = dict(cfg=0, K=7)
+    elif case == "n3072":
+        kw = dict(cfg=0, n=3072)
+    w = H.World(**kw)
+    x = (rng.standard_normal((1, w.n)) * (3.0 if case == "stack" else 1.0)).astype(np.float32)
+    if case == "stack":
+        resid = x
+    ws = w.layer_obj.workspace(1)
+    try:
+        F.set_option("decode_xcd", 1)
+        got = [w.gpu_forward(x, resid=resid) for _ in range(3)]
+        assert not F.layer_sync_error(ws)
+        xd = dev(x)
+        o = torch.empty((1, w.n), dtype=torch.float32, device="cuda")
+        assert "dec2_layer" in _kernels(F, lambda: w.layer_obj.forward(xd, o, T=1, ws=ws)), case
+    finally:
+        F.set_option("decode_xcd", 0)
+    for g in got[1:]:
+        for a, b in zip(g, got[0]):
+            assert np.array_equal(a, b)
+    out, ids, wts = got[0]
+    ref, rid, rw, _ = w.oracle_forward(x)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    err = H.out_rel(out - (x if resid is not None else 0), ref)
+    print(f"{case}: out rel err {err:.2e}")
+    assert err <= H.OUT_REL
 
 
 def _stack_worlds(nl, x_seed=21):
@@ -980,10 +1110,20 @@ def _layer_chain(layers, x0):
 
 
 @pytest.mark.parametrize("nl", [1, 6])
-def test_decode_stack_call_matches_layer_calls(F, nl):
+@pytest.mark.parametrize("xcd", [0, 1])
+def test_decode_stack_call_matches_layer_calls(F, nl, xcd):
     """frt_moe_stack_forward (config 2 layers: RMS norm, Zipf bias, residual chain) as one
-    persistent launch equals the chain of single-layer calls bit for bit (ids, weights, output),
-    with the three-kernel layer-by-layer path too; three graph replays of the stack call equal it."""
+    persistent launch equals the chain of single-layer calls bit for bit (ids, weights, output);
+    decode1.hip's kernel equals the three-kernel layer-by-layer path too, and decode2.hip's (xcd = 1)
+    is within the layer bar of it; three graph replays of the stack call equal it."""
+    F.set_option("decode_xcd", xcd)
+    try:
+        _stack_vs_layers(F, nl, xcd)
+    finally:
+        F.set_option("decode_xcd", 0)
+
+
+def _stack_vs_layers(F, nl, xcd):
     layers, x0 = _stack_worlds(nl)
     st = F.MoeStack([w.layer_obj for w in layers])
     outs, ids_ref, wts_ref = _layer_chain(layers, x0)
@@ -997,14 +1137,28 @@ def test_decode_stack_call_matches_layer_calls(F, nl):
     assert torch.equal(ids, ids_ref)
     assert torch.equal(wts, wts_ref)
     assert torch.equal(out, outs[-1])
+    kn = _kernels(F, lambda: st.forward(x0, out, ws=ws))
+    assert (kn & {"dec2_stack", "dec2_layer"}) if xcd else (kn & {"dec1_stack", "dec1_layer"}), kn
+    # decode1.hip's stack kernel equals the three-kernel path layer by layer bit for bit; decode2.hip's
+    # result is within the layer bar of it (same ids)
     try:
+        F.set_option("decode_xcd", 0)
+        out1 = torch.empty_like(out)
+        ids1 = torch.full((nl, H.K), -1, dtype=torch.int32, device="cuda")
+        st.forward(x0, out1, ids=ids1, ws=ws)
         F.set_option("decode_fused", 0)
         out3 = torch.empty_like(out)
         st.forward(x0, out3, ws=ws)
         torch.cuda.synchronize()
     finally:
         F.set_option("decode_fused", 1)
-    assert torch.equal(out3, out)
+        F.set_option("decode_xcd", xcd)
+    assert torch.equal(out3, out1)
+    assert torch.equal(ids1, ids_ref)
+    if xcd:
+        assert H.out_rel((out1 - x0).cpu().numpy(), (out - x0).cpu().numpy()) <= H.OUT_REL
+    else:
+        assert torch.equal(out1, out)
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         st.forward(x0, out, ids=ids, wts=wts, ws=ws, stream=s)

@@ -46,6 +46,7 @@ def test_noalloc_matches_workspace_entry(cfg):
         for a, b in zip(got, ref):
             assert np.array_equal(a, b), (cfg, T)
         assert np.isfinite(got[0]).all()
+        assert not F.noalloc_sync_error()   # no allocation-free call ran out of time
 
 
 def test_noalloc_refuses_prefill_sizes():
