@@ -79,7 +79,9 @@ class FrtMoeLayer(C.Structure):
     _fields_ = [("experts", C.c_void_p), ("stride", C.c_size_t), ("n_expert", C.c_int), ("shared", C.c_void_p),
                 ("router_w", C.c_void_p), ("router_bias", C.c_void_p), ("gate_w", C.c_void_p),
                 ("d_model", C.c_int), ("d_ff", C.c_int), ("top_k", C.c_int), ("flags", C.c_int),
-                ("next_router_w", C.c_void_p)]
+                ("next_router_w", C.c_void_p), ("shared_dense", C.c_int), ("shared_type", C.c_int),
+                ("shared_ff", C.c_int), ("shared_gate", C.c_void_p), ("shared_up", C.c_void_p),
+                ("shared_down", C.c_void_p)]
 
 
 class FrtExpertSlab(C.Structure):

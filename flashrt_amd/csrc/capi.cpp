@@ -140,6 +140,17 @@ int gen_correlated(uint64_t seed, int cfg, int layer, int tensor0, int T, int n,
                    hipStream_t stream);
 void gen_zipf_bias(uint64_t seed, int cfg, int layer, int E, float s, float alpha, float* bias);
 
+// shexp.hip
+bool shexp_type_ok(int type);
+bool shexp_shape_ok(int n, int ffs);
+size_t shexp_ws_bytes(int T, int n, int ffs);
+int shexp_run(int type, const void* g, const void* u, const void* d, int n, int ffs, const float* x, const int8_t* xq,
+              const float* xd, int T, float* sh, void* ws, hipStream_t stream);
+int hits_from_ids(const int32_t* ids, int T, int K, const uint8_t* arena, size_t stride, const uint8_t** hit_ptr,
+                  int32_t* hit_n, hipStream_t stream);
+int slot_combine(int T, int K, int n, const int32_t* ids, const float* wts, const float* Y, const float* sh,
+                 const float* gate, const float* resid, float* out, hipStream_t stream);
+
 constexpr int kDecodeMaxT = 4;
 
 // moe_hits runs a window in launches of at most hits_chunk(T, K, ff) tokens: 8 (the reference's
@@ -183,6 +194,107 @@ static bool window_path(const frt_moe_layer& L, int T) {
     return T <= 8 && dec_window_fits(T, K, L.d_ff) && router_fused_fits(T, n) && dec_check(1, K, n, L.d_ff) == kOk;
 }
 
+// ---- a layer whose shared expert is given as dense GGUF tensors (frt_moe_layer.shared_dense): the
+// routed experts as per-slot outputs (moe_hits for windows of up to 8 tokens, moe_q2::run beyond),
+// the shared expert (shexp.hip), then the slot combine.
+struct DenseWs {
+    float* u;                  // the layer input (normalised with FRT_LAYER_NORM_INPUT)
+    int8_t* xq;
+    float* xd;
+    float* part;               // router GEMM partials (prefill)
+    const uint8_t** hit_ptr;   // [T][K] (windows)
+    int32_t* hit_n;            // [T]
+    float* Y;                  // per-slot outputs [T][K][n]
+    float* sh;                 // shared expert output [T][n]
+    void* shws;
+    void* rws;                 // moe_hits scratch or moe_q2 workspace
+    size_t rws_bytes;
+    size_t end;                // bytes from the layer workspace's start
+};
+static bool dense_small(const frt_moe_layer& L, int T) {
+    return T <= 8 && L.top_k <= 32 && dec_check(1, L.top_k, L.d_model, L.d_ff) == kOk;
+}
+static DenseWs dense_carve(uint8_t* p0, uint8_t* p, const frt_moe_layer& L, int T) {
+    DenseWs w{};
+    auto take = [&](size_t b) {
+        uint8_t* r = p;
+        p += up256(b);
+        return r;
+    };
+    const int E = L.n_expert, K = L.top_k, n = L.d_model, ff = L.d_ff;
+    w.u = reinterpret_cast<float*>(take(size_t(T) * n * 4));
+    w.xq = reinterpret_cast<int8_t*>(take(size_t(T) * n));
+    w.xd = reinterpret_cast<float*>(take(size_t(T) * (n / kQ8) * 4));
+    w.hit_ptr = reinterpret_cast<const uint8_t**>(take(size_t(T) * K * 8));
+    w.hit_n = reinterpret_cast<int32_t*>(take(size_t(T) * 4));
+    w.Y = reinterpret_cast<float*>(take(size_t(T) * K * n * 4));
+    w.sh = reinterpret_cast<float*>(take(size_t(T) * n * 4));
+    w.shws = take(shexp_ws_bytes(T, n, L.shared_ff > 0 ? L.shared_ff : 64));
+    if (dense_small(L, T)) {
+        w.rws_bytes = dec_scratch_bytes(hits_chunk(T, K, ff), K, ff);
+    } else {
+        w.part = reinterpret_cast<float*>(take(router_gemm_ws_bytes(T, E, true)));
+        w.rws_bytes = pf_workspace_bytes(T, K, n, ff, E, false, false);
+    }
+    w.rws = take(w.rws_bytes);
+    w.end = size_t(p - p0);
+    return w;
+}
+
+static int dense_layer(const frt_moe_layer& L, const LayerWs& lw, const DenseWs& w, const float* x, int T,
+                       const float* resid, float* out, int32_t* ids, float* wts, uint32_t* counts, hipStream_t s) {
+    const int E = L.n_expert, K = L.top_k, n = L.d_model, ff = L.d_ff, ffs = L.shared_ff;
+    if (!L.shared_gate || !L.shared_up || !L.shared_down) return set_error(kErrNull, "moe_layer: shared tensors missing");
+    if (!shexp_type_ok(L.shared_type))
+        return set_error(kErrShape, "moe_layer: shared expert type %d (F32, F16, BF16 or Q8_0)", L.shared_type);
+    if (!shexp_shape_ok(n, ffs)) return set_error(kErrShape, "moe_layer: shared_ff=%d n=%d", ffs, n);
+    const bool small = dense_small(L, T);
+    if (!small)
+        if (int rc = pf_check(T, K, n, ff, E)) return rc;
+    const float* u = x;
+    if (L.flags & FRT_LAYER_NORM_INPUT) {
+        if (int rc = rmsnorm(x, T, n, w.u, s)) return rc;
+        u = w.u;
+        timing_mark(s, "rmsnorm");
+    }
+    if (small && router_fused_fits(T, n)) {
+        if (int rc = router_logits(u, T, L.router_w, L.router_bias, L.gate_w, E, n, lw.logits, lw.gate, s, 0, w.xq, w.xd))
+            return rc;
+    } else {
+        if (small) {
+            if (int rc = router_logits(u, T, L.router_w, L.router_bias, L.gate_w, E, n, lw.logits, lw.gate, s, 0, nullptr,
+                                       nullptr))
+                return rc;
+        } else if (int rc = router_gemm(u, T, L.router_w, L.router_bias, L.gate_w, E, n, lw.logits, lw.gate, w.part, s)) {
+            return rc;
+        }
+        if (small || L.shared_type == FRT_GGML_Q8_0)
+            if (int rc = quantize_q8(u, T, n, w.xq, w.xd, nullptr, nullptr, s)) return rc;
+    }
+    timing_mark(s, "router");
+    if (int rc = route_topk(s, lw.logits, T, E, K, ids, wts, counts, nullptr, 1 << 30)) return rc;
+    timing_mark(s, "route_topk");
+    if (small) {
+        if (int rc = hits_from_ids(ids, T, K, L.experts, L.stride, w.hit_ptr, w.hit_n, s)) return rc;
+        const int tc = hits_chunk(T, K, ff);
+        for (int t0 = 0; t0 < T; t0 += tc) {
+            const int tn = T - t0 < tc ? T - t0 : tc;
+            if (int rc = dec_hits(w.hit_ptr + size_t(t0) * K, w.hit_n + t0, K, w.xq + size_t(t0) * n,
+                                  w.xd + size_t(t0) * (n / kQ8), n, ff, w.rws, w.Y + size_t(t0) * K * n, s, tn))
+                return rc;
+        }
+    } else if (int rc = pf_run(L.experts, L.stride, E, n, ff, u, ids, T, K, w.Y, w.rws, w.rws_bytes, s, 0, 0)) {
+        return rc;
+    }
+    if (int rc = shexp_run(L.shared_type, L.shared_gate, L.shared_up, L.shared_down, n, ffs, u, w.xq, w.xd, T, w.sh,
+                           w.shws, s))
+        return rc;
+    timing_mark(s, "shared_expert");
+    if (int rc = slot_combine(T, K, n, ids, wts, w.Y, w.sh, lw.gate, resid, out, s)) return rc;
+    timing_mark(s, "combine");
+    return kOk;
+}
+
 static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t total) {
     LayerWs w{};
     uint8_t* p = static_cast<uint8_t*>(base);
@@ -200,6 +312,11 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
     // the decode window paths a call of T tokens can take, whatever "window_min_t" is set to: the
     // workspace holds the larger of their layouts, so a size queried once stays valid after the option
     // changes (both carve xq and xd first, then their own scratch)
+    if (L.shared_dense) {   // the dense shared expert's path (dense_layer)
+        const DenseWs d = dense_carve(static_cast<uint8_t*>(base), p, L, T);
+        w.bytes = d.end;
+        return w;
+    }
     const bool dec_ok = T <= kDecodeMaxT && T * K <= 63;
     const bool win_ok = T <= 8 && dec_window_fits(T, K, ff) && router_fused_fits(T, n) && dec_check(1, K, n, ff) == kOk;
     if (dec_ok || win_ok) {
@@ -417,7 +534,8 @@ size_t frt_moe_layer_workspace_bytes(const frt_moe_layer* L, int T) {
 int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const float* resid, float* out, int32_t* ids,
                           float* wts, uint32_t* counts, void* ws, size_t ws_bytes, void* stream) {
     if (!L || !x || !out || !ws) return set_error(kErrNull, "moe_layer: null pointer");
-    if (!L->experts || !L->shared || !L->router_w || !L->gate_w) return set_error(kErrNull, "moe_layer: layer weights missing");
+    if (!L->experts || (!L->shared && !L->shared_dense) || !L->router_w || !L->gate_w)
+        return set_error(kErrNull, "moe_layer: layer weights missing");
     if (T < 1) return set_error(kErrShape, "moe_layer: T=%d", T);
     if (int rc = dec1_take_timeout()) return rc;
     const int E = L->n_expert, K = L->top_k, n = L->d_model, ff = L->d_ff;
@@ -430,6 +548,12 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     float* wts_o = wts ? wts : w.wts;
     const int norm = (L->flags & FRT_LAYER_NORM_INPUT) ? 1 : 0;
     timing_mark(s, "begin");
+    if (L->shared_dense) {
+        uint8_t* b = static_cast<uint8_t*>(ws);
+        uint8_t* p = b + (reinterpret_cast<uint8_t*>(w.wts) - b) + up256(size_t(T) * K * 4);
+        const DenseWs d = dense_carve(b, p, *L, T);
+        return dense_layer(*L, w, d, x, T, resid, out, ids_o, wts_o, counts, s);
+    }
     if (T == 1 && g_dec1_on && dec2_support(E, K, n, ff, 1))   // one persistent launch, joins split by XCD
         return dec2_layer(x, L->router_w, L->router_bias, L->gate_w, E, K, L->experts, L->stride, L->shared, n, ff,
                           norm, resid, out, ids_o, wts_o, counts, w.sync, L->next_router_w, s);
@@ -513,7 +637,8 @@ int frt_moe_stack_forward(const frt_moe_layer* layers, int n_layer, const float*
     const frt_moe_layer& L0 = layers[0];
     for (int l = 0; l < n_layer; ++l) {
         const frt_moe_layer& Ll = layers[l];
-        if (!Ll.experts || !Ll.shared || !Ll.router_w || !Ll.gate_w) return set_error(kErrNull, "moe_stack: layer %d weights missing", l);
+        if (!Ll.experts || (!Ll.shared && !Ll.shared_dense) || !Ll.router_w || !Ll.gate_w)
+            return set_error(kErrNull, "moe_stack: layer %d weights missing", l);
         if (Ll.n_expert != L0.n_expert || Ll.top_k != L0.top_k || Ll.d_model != L0.d_model || Ll.d_ff != L0.d_ff ||
             Ll.stride != L0.stride || Ll.flags != L0.flags)
             return set_error(kErrShape, "moe_stack: layer %d differs in shape, stride or flags from layer 0", l);
@@ -529,7 +654,9 @@ int frt_moe_stack_forward(const frt_moe_layer* layers, int n_layer, const float*
                      reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + lw + up256(size_t(n) * 4))};
     constexpr int kChunk = 64;   // layers of one persistent launch
     const float* cur = x;
-    if (g_dec1_on && dec2_support(E, K, n, ff, 2)) {
+    bool dense = false;   // a dense shared expert: layer by layer (the persistent kernels take the Q2_0 blob)
+    for (int l = 0; l < n_layer; ++l) dense = dense || layers[l].shared_dense;
+    if (!dense && g_dec1_on && dec2_support(E, K, n, ff, 2)) {
         const LayerWs w = layer_carve(ws, L0, 1, ws_bytes);
         for (int l0 = 0, c = 0; l0 < n_layer; l0 += kChunk, ++c) {
             const int nl = n_layer - l0 < kChunk ? n_layer - l0 : kChunk;
@@ -541,7 +668,7 @@ int frt_moe_stack_forward(const frt_moe_layer* layers, int n_layer, const float*
         }
         return kOk;
     }
-    if (g_dec1_on && dec1_support(E, K, n, ff) == 2) {
+    if (!dense && g_dec1_on && dec1_support(E, K, n, ff) == 2) {
         const LayerWs w = layer_carve(ws, L0, 1, ws_bytes);
         for (int l0 = 0, c = 0; l0 < n_layer; l0 += kChunk, ++c) {
             const int nl = n_layer - l0 < kChunk ? n_layer - l0 : kChunk;
@@ -615,7 +742,7 @@ int frt_moe_layer_forward_ex(const frt_moe_layer* L, const float* x, int T, cons
     const LayerWs w = layer_carve(ws, *L, T, ws_bytes);
     const float* lg = w.logits;
     int ls = 1;
-    if (T == 1 && g_dec1_on && (dec2_support(E, K, n, ff, 1) || dec1_support(E, K, n, ff) >= 1))
+    if (T == 1 && g_dec1_on && !L->shared_dense && (dec2_support(E, K, n, ff, 1) || dec1_support(E, K, n, ff) >= 1))
         lg = dec1_logits(w.sync, &ls);   // the persistent call's (both kernels keep them in the same words)
     return layer_trace(lg, ls, ids ? ids : w.ids, T, E, K, tail_counts, tail_from, probs, static_cast<hipStream_t>(stream));
 }

@@ -183,6 +183,17 @@ class MoeLayer:
         self.d_model, self.top_k, self.n_expert = d_model, top_k, n_expert
         self._ws = None
 
+    def set_shared_dense(self, gguf_type: int, gate, up, down, shared_ff: int) -> None:
+        """The shared expert as the model's dense GGUF tensors (raw ggml-layout bytes on the device:
+        gate / up [shared_ff][d_model], down [d_model][shared_ff]) of type F32, F16, BF16 or Q8_0, in
+        place of the Q2_0 blob (frt_moe_layer.shared_dense)."""
+        self._shexp = (gate, up, down)
+        self.raw.shared_dense = 1
+        self.raw.shared_type = int(gguf_type)
+        self.raw.shared_ff = int(shared_ff)
+        self.raw.shared_gate, self.raw.shared_up, self.raw.shared_down = _p(gate), _p(up), _p(down)
+        self._ws = None
+
     def set_next_router(self, router_w) -> None:
         """The router matrix the next layer call reads; decode calls warm it into the caches
         during their last kernel (frt_moe_layer.next_router_w)."""

@@ -178,6 +178,21 @@ typedef struct frt_moe_layer {
      * the next router kernel reads it from, so that the next router kernel does not wait on HBM.
      * No reference counterpart (the reference's router is a ggml linear, blocks.hpp:85). */
     const float* next_router_w;
+    /* Optional: the shared expert as the model's dense GGUF tensors (ffn_gate_shexp, ffn_up_shexp
+     * [shared_ff][d_model], ffn_down_shexp [d_model][shared_ff], ggml row-major layout, device memory)
+     * instead of the planar Q2_0 blob `shared` (arch/qwen4exp/moe_ref.cu:117-123 computes it with
+     * linear() in whatever type the file ships). shared_dense = 0 (the default): `shared` is used.
+     * shared_type: FRT_GGML_F32, FRT_GGML_F16, FRT_GGML_BF16 or FRT_GGML_Q8_0 (Q8_0 weights take the
+     * input and h as Q8_0 activations, per-block integer dots; the others fp32 activations).
+     * shared_ff a multiple of 64, at most 4096. Such a layer runs router -> route_topk -> the routed
+     * experts as per-slot outputs (moe_hits up to 8 tokens, moe_q2::run beyond) -> the shared expert
+     * -> the combine; the persistent single-token kernels take only the Q2_0 blob. */
+    int shared_dense;
+    int shared_type;
+    int shared_ff;
+    const void* shared_gate;
+    const void* shared_up;
+    const void* shared_down;
 } frt_moe_layer;
 /* frt_moe_layer_forward with the routing records of moe_route_topk and MoeTrace (blocks.hpp:130-135,
  * :267-286): tail_counts [E] (optional) += 1 per selection of tokens t >= tail_from; probs [T][K]

@@ -210,6 +210,16 @@ struct MoeLayer {
         desc = frt_moe_layer{experts, stride, n_expert, shared, router_w, router_bias, gate_w,
                              d_model, d_ff,   top_k,    norm_input ? FRT_LAYER_NORM_INPUT : 0, nullptr};
     }
+    // the shared expert as the model's dense GGUF tensors (F32, F16, BF16 or Q8_0) instead of the
+    // Q2_0 blob (frt_moe_layer.shared_dense)
+    void set_shared_dense(int ggml_type, const void* gate, const void* up, const void* down, int shared_ff) {
+        desc.shared_dense = 1;
+        desc.shared_type = ggml_type;
+        desc.shared_ff = shared_ff;
+        desc.shared_gate = gate;
+        desc.shared_up = up;
+        desc.shared_down = down;
+    }
     size_t workspace_bytes(int T) const { return frt_moe_layer_workspace_bytes(&desc, T); }
     // out [T][d_model] = (resid ? resid : 0) + moe(x); ids/wts [T][top_k], counts [E] optional;
     // tail_counts [E] += 1 per selection of tokens t >= tail_from (optional)

@@ -418,6 +418,80 @@ void orc_moe_cpu(int n, int ff, const uint8_t* const* blobs, const int* ntok, co
 void orc_moe_layer(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blob, const float* router_w,
                    const float* router_bias, const float* gate_w, int n, int ff, int K, const float* x, int T,
                    int n_threads, int order, float* out, int32_t* ids, float* wts, float* logits_out, int norm_input) {
+    orc_moe_layer_shexp(arena, stride, E, -1, nullptr, nullptr, nullptr, 0, shared_blob, router_w, router_bias, gate_w, n,
+                        ff, K, x, T, n_threads, order, out, ids, wts, logits_out, norm_input);
+}
+
+namespace {
+// one weight of row r, column j of a dense [rows][cols] matrix of ggml type F32 / F16 / BF16
+float dense_w(int type, const void* w, int cols, int r, int j) {
+    const size_t i = size_t(r) * cols + j;
+    if (type == 0) return static_cast<const float*>(w)[i];
+    const uint16_t b = static_cast<const uint16_t*>(w)[i];
+    if (type == 1) return orc_f16_to_f32(b);
+    uint32_t u = uint32_t(b) << 16;   // bf16: the upper half of an fp32
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+// y[r] = row r of W (rows x cols) . a, for one activation vector
+void dense_mv(int type, const void* w, int rows, int cols, const float* a, const int8_t* aq, const float* ad,
+              float* y) {
+    for (int r = 0; r < rows; ++r) {
+        if (type == 8) {   // Q8_0: 34-byte blocks {fp16 d; int8 q[32]}, ggml_vec_dot_q8_0_q8_0
+            const uint8_t* row = static_cast<const uint8_t*>(w) + size_t(r) * (cols / kQ8) * 34;
+            float sumf = 0.0f;
+            for (int b = 0; b < cols / kQ8; ++b) {
+                const uint8_t* blk = row + size_t(b) * 34;
+                uint16_t db;
+                std::memcpy(&db, blk, 2);
+                const int8_t* q = reinterpret_cast<const int8_t*>(blk + 2);
+                int sumi = 0;
+                for (int j = 0; j < kQ8; ++j) sumi += int(q[j]) * int(aq[b * kQ8 + j]);
+                const float dd = orc_f16_to_f32(db) * ad[b];
+                sumf += float(sumi) * dd;
+            }
+            y[r] = sumf;
+        } else {
+            double s = 0.0;
+            for (int j = 0; j < cols; ++j) s += double(dense_w(type, w, cols, r, j) * a[j]);
+            y[r] = float(s);
+        }
+    }
+}
+}  // namespace
+
+void orc_dense_mv(int type, const void* w, int rows, int cols, const float* x, int T, float* y) {
+    std::vector<int8_t> xq(cols);
+    std::vector<float> xd(cols / kQ8);
+    for (int t = 0; t < T; ++t) {
+        const float* xt = x + size_t(t) * cols;
+        if (type == 8) orc_quantize_q8(xt, cols, xq.data(), xd.data());
+        dense_mv(type, w, rows, cols, xt, xq.data(), xd.data(), y + size_t(t) * rows);
+    }
+}
+
+void orc_shexp_ffn(int type, const void* gate, const void* up, const void* down, int n, int ffs, const float* x, int T,
+                   float* out) {
+    std::vector<float> g(ffs), u(ffs);
+    std::vector<int8_t> xq(n), hq(ffs);
+    std::vector<float> xd(n / kQ8), hd(ffs / kQ8);
+    for (int t = 0; t < T; ++t) {
+        const float* xt = x + size_t(t) * n;
+        if (type == 8) orc_quantize_q8(xt, n, xq.data(), xd.data());
+        dense_mv(type, gate, ffs, n, xt, xq.data(), xd.data(), g.data());
+        dense_mv(type, up, ffs, n, xt, xq.data(), xd.data(), u.data());
+        for (int i = 0; i < ffs; ++i) g[i] = swiglu(g[i], u[i]);
+        if (type == 8) orc_quantize_q8(g.data(), ffs, hq.data(), hd.data());
+        dense_mv(type, down, n, ffs, g.data(), hq.data(), hd.data(), out + size_t(t) * n);
+    }
+}
+
+void orc_moe_layer_shexp(const uint8_t* arena, size_t stride, int E, int shared_type, const void* sg, const void* su,
+                         const void* sd, int ffs, const uint8_t* shared_blob, const float* router_w,
+                         const float* router_bias, const float* gate_w, int n, int ff, int K, const float* x, int T,
+                         int n_threads, int order, float* out, int32_t* ids, float* wts, float* logits_out,
+                         int norm_input) {
     std::vector<float> un;
     if (norm_input) {
         un.resize(size_t(T) * n);
@@ -459,8 +533,11 @@ void orc_moe_layer(const uint8_t* arena, size_t stride, int E, const uint8_t* sh
     for (int t0 = 0; t0 < T; t0 += 4) {
         const int c = std::min(4, T - t0);
         std::vector<float> shc(size_t(c) * n);
-        orc_expert_ffn(shared_blob, n, ff, xq.data() + size_t(t0) * n, xd.data() + size_t(t0) * (n / kQ8), c, shc.data(),
-                       n, order);
+        if (shared_type >= 0)
+            orc_shexp_ffn(shared_type, sg, su, sd, n, ffs, x + size_t(t0) * n, c, shc.data());
+        else
+            orc_expert_ffn(shared_blob, n, ff, xq.data() + size_t(t0) * n, xd.data() + size_t(t0) * (n / kQ8), c,
+                           shc.data(), n, order);
         for (int t = t0; t < t0 + c; ++t) {
             const float gl = orc_dot_canon(gate_w, x + size_t(t) * n, n);
             const float g = 1.0f / (1.0f + std::exp(-gl));

@@ -86,6 +86,26 @@ void orc_moe_layer(const uint8_t* arena, size_t stride, int E, const uint8_t* sh
                    const float* router_bias, const float* gate_w, int n, int ff, int K, const float* x, int T,
                    int n_threads, int order, float* out, int32_t* ids, float* wts, float* logits_out, int norm_input);
 
+/* ---- the shared expert in the model's own GGUF type (moe_ref.cu:117-123 computes it with ggml's
+ * linear(): ffn_gate_shexp / ffn_up_shexp [ffs][n], ffn_down_shexp [n][ffs], row-major ggml layout),
+ * on the layer input x (fp32 [T][n]); out [T][n]. type (ggml ids): 0 F32, 1 F16, 30 BF16, 8 Q8_0
+ * (blocks {fp16 d; int8 q[32]}). Q8_0: x and h are Q8_0 activations (orc_quantize_q8), each row
+ * y = sum over blocks ascending of float(sumi) * (d_w * d_a) (ggml's vec_dot_q8_0_q8_0 order);
+ * F32/F16/BF16: x and h stay fp32, y = sum_j w_j x_j with fp32 products summed in double, then
+ * rounded. h = g / (1 + exp(-g)) * u (fp32). This build's definition: ggml's dense kernels are not
+ * in this image, and no reference test pins the shared expert on its own. */
+void orc_shexp_ffn(int type, const void* gate, const void* up, const void* down, int n, int ffs, const float* x, int T,
+                   float* out);
+/* one of its products: y [T][rows] = W x_t, x [T][cols] fp32 (Q8_0: quantized per token first) */
+void orc_dense_mv(int type, const void* w, int rows, int cols, const float* x, int T, float* y);
+/* orc_moe_layer with the shared expert given as orc_shexp_ffn's tensors (shared_type >= 0) in place of
+ * a Q2_0 blob (shared_type < 0: orc_moe_layer itself). */
+void orc_moe_layer_shexp(const uint8_t* arena, size_t stride, int E, int shared_type, const void* sg, const void* su,
+                         const void* sd, int ffs, const uint8_t* shared_blob, const float* router_w,
+                         const float* router_bias, const float* gate_w, int n, int ff, int K, const float* x, int T,
+                         int n_threads, int order, float* out, int32_t* ids, float* wts, float* logits_out,
+                         int norm_input);
+
 /* ---- synthetic inputs: the seeded recipe restated independently in the HIP library ---- */
 uint64_t orc_gen_key(uint64_t seed, uint64_t cfg, uint64_t layer, uint64_t tensor);
 uint64_t orc_gen_u64(uint64_t key, uint64_t i);

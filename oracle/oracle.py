@@ -69,6 +69,13 @@ def lib():
         L.orc_moe_layer.argtypes = [C.c_void_p, C.c_size_t, C.c_int, _u8p, _f32p, C.c_void_p, _f32p, C.c_int, C.c_int,
                                     C.c_int, _f32p, C.c_int, C.c_int, C.c_int, _f32p, _i32p, _f32p, C.c_void_p, C.c_int]
         L.orc_rmsnorm.argtypes = [_f32p, C.c_int, C.c_int, _f32p]
+        L.orc_dense_mv.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int, _f32p, C.c_int, _f32p]
+        L.orc_shexp_ffn.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, _f32p, C.c_int,
+                                    _f32p]
+        L.orc_moe_layer_shexp.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                          C.c_void_p, C.c_int, C.c_void_p, _f32p, C.c_void_p, _f32p, C.c_int, C.c_int,
+                                          C.c_int, _f32p, C.c_int, C.c_int, C.c_int, _f32p, _i32p, _f32p, C.c_void_p,
+                                          C.c_int]
         L.orc_gen_key.restype = C.c_uint64
         L.orc_gen_key.argtypes = [C.c_uint64] * 4
         L.orc_gen_u64.restype = C.c_uint64
@@ -242,11 +249,12 @@ def rmsnorm(x: np.ndarray) -> np.ndarray:
     return u
 
 
-def moe_layer(arena: np.ndarray, stride: int, E: int, shared: np.ndarray, router_w: np.ndarray, router_bias,
+def moe_layer(arena: np.ndarray, stride: int, E: int, shared, router_w: np.ndarray, router_bias,
               gate_w: np.ndarray, n: int, ff: int, K: int, x: np.ndarray, threads: int = 8, order: int = 0,
               norm_input: bool = False):
     """The whole layer (moe_block semantics). arena: uint8 [E*stride] (or an object exposing
-    .ctypes.data). Returns out [T][n], ids, wts, logits."""
+    .ctypes.data). shared: the Q2_0 blob, or a tuple (ggml type, gate, up, down, ffs) of the dense
+    shared expert (raw ggml-layout bytes). Returns out [T][n], ids, wts, logits."""
     x = np.ascontiguousarray(x, np.float32).reshape(-1, n)
     T = x.shape[0]
     out = np.zeros((T, n), np.float32)
@@ -254,7 +262,31 @@ def moe_layer(arena: np.ndarray, stride: int, E: int, shared: np.ndarray, router
     wts = np.zeros((T, K), np.float32)
     logits = np.zeros((T, E), np.float32)
     b = None if router_bias is None else np.ascontiguousarray(router_bias, np.float32)
-    lib().orc_moe_layer(arena.ctypes.data, stride, E, shared, np.ascontiguousarray(router_w, np.float32).reshape(-1),
-                        None if b is None else b.ctypes.data, np.ascontiguousarray(gate_w, np.float32), n, ff, K,
-                        x.reshape(-1), T, threads, order, out, ids, wts, logits.ctypes.data, int(norm_input))
+    if isinstance(shared, tuple):
+        st, sg, su, sd, ffs = shared
+        sg, su, sd = (np.ascontiguousarray(a).view(np.uint8) for a in (sg, su, sd))
+        sp = (st, sg.ctypes.data, su.ctypes.data, sd.ctypes.data, ffs, None)
+    else:
+        sp = (-1, None, None, None, 0, np.ascontiguousarray(shared, np.uint8).ctypes.data)
+    lib().orc_moe_layer_shexp(arena.ctypes.data, stride, E, *sp, np.ascontiguousarray(router_w, np.float32).reshape(-1),
+                              None if b is None else b.ctypes.data, np.ascontiguousarray(gate_w, np.float32), n, ff, K,
+                              x.reshape(-1), T, threads, order, out, ids, wts, logits.ctypes.data, int(norm_input))
     return out, ids, wts, logits
+
+
+def dense_mv(gtype: int, w, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    """orc_dense_mv: y [T][rows] = W x_t for a ggml-layout dense matrix of type gtype."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+    y = np.zeros((x.shape[0], rows), np.float32)
+    wb = np.ascontiguousarray(w).view(np.uint8)
+    lib().orc_dense_mv(gtype, wb.ctypes.data, rows, cols, x.reshape(-1), x.shape[0], y)
+    return y
+
+
+def shexp_ffn(gtype: int, gate, up, down, n: int, ffs: int, x: np.ndarray) -> np.ndarray:
+    """The dense shared expert (orc_shexp_ffn) of ggml type gtype on x [T][n] -> [T][n]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, n)
+    out = np.zeros_like(x)
+    g, u, d = (np.ascontiguousarray(a).view(np.uint8) for a in (gate, up, down))
+    lib().orc_shexp_ffn(gtype, g.ctypes.data, u.ctypes.data, d.ctypes.data, n, ffs, x.reshape(-1), x.shape[0], out)
+    return out

@@ -82,3 +82,45 @@ class World:
     def oracle_forward(self, x: np.ndarray, threads: int = 8):
         return O.moe_layer(self.arena_h, self.stride, self.E, self.shared_h, self.router_h, self.bias_h, self.gate_h,
                            self.n, self.ff, self.K, x, threads=threads, norm_input=self.norm_input)
+
+
+# ---- the shared expert in a dense GGUF type (ggml ids: F32 0, F16 1, Q8_0 8, BF16 30)
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_BF16 = 0, 1, 8, 30
+
+
+def dense_tensor(gtype: int, rows: int, cols: int, rng: np.random.Generator, sd: float = 0.02) -> np.ndarray:
+    """A seeded [rows][cols] weight matrix in ggml's row-major layout of type gtype, as raw bytes."""
+    if gtype == GGML_Q8_0:
+        nb = rows * cols // 32
+        blk = np.zeros((nb, 34), np.uint8)
+        d = (rng.uniform(0.5, 1.5, nb) * sd * 1.7 / 127).astype(np.float16)
+        blk[:, :2] = d.view(np.uint8).reshape(nb, 2)
+        blk[:, 2:] = rng.integers(-127, 128, (nb, 32)).astype(np.int8).view(np.uint8)
+        return blk.reshape(-1)
+    w = (rng.standard_normal((rows, cols)) * sd).astype(np.float32)
+    if gtype == GGML_F32:
+        return w.view(np.uint8).reshape(-1)
+    if gtype == GGML_F16:
+        return w.astype(np.float16).view(np.uint8).reshape(-1)
+    if gtype == GGML_BF16:
+        u = w.view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)   # round to nearest even
+        return r.view(np.uint8).reshape(-1)
+    raise ValueError(gtype)
+
+
+def dense_values(gtype: int, raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """The float64 values of a dense ggml matrix (dequantized Q8_0: d * q)."""
+    raw = np.ascontiguousarray(raw, np.uint8)
+    if gtype == GGML_Q8_0:
+        blk = raw.reshape(-1, 34)
+        d = blk[:, :2].copy().view(np.float16).astype(np.float64).reshape(-1, 1)
+        q = blk[:, 2:].view(np.int8).astype(np.float64)
+        return (d * q).reshape(rows, cols)
+    if gtype == GGML_F32:
+        return raw.view(np.float32).astype(np.float64).reshape(rows, cols)
+    if gtype == GGML_F16:
+        return raw.view(np.float16).astype(np.float64).reshape(rows, cols)
+    if gtype == GGML_BF16:
+        return (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64).reshape(rows, cols)
+    raise ValueError(gtype)

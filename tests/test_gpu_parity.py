@@ -1017,6 +1017,64 @@ def _timeout_path(F, w0):
         assert np.array_equal(a, b)
 
 
+# ---------------------------------------------------------------- the shared expert in a dense GGUF type
+
+def _dense_world(gtype, ffs, seed, **kw):
+    w = H.World(**kw)
+    rng = np.random.default_rng(seed)
+    raw = [H.dense_tensor(gtype, r, c, rng) for r, c in ((ffs, w.n), (ffs, w.n), (w.n, ffs))]
+    dv = [torch.from_numpy(a).cuda() for a in raw]
+    w.layer_obj.set_shared_dense(gtype, *dv, ffs)
+    w.dense = (gtype, *raw, ffs)
+    w._dense_keep = dv
+    return w
+
+
+@pytest.mark.parametrize("gtype", [H.GGML_Q8_0, H.GGML_F16, H.GGML_BF16, H.GGML_F32])
+@pytest.mark.parametrize("T", [1, 3, 8, 200])
+def test_layer_dense_shared_expert(F, gtype, T):
+    """The layer with the shared expert in the model's own GGUF type (frt_moe_layer.shared_dense;
+    the reference runs ffn_*_shexp through linear(), moe_ref.cu:117-123): ids bit-exact, weights
+    1e-6 and outputs within 2e-3 of the oracle's layer with orc_shexp_ffn, for a single token, a
+    3- and an 8-token window (moe_hits) and a 200-token chunk (moe_q2::run), shared ff 768 (not the
+    experts' 512)."""
+    w = _dense_world(gtype, 768, 30 + gtype, cfg=0)
+    x = np.random.default_rng(T + gtype).standard_normal((T, H.N)).astype(np.float32)
+    out, ids, wts = w.gpu_forward(x)
+    ref, rid, rw, _ = O.moe_layer(w.arena_h, w.stride, w.E, w.dense, w.router_h, w.bias_h, w.gate_h, w.n, w.ff, w.K,
+                                  x, threads=8)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    err = H.out_rel(out, ref)
+    print(f"type {gtype} T {T}: out rel err {err:.2e}")
+    assert err <= H.OUT_REL
+
+
+def test_layer_dense_shared_expert_stack_norm(F):
+    """Config 2 layers (RMS norm, Zipf bias, residual) with a Q8_0 shared expert of ff 512, chained
+    by a two-layer stack call (layer by layer: the persistent kernels take only the Q2_0 blob), each
+    layer checked teacher-forced against the oracle, and the stack call equal to the layer calls."""
+    ws_ = []
+    for layer in (0, 1):
+        bias = O.gen_zipf_bias(2, layer, H.E, H.ZIPF_S_STACK)
+        ws_.append(_dense_world(H.GGML_Q8_0, 512, 60 + layer, cfg=2, layer=layer, bias=bias, norm_input=True))
+    x = O.gen_normal(2, 0, O.X_TENSOR, H.N).reshape(1, H.N) * np.float32(3.0)
+    cur = x
+    for w in ws_:
+        out, ids, wts = w.gpu_forward(cur, resid=cur)
+        ref, rid, rw, _ = O.moe_layer(w.arena_h, w.stride, w.E, w.dense, w.router_h, w.bias_h, w.gate_h, w.n, w.ff,
+                                      w.K, cur, threads=8, norm_input=True)
+        assert np.array_equal(ids, rid)
+        assert H.w_rel(wts, rw) <= H.W_REL
+        assert H.out_rel(out - cur, ref) <= H.OUT_REL
+        cur = out
+    st = F.MoeStack([w.layer_obj for w in ws_])
+    o = torch.empty((1, H.N), dtype=torch.float32, device="cuda")
+    st.forward(dev(x), o)
+    torch.cuda.synchronize()
+    assert np.array_equal(o.cpu().numpy(), cur)
+
+
 def _kernels(F, fn):
     """The library kernels fn() launches (names of its per-kernel timing)."""
     import ctypes as C

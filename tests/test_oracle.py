@@ -440,3 +440,88 @@ def test_oracle_vs_compiled_reference_fresh_inputs():
             yr = np.zeros((3, rows), np.float32)
             R.ref_matvec(w, rows, cols, xs, 3, 0, rows, yr, rows, use_avx)
             assert np.array_equal(matvec_q(w, rows, cols, xs, use_avx).view(np.uint32), yr.view(np.uint32))
+
+
+# ---------------------------------------------------------------- the dense shared expert
+
+@pytest.mark.parametrize("gtype", [0, 1, 8, 30])
+def test_dense_mv_closed_form(gtype):
+    """orc_dense_mv against float64 closed forms: dense types, sum_j w_j x_j on the exact float
+    values (within 1e-6 of each row's |w|.|x|); Q8_0, per 32-block the exact integer sum of
+    q_w q_a (numpy int64) times d_w d_a, on the oracle's own Q8_0 of x (pinned elsewhere), within
+    1e-6 of the row's sum of |terms|. A transposed operand or a dropped block fails both."""
+    from tests import helpers as H
+    rng = np.random.default_rng(100 + gtype)
+    rows, cols, T = 96, 512, 3
+    w = H.dense_tensor(gtype, rows, cols, rng)
+    x = rng.standard_normal((T, cols)).astype(np.float32)
+    y = O.dense_mv(gtype, w, rows, cols, x)
+    if gtype == 8:
+        blk = w.reshape(rows, cols // 32, 34)
+        dw = blk[:, :, :2].copy().view(np.float16).astype(np.float64)[..., 0]
+        qw = blk[:, :, 2:].view(np.int8).astype(np.int64)
+        for t in range(T):
+            qa, da = O.quantize_q8(x[t:t + 1])
+            qa = qa.reshape(cols // 32, 32).astype(np.int64)
+            sumi = np.einsum("rbj,bj->rb", qw, qa)
+            terms = sumi * dw * da.reshape(-1).astype(np.float64)
+            want = terms.sum(axis=1)
+            assert np.all(np.abs(y[t] - want) <= 1e-6 * np.abs(terms).sum(axis=1) + 1e-30)
+    else:
+        wv = H.dense_values(gtype, w, rows, cols)
+        want = wv @ x.astype(np.float64).T
+        bound = np.abs(wv) @ np.abs(x.astype(np.float64)).T
+        assert np.all(np.abs(y.T - want) <= 1e-6 * bound)
+    # a known answer: unit weights and unit inputs give cols per row (Q8_0: d = 1, q = 1; x = 1
+    # quantizes to q = 127 with d = fp16(1/127), so each block sums 32 * 127 * d)
+    if gtype == 8:
+        blk = np.zeros((rows * cols // 32, 34), np.uint8)
+        blk[:, :2] = np.array([np.float16(1.0)]).view(np.uint8)
+        blk[:, 2:] = 1
+        y1 = O.dense_mv(8, blk.reshape(-1), rows, cols, np.ones((1, cols), np.float32))
+        d = float(np.float16(1.0 / 127))
+        assert np.allclose(y1, cols / 32 * float(np.float32(4064) * np.float32(d)), rtol=1e-6)
+
+
+@pytest.mark.parametrize("gtype", [0, 1, 8, 30])
+def test_shexp_ffn_composition(gtype):
+    """orc_shexp_ffn equals its composition from orc_dense_mv: gate and up products, SwiGLU in
+    fp32, then the down product (on h quantized to Q8_0 for the Q8_0 type), within 2e-3 of each
+    token's largest output (float rounding of h may move a Q8 code)."""
+    from tests import helpers as H
+    rng = np.random.default_rng(7 + gtype)
+    n, ffs, T = 512, 256, 3
+    g, u, d = (H.dense_tensor(gtype, r, c, rng) for r, c in ((ffs, n), (ffs, n), (n, ffs)))
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    out = O.shexp_ffn(gtype, g, u, d, n, ffs, x)
+    gv = O.dense_mv(gtype, g, ffs, n, x)
+    uv = O.dense_mv(gtype, u, ffs, n, x)
+    h = (gv / (np.float32(1) + np.exp(-gv)) * uv).astype(np.float32)
+    want = O.dense_mv(gtype, d, n, ffs, h)
+    err = np.abs(out - want).max(axis=1) / np.abs(want).max(axis=1)
+    assert err.max() <= 2e-3, err
+    assert np.abs(out).max() > 0
+
+
+def test_moe_layer_with_dense_shared_expert():
+    """orc_moe_layer_shexp with a dense (Q8_0) shared expert = the layer with a zero-weight Q2_0
+    shared blob (routed part only) plus sigmoid(gate) times orc_shexp_ffn, per token."""
+    from tests import helpers as H
+    rng = np.random.default_rng(5)
+    n, ff, E, K, T = 512, 128, 16, 3, 5
+    stride = O.expert_bytes(n, ff)
+    arena = np.concatenate([O.gen_expert(0, 0, e, n, ff) for e in range(E)])
+    zero_shared = np.zeros(stride, np.uint8)   # all scales 0: the shared term vanishes
+    router = (rng.standard_normal((E, n)) * 0.05).astype(np.float32)
+    gate = (rng.standard_normal(n) * 0.05).astype(np.float32)
+    ffs = 256
+    g, u, d = (H.dense_tensor(8, r, c, rng) for r, c in ((ffs, n), (ffs, n), (n, ffs)))
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    out, ids, wts, lg = O.moe_layer(arena, stride, E, (8, g, u, d, ffs), router, None, gate, n, ff, K, x)
+    routed, ids0, wts0, _ = O.moe_layer(arena, stride, E, zero_shared, router, None, gate, n, ff, K, x)
+    assert np.array_equal(ids, ids0) and np.array_equal(wts, wts0)
+    sh = O.shexp_ffn(8, g, u, d, n, ffs, x)
+    gl = np.array([O.lib().orc_dot_canon(gate, np.ascontiguousarray(x[t]), n) for t in range(T)], np.float32)
+    sg = (np.float32(1) / (np.float32(1) + np.exp(-gl))).astype(np.float32)
+    want = routed + sh * sg[:, None]
+    assert np.allclose(out, want, rtol=1e-6, atol=1e-6)
