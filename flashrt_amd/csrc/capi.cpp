@@ -146,10 +146,13 @@ bool shexp_shape_ok(int n, int ffs);
 size_t shexp_ws_bytes(int T, int n, int ffs);
 int shexp_run(int type, const void* g, const void* u, const void* d, int n, int ffs, const float* x, const int8_t* xq,
               const float* xd, int T, float* sh, void* ws, hipStream_t stream);
-int hits_from_ids(const int32_t* ids, int T, int K, const uint8_t* arena, size_t stride, const uint8_t** hit_ptr,
-                  int32_t* hit_n, hipStream_t stream);
-int slot_combine(int T, int K, int n, const int32_t* ids, const float* wts, const float* Y, const float* sh,
-                 const float* gate, const float* resid, float* out, hipStream_t stream);
+int hits_from_ids(const int32_t* ids, int T, int K, const uint8_t* arena, size_t stride, const uint8_t* shared,
+                  const uint8_t** hit_ptr, int32_t* hit_n, hipStream_t stream);
+int slot_combine(int T, int K, int S, int n, const int32_t* ids, const float* wts, const float* Y, const float* sh,
+                 size_t sh_stride, const float* gate, const float* resid, float* out, hipStream_t stream);
+// decode.hip
+bool dec_shape_templated(int n, int ff);
+bool dec_shape_generic(int n, int ff);
 
 constexpr int kDecodeMaxT = 4;
 
@@ -194,9 +197,11 @@ static bool window_path(const frt_moe_layer& L, int T) {
     return T <= 8 && dec_window_fits(T, K, L.d_ff) && router_fused_fits(T, n) && dec_check(1, K, n, L.d_ff) == kOk;
 }
 
-// ---- a layer whose shared expert is given as dense GGUF tensors (frt_moe_layer.shared_dense): the
-// routed experts as per-slot outputs (moe_hits for windows of up to 8 tokens, moe_q2::run beyond),
-// the shared expert (shexp.hip), then the slot combine.
+// ---- the slot path of a layer: the routed experts as per-slot outputs (moe_hits for windows of up to 8
+// tokens, moe_q2::run beyond), the shared expert, then the slot combine. Taken by a layer whose shared
+// expert is given as dense GGUF tensors (frt_moe_layer.shared_dense; shexp.hip), and by windows whose
+// shape is outside the templated decode kernels (n a multiple of 512, ff a multiple of 64 up to 4096:
+// the reference's moe_hits envelope), where the Q2_0 shared expert is moe_hits slot K.
 struct DenseWs {
     float* u;                  // the layer input (normalised with FRT_LAYER_NORM_INPUT)
     int8_t* xq;
@@ -212,7 +217,14 @@ struct DenseWs {
     size_t end;                // bytes from the layer workspace's start
 };
 static bool dense_small(const frt_moe_layer& L, int T) {
-    return T <= 8 && L.top_k <= 32 && dec_check(1, L.top_k, L.d_model, L.d_ff) == kOk;
+    const int S = L.shared_dense ? L.top_k : L.top_k + 1;   // moe_hits slots per token
+    return T <= 8 && S <= 32 && (dec_shape_templated(L.d_model, L.d_ff) || dec_shape_generic(L.d_model, L.d_ff));
+}
+// the slot path: a dense shared expert, or a window of a shape the templated decode kernels lack
+static bool slot_path(const frt_moe_layer& L, int T) {
+    if (L.shared_dense) return true;
+    return T <= 8 && !dec_shape_templated(L.d_model, L.d_ff) && dense_small(L, T) &&
+           router_fused_fits(T, L.d_model);
 }
 static DenseWs dense_carve(uint8_t* p0, uint8_t* p, const frt_moe_layer& L, int T) {
     DenseWs w{};
@@ -225,13 +237,14 @@ static DenseWs dense_carve(uint8_t* p0, uint8_t* p, const frt_moe_layer& L, int 
     w.u = reinterpret_cast<float*>(take(size_t(T) * n * 4));
     w.xq = reinterpret_cast<int8_t*>(take(size_t(T) * n));
     w.xd = reinterpret_cast<float*>(take(size_t(T) * (n / kQ8) * 4));
-    w.hit_ptr = reinterpret_cast<const uint8_t**>(take(size_t(T) * K * 8));
+    w.hit_ptr = reinterpret_cast<const uint8_t**>(take(size_t(T) * (K + 1) * 8));
     w.hit_n = reinterpret_cast<int32_t*>(take(size_t(T) * 4));
-    w.Y = reinterpret_cast<float*>(take(size_t(T) * K * n * 4));
+    w.Y = reinterpret_cast<float*>(take(size_t(T) * (K + 1) * n * 4));
     w.sh = reinterpret_cast<float*>(take(size_t(T) * n * 4));
     w.shws = take(shexp_ws_bytes(T, n, L.shared_ff > 0 ? L.shared_ff : 64));
     if (dense_small(L, T)) {
-        w.rws_bytes = dec_scratch_bytes(hits_chunk(T, K, ff), K, ff);
+        const int S = L.shared_dense ? K : K + 1;
+        w.rws_bytes = dec_scratch_bytes(hits_chunk(T, S, ff), S, ff);
     } else {
         w.part = reinterpret_cast<float*>(take(router_gemm_ws_bytes(T, E, true)));
         w.rws_bytes = pf_workspace_bytes(T, K, n, ff, E, false, false);
@@ -244,11 +257,16 @@ static DenseWs dense_carve(uint8_t* p0, uint8_t* p, const frt_moe_layer& L, int 
 static int dense_layer(const frt_moe_layer& L, const LayerWs& lw, const DenseWs& w, const float* x, int T,
                        const float* resid, float* out, int32_t* ids, float* wts, uint32_t* counts, hipStream_t s) {
     const int E = L.n_expert, K = L.top_k, n = L.d_model, ff = L.d_ff, ffs = L.shared_ff;
-    if (!L.shared_gate || !L.shared_up || !L.shared_down) return set_error(kErrNull, "moe_layer: shared tensors missing");
-    if (!shexp_type_ok(L.shared_type))
-        return set_error(kErrShape, "moe_layer: shared expert type %d (F32, F16, BF16 or Q8_0)", L.shared_type);
-    if (!shexp_shape_ok(n, ffs)) return set_error(kErrShape, "moe_layer: shared_ff=%d n=%d", ffs, n);
+    const bool dense = L.shared_dense != 0;
+    if (dense) {
+        if (!L.shared_gate || !L.shared_up || !L.shared_down) return set_error(kErrNull, "moe_layer: shared tensors missing");
+        if (!shexp_type_ok(L.shared_type))
+            return set_error(kErrShape, "moe_layer: shared expert type %d (F32, F16, BF16 or Q8_0)", L.shared_type);
+        if (!shexp_shape_ok(n, ffs)) return set_error(kErrShape, "moe_layer: shared_ff=%d n=%d", ffs, n);
+    }
     const bool small = dense_small(L, T);
+    const int S = dense ? K : K + 1;   // moe_hits slots per token (the Q2_0 shared expert as slot K)
+    if (!dense && !small) return set_error(kErrShape, "moe_layer: slot path for T=%d K=%d n=%d ff=%d", T, K, n, ff);
     if (!small)
         if (int rc = pf_check(T, K, n, ff, E)) return rc;
     const float* u = x;
@@ -268,29 +286,36 @@ static int dense_layer(const frt_moe_layer& L, const LayerWs& lw, const DenseWs&
         } else if (int rc = router_gemm(u, T, L.router_w, L.router_bias, L.gate_w, E, n, lw.logits, lw.gate, w.part, s)) {
             return rc;
         }
-        if (small || L.shared_type == FRT_GGML_Q8_0)
+        if (small || (dense && L.shared_type == FRT_GGML_Q8_0))
             if (int rc = quantize_q8(u, T, n, w.xq, w.xd, nullptr, nullptr, s)) return rc;
     }
     timing_mark(s, "router");
     if (int rc = route_topk(s, lw.logits, T, E, K, ids, wts, counts, nullptr, 1 << 30)) return rc;
     timing_mark(s, "route_topk");
     if (small) {
-        if (int rc = hits_from_ids(ids, T, K, L.experts, L.stride, w.hit_ptr, w.hit_n, s)) return rc;
-        const int tc = hits_chunk(T, K, ff);
+        if (int rc = hits_from_ids(ids, T, K, L.experts, L.stride, dense ? nullptr : L.shared, w.hit_ptr, w.hit_n, s))
+            return rc;
+        const int tc = hits_chunk(T, S, ff);
         for (int t0 = 0; t0 < T; t0 += tc) {
             const int tn = T - t0 < tc ? T - t0 : tc;
-            if (int rc = dec_hits(w.hit_ptr + size_t(t0) * K, w.hit_n + t0, K, w.xq + size_t(t0) * n,
-                                  w.xd + size_t(t0) * (n / kQ8), n, ff, w.rws, w.Y + size_t(t0) * K * n, s, tn))
+            if (int rc = dec_hits(w.hit_ptr + size_t(t0) * S, w.hit_n + t0, S, w.xq + size_t(t0) * n,
+                                  w.xd + size_t(t0) * (n / kQ8), n, ff, w.rws, w.Y + size_t(t0) * S * n, s, tn))
                 return rc;
         }
     } else if (int rc = pf_run(L.experts, L.stride, E, n, ff, u, ids, T, K, w.Y, w.rws, w.rws_bytes, s, 0, 0)) {
         return rc;
     }
-    if (int rc = shexp_run(L.shared_type, L.shared_gate, L.shared_up, L.shared_down, n, ffs, u, w.xq, w.xd, T, w.sh,
-                           w.shws, s))
-        return rc;
-    timing_mark(s, "shared_expert");
-    if (int rc = slot_combine(T, K, n, ids, wts, w.Y, w.sh, lw.gate, resid, out, s)) return rc;
+    const float* sh = w.Y + size_t(K) * n;   // the Q2_0 shared expert: slot K of each token
+    size_t sh_stride = size_t(S) * n;
+    if (dense) {
+        if (int rc = shexp_run(L.shared_type, L.shared_gate, L.shared_up, L.shared_down, n, ffs, u, w.xq, w.xd, T, w.sh,
+                               w.shws, s))
+            return rc;
+        timing_mark(s, "shared_expert");
+        sh = w.sh;
+        sh_stride = size_t(n);
+    }
+    if (int rc = slot_combine(T, K, S, n, ids, wts, w.Y, sh, sh_stride, lw.gate, resid, out, s)) return rc;
     timing_mark(s, "combine");
     return kOk;
 }
@@ -312,7 +337,7 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
     // the decode window paths a call of T tokens can take, whatever "window_min_t" is set to: the
     // workspace holds the larger of their layouts, so a size queried once stays valid after the option
     // changes (both carve xq and xd first, then their own scratch)
-    if (L.shared_dense) {   // the dense shared expert's path (dense_layer)
+    if (slot_path(L, T)) {   // the slot path (dense_layer)
         const DenseWs d = dense_carve(static_cast<uint8_t*>(base), p, L, T);
         w.bytes = d.end;
         return w;
@@ -509,7 +534,8 @@ int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, con
     if (!hit_ptr || !hit_n || !x || !scratch || !yh) return set_error(kErrNull, "moe_hits: null pointer");
     if (T < 1 || K < 1 || K > 32) return set_error(kErrShape, "moe_hits: T=%d K=%d", T, K);
     const int tc = hits_chunk(T, K, ff);
-    if (int rc = dec_check(1, K, n, ff)) return rc;
+    if (!dec_shape_templated(n, ff) && !dec_shape_generic(n, ff))   // (moe_fast.cu:557)
+        return set_error(kErrShape, "moe_hits: n=%d ff=%d (n %% 512 == 0, ff %% 64 == 0, ff <= 4096)", n, ff);
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint8_t* p = static_cast<uint8_t*>(scratch);
     int8_t* xq = reinterpret_cast<int8_t*>(p);
@@ -548,7 +574,7 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     float* wts_o = wts ? wts : w.wts;
     const int norm = (L->flags & FRT_LAYER_NORM_INPUT) ? 1 : 0;
     timing_mark(s, "begin");
-    if (L->shared_dense) {
+    if (slot_path(*L, T)) {
         uint8_t* b = static_cast<uint8_t*>(ws);
         uint8_t* p = b + (reinterpret_cast<uint8_t*>(w.wts) - b) + up256(size_t(T) * K * 4);
         const DenseWs d = dense_carve(b, p, *L, T);

@@ -38,6 +38,8 @@ namespace {
 // open them, so the list is what a serial pass over the items builds. One workgroup of at least
 // kHitsMaxItems threads (thread i: item i); s_key [kHitsMaxItems] holds the keys, s_live the flags.
 constexpr int kHitsMaxItems = 128;
+constexpr int kGenMaxN = 16384;   // moe_hits rows of any other shape: n and ff at most these
+constexpr int kGenMaxFF = 4096;
 struct GroupLds {
     uint64_t key[kHitsMaxItems];
     int live[kHitsMaxItems], j[kHitsMaxItems], u[kHitsMaxItems];
@@ -723,6 +725,151 @@ __global__ void __launch_bounds__(256) k_hits_down(const DecEntry* __restrict__ 
     }
 }
 
+// ---- moe_hits at any shape of the reference's envelope (n a multiple of 512, ff a multiple of 64 up
+// to 4096; arch/qwen4exp/moe_fast.cu:557): the same products with the row length a runtime value. Each
+// lane walks the 64-blocks lane, lane + 64, ... of a row; the activation blocks are read from the
+// global Q8_0 input (L1 / L2 hits after the first row). Float order: each lane's blocks in order, then
+// the wave's pairwise tree (the shapes of the templated kernels keep those kernels).
+// Gate / up: workgroup (rb, u) takes ff rows 32 rb .. 32 rb + 31 of entry u, 8 rows per wave; SwiGLU
+// and Q8_0 of the 32-row h block per token, as gateup_body.
+__global__ void __launch_bounds__(256) k_gen_gateup(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
+                                                    const int8_t* __restrict__ xq, const float* __restrict__ xd, int n,
+                                                    int ff, int8_t* __restrict__ hq, float* __restrict__ hd) {
+    __shared__ float hrow[kDecMaxT][32];
+    if (int(blockIdx.y) >= *n_ent) return;
+    const DecEntry e = ent[blockIdx.y];
+    const int rb = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nb = n / kBlock;
+    const size_t mb = mat_bytes(ff, n);
+    const uint8_t* gcodes = e.blob;
+    const uint16_t* gscal = reinterpret_cast<const uint16_t*>(e.blob + size_t(ff) * nb * 16);
+    const uint8_t* ucodes = e.blob + mb;
+    const uint16_t* uscal = reinterpret_cast<const uint16_t*>(e.blob + mb + size_t(ff) * nb * 16);
+    for (int i = 0; i < 8; ++i) {
+        const int r = rb * 32 + wave * 8 + i;
+        float ag[kDecMaxT], au[kDecMaxT];
+#pragma unroll
+        for (int j = 0; j < kDecMaxT; ++j) ag[j] = au[j] = 0.0f;
+        for (int b = lane; b < nb; b += 64) {
+            const uint4 cg = gld_u4(gcodes + (size_t(r) * nb + b) * 16);
+            const uint4 cu = gld_u4(ucodes + (size_t(r) * nb + b) * 16);
+            const float dg = h2f(gld<uint16_t>(gscal + size_t(r) * nb + b));
+            const float du = h2f(gld<uint16_t>(uscal + size_t(r) * nb + b));
+            const uint32_t wg[4] = {cg.x, cg.y, cg.z, cg.w}, wu[4] = {cu.x, cu.y, cu.z, cu.w};
+#pragma unroll
+            for (int j = 0; j < kDecMaxT; ++j) {
+                if (j >= e.ntok) break;
+                const int t = e.tok[j];
+                const int4* src = reinterpret_cast<const int4*>(xq + size_t(t) * n + size_t(b) * kBlock);
+                int xa[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int4 v = src[q];
+                    xa[4 * q] = v.x;
+                    xa[4 * q + 1] = v.y;
+                    xa[4 * q + 2] = v.z;
+                    xa[4 * q + 3] = v.w;
+                }
+                int s0 = 0, s1 = 0, g0 = 0, g1 = 0, u0 = 0, u1 = 0;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) s0 = dot4(xa[q], 0x01010101, s0);
+#pragma unroll
+                for (int q = 8; q < 16; ++q) s1 = dot4(xa[q], 0x01010101, s1);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    g0 = dot4(int(wg[w] & 0x03030303u), xa[w], g0);
+                    g0 = dot4(int((wg[w] >> 2) & 0x03030303u), xa[4 + w], g0);
+                    g1 = dot4(int((wg[w] >> 4) & 0x03030303u), xa[8 + w], g1);
+                    g1 = dot4(int((wg[w] >> 6) & 0x03030303u), xa[12 + w], g1);
+                    u0 = dot4(int(wu[w] & 0x03030303u), xa[w], u0);
+                    u0 = dot4(int((wu[w] >> 2) & 0x03030303u), xa[4 + w], u0);
+                    u1 = dot4(int((wu[w] >> 4) & 0x03030303u), xa[8 + w], u1);
+                    u1 = dot4(int((wu[w] >> 6) & 0x03030303u), xa[12 + w], u1);
+                }
+                const float xd0 = xd[size_t(t) * (n / kQ8) + 2 * b], xd1 = xd[size_t(t) * (n / kQ8) + 2 * b + 1];
+                const float fg = float(g0 - s0) * xd0 + float(g1 - s1) * xd1;
+                const float fu = float(u0 - s0) * xd0 + float(u1 - s1) * xd1;
+                ag[j] = ag[j] + fg * dg;
+                au[j] = au[j] + fu * du;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kDecMaxT; ++j) {
+            if (j >= e.ntok) break;
+            const float a = wave_sum_tree(ag[j]), c = wave_sum_tree(au[j]);
+            if (lane == 0) hrow[j][wave * 8 + i] = a / (1.0f + expf(-a)) * c;
+        }
+    }
+    __syncthreads();
+    if (wave < e.ntok) {   // Q8_0 of the 32-row block of h for token slot `wave`
+        const float v = lane < 32 ? hrow[wave][lane] : 0.0f;
+        const float am = half_max(fabsf(v));
+        const float d = q8_scale(am);
+        const float id = q8_inv(d);
+        const int c = e.base + wave;
+        if (lane < 32) hq[size_t(c) * ff + rb * 32 + lane] = int8_t(q8_code(v, id));
+        if (lane == 0) hd[size_t(c) * (ff / kQ8) + rb] = f16_round(d);
+    }
+}
+
+// Down with per-slot outputs: workgroup (x, u) takes output rows 4x .. 4x + 3 (one per wave) of entry
+// u; yh[tok][slot] as k_hits_down writes it.
+__global__ void __launch_bounds__(256) k_gen_down(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
+                                                  const int8_t* __restrict__ hq, const float* __restrict__ hd, int n,
+                                                  int ff, int K, float* __restrict__ yh) {
+    if (int(blockIdx.y) >= *n_ent) return;
+    const DecEntry e = ent[blockIdx.y];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + wave;
+    if (r >= n) return;
+    const int nbf = ff / kBlock;
+    const uint8_t* db = e.blob + 2 * mat_bytes(ff, n);
+    float acc[kDecMaxT];
+#pragma unroll
+    for (int j = 0; j < kDecMaxT; ++j) acc[j] = 0.0f;
+    for (int c = lane; c < nbf; c += 64) {
+        const uint4 cd = gld_u4(db + (size_t(r) * nbf + c) * 16);
+        const float dw = h2f(gld<uint16_t>(db + size_t(n) * nbf * 16 + (size_t(r) * nbf + c) * 2));
+        const uint32_t wd[4] = {cd.x, cd.y, cd.z, cd.w};
+#pragma unroll
+        for (int j = 0; j < kDecMaxT; ++j) {
+            if (j >= e.ntok) break;
+            const int slot = e.base + j;
+            const int4* hp = reinterpret_cast<const int4*>(hq + size_t(slot) * ff + size_t(c) * kBlock);
+            int ha[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int4 v = hp[q];
+                ha[4 * q] = v.x;
+                ha[4 * q + 1] = v.y;
+                ha[4 * q + 2] = v.z;
+                ha[4 * q + 3] = v.w;
+            }
+            int s0 = 0, s1 = 0, q0 = 0, q1 = 0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                q0 = dot4(int(wd[w] & 0x03030303u), ha[w], q0);
+                q0 = dot4(int((wd[w] >> 2) & 0x03030303u), ha[4 + w], q0);
+                q1 = dot4(int((wd[w] >> 4) & 0x03030303u), ha[8 + w], q1);
+                q1 = dot4(int((wd[w] >> 6) & 0x03030303u), ha[12 + w], q1);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) s0 = dot4(ha[q], 0x01010101, s0);
+#pragma unroll
+            for (int q = 8; q < 16; ++q) s1 = dot4(ha[q], 0x01010101, s1);
+            const float f = float(q0 - s0) * hd[size_t(slot) * (ff / kQ8) + 2 * c] +
+                            float(q1 - s1) * hd[size_t(slot) * (ff / kQ8) + 2 * c + 1];
+            acc[j] = acc[j] + f * dw;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kDecMaxT; ++j) {
+        if (j >= e.ntok) break;
+        const float y = wave_sum_tree(acc[j]);
+        if (lane == 0) yh[(size_t(e.tok[j]) * K + e.slot[j]) * n + r] = y;
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- host side
@@ -789,6 +936,17 @@ static int dec_down(const DecScratch& s, int n, int ff, int T, int K, const floa
     return kOk;
 }
 
+// the GEMV shapes instantiated as templates (n / 64 in {16, 32, 40, 48, 64}, ff / 64 in {4, 8, 10, 16})
+bool dec_shape_templated(int n, int ff) {
+    if (n % 64 || ff % 64) return false;
+    const int nb = n / kBlock, nbf = ff / kBlock;
+    return (nb == 16 || nb == 32 || nb == 40 || nb == 48 || nb == 64) && (nbf == 4 || nbf == 8 || nbf == 10 || nbf == 16);
+}
+// the reference's moe_hits envelope (moe_fast.cu:557: n % 512 == 0, ff % 64 == 0, ff <= 4096), n capped here
+bool dec_shape_generic(int n, int ff) {
+    return n >= 512 && n % 512 == 0 && n <= kGenMaxN && ff >= 64 && ff % 64 == 0 && ff <= kGenMaxFF;
+}
+
 int dec_check(int T, int K, int n, int ff) {
     if (T < 1 || T > kDecMaxT) return set_error(kErrShape, "decode: T=%d (1..4)", T);
     if (K < 1 || K > 32 || T * K > 63) return set_error(kErrShape, "decode: K=%d with T=%d (T*K <= 63)", K, T);
@@ -843,11 +1001,24 @@ static int hits_run(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, 
                     int n, int ff, void* scratch, float* yh, hipStream_t stream, int T, const WinComb& wc) {
     if (T < 1 || T > kDecMaxHitsT || K < 1 || K > 32 || T * K > kHitsMaxItems)
         return set_error(kErrShape, "moe_hits: T=%d K=%d (T <= %d, T*K <= %d per launch)", T, K, kDecMaxHitsT, kHitsMaxItems);
-    if (int rc = dec_check(1, K, n, ff)) return rc;   // (k_hits_down stages 64 slots: at most 75 KB of LDS)
+    const bool tmpl = dec_shape_templated(n, ff);
+    if (!tmpl && (wc.arrive || !dec_shape_generic(n, ff)))
+        return set_error(kErrShape, "moe_hits: n=%d ff=%d (n a multiple of 512 up to %d, ff a multiple of 64 up to %d)",
+                         n, ff, kGenMaxN, kGenMaxFF);
     const DecScratch s = dec_carve(scratch, T, K, ff);
     if (hit_ptr) {   // (null: the caller has filled the entry list, dec_window)
         k_hits_group<<<1, kHitsMaxItems, 0, stream>>>(hit_ptr, hit_n, K, T, s.ent, s.n_ent);
         timing_mark(stream, "hits_group");
+    }
+    if (!tmpl) {   // a shape outside the templated set: the runtime-shape kernels
+        const int U_max = T * K < kDecMaxEnt ? T * K : kDecMaxEnt;
+        launch_timed("dec_gateup", k_gen_gateup, dim3(ff / 32, U_max), dim3(256), 0, stream, s.ent, s.n_ent, xq, xd, n,
+                     ff, s.hq, s.hd);
+        FRT_LAUNCHED("moe_hits gate/up");
+        launch_timed("dec_down", k_gen_down, dim3((n + 3) / 4, U_max), dim3(256), 0, stream, s.ent, s.n_ent, s.hq, s.hd,
+                     n, ff, K, yh);
+        FRT_LAUNCHED("moe_hits down");
+        return kOk;
     }
     const int nb = n / kBlock;
     dim3 g1(ff / 32, T * K);

@@ -1,4 +1,5 @@
-// The shared expert in the model's own GGUF type, and the layer path around it.
+// The shared expert in the model's own GGUF type, and the slot path of a layer (per-slot expert
+// outputs, then a combine) that it and the shapes outside the templated decode kernels take.
 //
 // The reference computes the shared expert with ggml's linear() on whatever type the model file
 // ships (arch/qwen4exp/moe_ref.cu:117-123; moe_fast.cu:1056-1068; moe_stream.cu:169-173), then adds
@@ -175,20 +176,26 @@ __global__ void __launch_bounds__(kShNT) k_shexp_mv(const uint8_t* __restrict__ 
     }
 }
 
-// hit lists of moe_hits from routing ids: hit_ptr[t][k] = arena + ids[t][k] * stride, hit_n[t] = K
+// hit lists of moe_hits from routing ids: hit_ptr[t][k] = arena + ids[t][k] * stride for k < K, and,
+// with a shared blob, hit_ptr[t][K] = shared; hit_n[t] = the slots per token (K or K + 1)
 __global__ void k_hits_from_ids(const int32_t* __restrict__ ids, int T, int K, const uint8_t* arena, size_t stride,
-                                const uint8_t** hit_ptr, int32_t* hit_n) {
+                                const uint8_t* shared, const uint8_t** hit_ptr, int32_t* hit_n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < T * K) hit_ptr[i] = arena + size_t(ids[i]) * stride;
-    if (i < T) hit_n[i] = K;
+    const int S = shared ? K + 1 : K;
+    if (i < T * S) {
+        const int t = i / S, k = i % S;
+        hit_ptr[i] = k < K ? arena + size_t(ids[t * K + k]) * stride : shared;
+    }
+    if (i < T) hit_n[i] = S;
 }
 
 // out[t][i] = (resid) + (sum over the token's K slots in ascending expert id of w * Y[slot][i]
-// + sh[t][i] * sigmoid(gate[t])). Y: per-slot rows, slot t * K + k in rank order (moe_hits' yh or
-// moe_q2::run's yd).
-__global__ void __launch_bounds__(256) k_slot_combine(int T, int K, int n, const int32_t* __restrict__ ids,
+// + sh[t][i] * sigmoid(gate[t])). Y: per-slot rows, S slots per token, slot t * S + k in rank order
+// (moe_hits' yh or moe_q2::run's yd); sh: the shared expert's row of token t at sh + t * sh_stride.
+__global__ void __launch_bounds__(256) k_slot_combine(int T, int K, int S, int n, const int32_t* __restrict__ ids,
                                                       const float* __restrict__ wts, const float* __restrict__ Y,
-                                                      const float* __restrict__ sh, const float* __restrict__ gate,
+                                                      const float* __restrict__ sh, size_t sh_stride,
+                                                      const float* __restrict__ gate,
                                                       const float* __restrict__ resid, float* __restrict__ out) {
     __shared__ int s_ord[32];
     __shared__ float s_w[32];
@@ -206,10 +213,10 @@ __global__ void __launch_bounds__(256) k_slot_combine(int T, int K, int n, const
     for (int i = blockIdx.x * 256 + tid; i < n; i += gridDim.x * 256) {
         float acc = 0.0f;
         for (int r = 0; r < K; ++r) {
-            const float p = s_w[r] * Y[(size_t(t) * K + s_ord[r]) * n + i];
+            const float p = s_w[r] * Y[(size_t(t) * S + s_ord[r]) * n + i];
             acc = acc + p;
         }
-        const float p = sh[size_t(t) * n + i] * g;
+        const float p = sh[size_t(t) * sh_stride + i] * g;
         float o = acc + p;
         if (resid) o = resid[size_t(t) * n + i] + o;
         out[size_t(t) * n + i] = o;
@@ -276,19 +283,19 @@ int shexp_run(int type, const void* g, const void* u, const void* d, int n, int 
     return shexp_mv(type, false, d, nullptr, n, ffs, h, nullptr, nullptr, T, sh, stream);
 }
 
-int hits_from_ids(const int32_t* ids, int T, int K, const uint8_t* arena, size_t stride, const uint8_t** hit_ptr,
-                  int32_t* hit_n, hipStream_t stream) {
-    const int cnt = T * K > T ? T * K : T;
-    k_hits_from_ids<<<(cnt + 255) / 256, 256, 0, stream>>>(ids, T, K, arena, stride, hit_ptr, hit_n);
+int hits_from_ids(const int32_t* ids, int T, int K, const uint8_t* arena, size_t stride, const uint8_t* shared,
+                  const uint8_t** hit_ptr, int32_t* hit_n, hipStream_t stream) {
+    const int cnt = T * (K + 1);
+    k_hits_from_ids<<<(cnt + 255) / 256, 256, 0, stream>>>(ids, T, K, arena, stride, shared, hit_ptr, hit_n);
     FRT_LAUNCHED("hit lists");
     return kOk;
 }
 
-int slot_combine(int T, int K, int n, const int32_t* ids, const float* wts, const float* Y, const float* sh,
-                 const float* gate, const float* resid, float* out, hipStream_t stream) {
+int slot_combine(int T, int K, int S, int n, const int32_t* ids, const float* wts, const float* Y, const float* sh,
+                 size_t sh_stride, const float* gate, const float* resid, float* out, hipStream_t stream) {
     if (K < 1 || K > 32) return set_error(kErrShape, "combine: K=%d", K);
     const dim3 grid((n + 255) / 256 < 8 ? (n + 255) / 256 : 8, T);
-    k_slot_combine<<<grid, 256, 0, stream>>>(T, K, n, ids, wts, Y, sh, gate, resid, out);
+    k_slot_combine<<<grid, 256, 0, stream>>>(T, K, S, n, ids, wts, Y, sh, sh_stride, gate, resid, out);
     FRT_LAUNCHED("combine");
     return kOk;
 }

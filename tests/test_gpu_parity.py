@@ -314,6 +314,64 @@ def test_layer_decode_resid(F, w0):
     assert np.array_equal(out_r, (r + out).astype(np.float32))
 
 
+ENVELOPE = [(1536, 768), (512, 2048), (4096, 4096)]
+
+
+@pytest.mark.parametrize("n,ff", ENVELOPE)
+def test_moe_hits_envelope(F, n, ff):
+    """moe_hits at shapes of the reference's envelope outside the templated kernels (n % 512 == 0,
+    ff % 64 == 0, ff <= 4096; arch/qwen4exp/moe_fast.cu:557): T = 1 and 3 tokens (a blob shared by
+    two tokens, pad slots untouched), every written slot within 2e-3 of the oracle's expert_ffn;
+    shapes the reference refuses are refused (FRT_ERR_SHAPE)."""
+    E, K = 12, 4
+    w = H.World(cfg=0, n=n, ff=ff, E=E, K=K)
+    rng = np.random.default_rng(n + ff)
+    for T in (1, 3):
+        x = rng.standard_normal((T, n)).astype(np.float32)
+        hit_n = np.array([K, K - 1, 2][:T], np.int32)
+        experts = np.stack([rng.choice(E, size=K, replace=False) for _ in range(T)]).astype(np.int64)
+        if T > 1:
+            experts[1, 0] = experts[0, 0]
+        ptr = torch.tensor((w.arena.data_ptr() + experts * w.stride).reshape(-1), dtype=torch.int64, device="cuda")
+        yh = torch.full((T, K, n), float("nan"), dtype=torch.float32, device="cuda")
+        scratch = torch.empty(F.moe_hits_scratch_bytes(K, ff, T, n), dtype=torch.uint8, device="cuda")
+        F.moe_hits(ptr, dev(hit_n), K, dev(x), n, ff, scratch, yh, T=T)
+        torch.cuda.synchronize()
+        y = yh.cpu().numpy()
+        for t in range(T):
+            for k in range(K):
+                if k >= hit_n[t]:
+                    assert np.isnan(y[t, k]).all()
+                    continue
+                ref = O.expert_ffn(w.blob(int(experts[t, k])), n, ff, x[t])
+                assert H.out_rel(y[t, k][None], ref) <= H.OUT_REL, (n, ff, T, t, k)
+    x = torch.zeros((1, 1000), dtype=torch.float32, device="cuda")
+    ptr = torch.tensor([w.arena.data_ptr()], dtype=torch.int64, device="cuda")
+    one = torch.ones(1, dtype=torch.int32, device="cuda")
+    yh = torch.empty((1, 1, 4096), dtype=torch.float32, device="cuda")
+    scratch = torch.empty(1 << 24, dtype=torch.uint8, device="cuda")
+    for bad_n, bad_ff in ((1000, ff), (n, 4160), (n, 96), (768, ff)):
+        with pytest.raises(F.FrtError) as e:
+            F.moe_hits(ptr, one, 1, x, bad_n, bad_ff, scratch, yh, T=1)
+        assert e.value.code == -1, (bad_n, bad_ff)
+
+
+@pytest.mark.parametrize("n,ff", ENVELOPE)
+def test_layer_envelope_decode(F, n, ff):
+    """Whole layers at those shapes for T = 1 and 3 (router, routing, the routed experts and the Q2_0
+    shared expert through moe_hits, combine): ids bit-exact, weights 1e-6, outputs within 2e-3 of
+    the oracle."""
+    w = H.World(cfg=0, n=n, ff=ff, E=16, K=4)
+    rng = np.random.default_rng(3 * n + ff)
+    for T in (1, 3):
+        x = rng.standard_normal((T, n)).astype(np.float32)
+        out, ids, wts = w.gpu_forward(x)
+        ref, rid, rw, _ = w.oracle_forward(x)
+        assert np.array_equal(ids, rid), (n, ff, T)
+        assert H.w_rel(wts, rw) <= H.W_REL
+        assert H.out_rel(out, ref) <= H.OUT_REL, (n, ff, T)
+
+
 def test_moe_hits(F, w0):
     """tests/test_moe_hits.cpp:42-166: per-slot expert outputs; pad entries (k >= hit_n) untouched."""
     T, K = 3, 16
