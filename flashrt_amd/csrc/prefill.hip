@@ -644,6 +644,17 @@ __device__ __forceinline__ void store4(_Float16* p, floatx4 v) {
     const half4v h = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
     *reinterpret_cast<half4v*>(p) = h;
 }
+// (chunked down: fp32 only; the chunks run one after another on the stream)
+__device__ __forceinline__ void add4(float* p, floatx4 v) {
+    float4 o = *reinterpret_cast<float4*>(p);
+    o.x += v[0];
+    o.y += v[1];
+    o.z += v[2];
+    o.w += v[3];
+    *reinterpret_cast<float4*>(p) = o;
+}
+template <typename T>
+__device__ __forceinline__ void add4(T*, floatx4) {}
 __device__ __forceinline__ void store4(__hip_bfloat16* p, floatx4 v) {
     p[0] = __float2bfloat16(v[0]);
     p[1] = __float2bfloat16(v[1]);
@@ -651,14 +662,20 @@ __device__ __forceinline__ void store4(__hip_bfloat16* p, floatx4 v) {
     p[3] = __float2bfloat16(v[3]);
 }
 
+// ff above 1024 runs in chunks of K = 1024 (the tile's activations of one chunk in LDS): chunk k0 .. k0
+// + 256 NQ - 1 of h (rows hstride long) against weight blocks k0 / 64 .. of each row, the chunk's
+// products added to yd (fp32) after the first chunk (accumulate).
 template <int NQ, bool TAIL, typename OutT>
 __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ arena, size_t stride, int E,
                                                  const uint8_t* __restrict__ shared_blob, int n, int ff,
                                                  const _Float16* __restrict__ h, const int32_t* __restrict__ bounds,
                                                  const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-                                                 OutT* __restrict__ yd, const int32_t* __restrict__ slot_of) {
-    constexpr int ffp = NQ * 256;      // h row length
+                                                 OutT* __restrict__ yd, const int32_t* __restrict__ slot_of, int k0,
+                                                 int hstride, int accumulate) {
+    constexpr int ffp = NQ * 256;      // the chunk's h length
     const int nbk = ff / kBlock;       // weight blocks per row
+    const int b0 = k0 / kBlock;        // the chunk's first weight block
+    const int nbc = min(nbk - b0, ffp / kBlock);   // weight blocks of the chunk
     constexpr int cpt = ffp / 8;       // 16-byte activation chunks per token
     constexpr int kDB = kTN * cpt / 256;   // activation loads per lane
     if (int(blockIdx.y) >= *n_tiles) return;
@@ -678,7 +695,7 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
 #pragma unroll
     for (int p = 0; p < kDB; ++p) {
         const int P = 256 * p + tid, j = P / cpt, kc = (P % cpt) ^ (j & 15);
-        ldsdma16(h + size_t(sRow[j]) * ffp + kc * 8, smem + P * 16 - lane * 16);
+        ldsdma16(h + size_t(sRow[j]) * hstride + k0 + kc * 8, smem + P * 16 - lane * 16);
     }
 
     uint32_t aoff[4];   // this lane's row in its row block, for tile i
@@ -693,7 +710,7 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
     // read row n - 1 and are never stored
     auto load_a = [&](int s, ARegs& a) {
         const int rb = s / NQ;
-        const uint32_t blk = min(4 * (s % NQ) + lg, nbk - 1);
+        const uint32_t blk = b0 + min(4 * (s % NQ) + lg, nbc - 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const size_t o = size_t(min(rb * 256 + int(aoff[i]), n - 1)) * nbk + blk;
@@ -753,7 +770,10 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int r = rb * 256 + 64 * wave + 16 * i + 4 * lg;
-                            if (r < n) store4(yd + yslot[c] + r, acc[i][c]);   // (n % 4 == 0)
+                            if (r < n) {   // (n % 4 == 0)
+                                if (accumulate) add4(yd + yslot[c] + r, acc[i][c]);
+                                else store4(yd + yslot[c] + r, acc[i][c]);
+                            }
                         }
                     }
 #pragma unroll
@@ -862,7 +882,8 @@ static PfWs pf_carve(void* base, int T, int K, int n, int ff, int E, bool shared
     w.xhi = reinterpret_cast<_Float16*>(take(size_t(T) * pf_np(n) * 2));
     w.xlo = reinterpret_cast<_Float16*>(take(size_t(T) * pf_np(n) * 2));
     w.h16 = reinterpret_cast<_Float16*>(take(size_t(S) * ((ff + 255) & ~255) * 2));
-    w.yd = own_yd ? reinterpret_cast<_Float16*>(take(size_t(S) * n * 2)) : nullptr;
+    // (fp32 when ff > 1024: the down GEMM's chunks are added up in it)
+    w.yd = own_yd ? reinterpret_cast<_Float16*>(take(size_t(S) * n * (ff > 1024 ? 4 : 2))) : nullptr;
     w.bytes = size_t(p - static_cast<uint8_t*>(base));
     return w;
 }
@@ -876,10 +897,9 @@ int quantize_pairs(const float* x, int rows, int n, int np, int blk, _Float16* x
 int pf_check(int T, int K, int n, int ff, int E) {
     if (T < 1 || K < 1 || K > 32 || E < 1 || E > 4096 || K > E) return set_error(kErrShape, "prefill: T=%d K=%d E=%d", T, K, E);
     // n and ff multiples of 128 (moe_q2.cu:516-517); gate/up: slices of 128 ff rows; down: the tile's
-    // h (ff rounded up to 256) in LDS, at most 1024
-    if (n % 128 || n < 128 || n > 65536 || ff % 128 || ff < 128 || ff > 1024)
-        return set_error(kErrShape, "prefill: n=%d ff=%d (n a multiple of 128; ff a multiple of 128 up to 1024)", n,
-                         ff);
+    // h (ff rounded up to 256) in LDS in chunks of at most 1024
+    if (n % 128 || n < 128 || n > 65536 || ff % 128 || ff < 128 || ff > 4096)
+        return set_error(kErrShape, "prefill: n=%d ff=%d (n and ff multiples of 128; ff at most 4096)", n, ff);
     return kOk;
 }
 
@@ -923,19 +943,26 @@ static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uin
                  (const _Float16*)w.xlo, (const int32_t*)w.tok_of, (const int32_t*)w.bounds, (const int2*)w.tiles,
                  (const int32_t*)w.n_tiles, w.h16);
     timing_mark(stream, "pf_gateup");
-    const int nq = (ff + 255) / 256;                     // stretches per h row
-    const size_t down_lds = size_t(kTN) * nq * 256 * 2;  // the tile's activations
-    const bool tail = ((n + 255) / 256) * nq % 4 != 0;
+    const int ffp = (ff + 255) / 256 * 256;   // h row length
+    // ff up to 1024: one pass over the whole h row; beyond, chunks of 1024 added up in fp32 yd
+    if (ffp > 1024 && !std::is_same<OutT, float>::value)
+        return set_error(kErrShape, "prefill: ff=%d above 1024 needs fp32 per-slot outputs", ff);
+    for (int k0 = 0; k0 < ffp; k0 += 1024) {
+        const int nq = (ffp - k0 < 1024 ? ffp - k0 : 1024) / 256;   // stretches of this chunk
+        const size_t down_lds = size_t(kTN) * nq * 256 * 2;         // the tile's activations
+        const bool tail = ((n + 255) / 256) * nq % 4 != 0;
+        const int acc = k0 > 0 ? 1 : 0;
 #define FRT_PF_DOWN(NQV, TL)                                                                                 \
     if (nq == NQV && tail == TL) {                                                                           \
         if (int rc = pf_down_attr<NQV, TL, OutT>(down_lds)) return rc;                                       \
         launch_timed("pf_down", k_pf_down<NQV, TL, OutT>, dim3(1, mt), dim3(256), down_lds, stream, arena, stride, E, \
                      shared_blob, n, ff, (const _Float16*)w.h16, (const int32_t*)w.bounds, (const int2*)w.tiles, \
-                     (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of);                             \
+                     (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of, k0, ffp, acc);               \
     }
-    FRT_PF_DOWN(1, false) FRT_PF_DOWN(1, true) FRT_PF_DOWN(2, false) FRT_PF_DOWN(2, true)
-    FRT_PF_DOWN(3, false) FRT_PF_DOWN(3, true) FRT_PF_DOWN(4, false) FRT_PF_DOWN(4, true)
+        FRT_PF_DOWN(1, false) FRT_PF_DOWN(1, true) FRT_PF_DOWN(2, false) FRT_PF_DOWN(2, true)
+        FRT_PF_DOWN(3, false) FRT_PF_DOWN(3, true) FRT_PF_DOWN(4, false) FRT_PF_DOWN(4, true)
 #undef FRT_PF_DOWN
+    }
     return kOk;
 }
 
@@ -989,6 +1016,14 @@ int pf_moe(const uint8_t* arena, size_t stride, int E, const uint8_t* shared_blo
     if (int rc = pf_check(T, K, n, ff, E)) return rc;
     const PfWs w = pf_carve(ws, T, K, n, ff, E, true, true);
     if (w.bytes > ws_bytes) return set_error(kErrWorkspace, "prefill: workspace %zu < %zu", ws_bytes, w.bytes);
+    if (ff > 1024) {   // fp32 per-slot outputs
+        if (int rc = pf_experts(arena, stride, E, shared_blob, n, ff, x, ids, T, K, w.yd, 0, 32, w, stream)) return rc;
+        launch_timed("pf_combine", k_pf_combine<float>, dim3((n + 1023) / 1024, T), dim3(256), 0, stream,
+                     (const float*)w.yd, ids, wts, gate, T, K, n, 1, resid, out);
+        timing_mark(stream, "pf_combine");
+        FRT_LAUNCHED("prefill combine");
+        return kOk;
+    }
     if (int rc = pf_experts(arena, stride, E, shared_blob, n, ff, x, ids, T, K, w.yd, 2, 32, w, stream)) return rc;
     launch_timed("pf_combine", k_pf_combine<_Float16>, dim3((n + 1023) / 1024, T), dim3(256), 0, stream,
                  (const _Float16*)w.yd, ids, wts, gate, T, K, n, 1, resid, out);

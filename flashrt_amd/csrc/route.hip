@@ -312,6 +312,9 @@ int router_logits(const float* x, int T, const float* W, const float* bias, cons
 int rmsnorm(const float* x, int T, int n, float* u, hipStream_t stream) {
     const unsigned grid = unsigned((T + 3) / 4);
     switch (n / 64) {
+        case 8: k_rmsnorm<8><<<grid, 256, 0, stream>>>(x, T, u); break;
+        case 24: k_rmsnorm<24><<<grid, 256, 0, stream>>>(x, T, u); break;
+        case 56: k_rmsnorm<56><<<grid, 256, 0, stream>>>(x, T, u); break;
         case 32: k_rmsnorm<32><<<grid, 256, 0, stream>>>(x, T, u); break;
         case 40: k_rmsnorm<40><<<grid, 256, 0, stream>>>(x, T, u); break;
         case 16: k_rmsnorm<16><<<grid, 256, 0, stream>>>(x, T, u); break;
@@ -606,14 +609,16 @@ size_t router_gemm_ws_bytes(int T, int E, bool gate) { return size_t(kRgSplit) *
 
 int router_gemm(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
                 float* logits, float* gate, float* part, hipStream_t stream) {
-    if (n != 2048 && n != 2560 && n != 1024 && n != 3072 && n != 4096)
-        return set_error(kErrShape, "router_gemm: n=%d", n);
+    if (n % 512 || n < 512 || n > 4096) return set_error(kErrShape, "router_gemm: n=%d (a multiple of 512 up to 4096)", n);
     if (T < 1 || E < 1 || !part || (gate_w && !gate)) return set_error(kErrShape, "router_gemm: T=%d E=%d", T, E);
     const int E1 = E + (gate_w ? 1 : 0);
     dim3 grid((E1 + 63) / 64, (T + 63) / 64, kRgSplit);
     if (g_router_mfma) {
         switch (n / 64) {
+            case 8: k_router_mfma<8><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
             case 16: k_router_mfma<16><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 24: k_router_mfma<24><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 56: k_router_mfma<56><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
             case 32: k_router_mfma<32><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
             case 40: k_router_mfma<40><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
             case 48: k_router_mfma<48><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
@@ -622,7 +627,10 @@ int router_gemm(const float* x, int T, const float* W, const float* bias, const 
         }
     } else {
         switch (n / 64) {
+            case 8: k_router_gemm<8><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
             case 16: k_router_gemm<16><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 24: k_router_gemm<24><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 56: k_router_gemm<56><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
             case 32: k_router_gemm<32><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
             case 40: k_router_gemm<40><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
             case 48: k_router_gemm<48><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;

@@ -106,7 +106,7 @@ int frt_router_logits(void* stream, const float* x, int T, const float* W, const
                       int E, int n, float* logits, float* gate);
 
 /* ---- the same router logits for many tokens (a prefill chunk) as a K-split GEMM on the matrix
- * cores, bit for bit the canonical order of frt_router_logits. n in {1024, 2048, 2560, 3072, 4096};
+ * cores, bit for bit the canonical order of frt_router_logits. n a multiple of 512 up to 4096;
  * ws of frt_router_gemm_workspace_bytes(T, E, gate_w != NULL). */
 size_t frt_router_gemm_workspace_bytes(int T, int E, int has_gate);
 int frt_router_logits_gemm(void* stream, const float* x, int T, const float* W, const float* bias, const float* gate_w,
@@ -138,7 +138,8 @@ int frt_moe_dispatch(void* stream, const int32_t* ids, int T, int K, int E, int3
  * yd [T*K][n]: slot t*K + k gets down(silu(gate x_t) * up x_t) of expert ids[t*K + k], expert e's
  * blob at experts + e * stride. yd_bf16 selects bf16 output. block64: x and h are quantized in Q8
  * blocks of 64 values instead of the CPU path's 32 (moe_q2.cu's AB = 64). Shapes: n and ff multiples
- * of 128 (moe_q2.cu:516-517), ff at most 1024 (FRT_ERR_SHAPE otherwise). */
+ * of 128 (moe_q2.cu:516-517), ff at most 4096; ff above 1024 takes fp32 yd only (the down GEMM adds
+ * up chunks of 1024 in it). FRT_ERR_SHAPE otherwise. */
 size_t frt_moe_q2_workspace_bytes(int T, int K, int n, int ff, int E);
 int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, const float* x, const int32_t* ids,
                    int T, int K, void* yd, void* ws, size_t ws_bytes, void* stream, int block64, int yd_bf16);
@@ -146,6 +147,7 @@ int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, 
 /* ---- decode expert GEMVs (arch/qwen4exp/moe_fast.hpp:134-142 moe_hits_scratch_bytes, moe_hits).
  * yh [T][K][n]: entry (t, k) for k < hit_n[t] = down(silu(gate x) * up x) of the blob at
  * hit_ptr[t*K + k] (device array of device pointers); entries k >= hit_n[t] are not written.
+ * Shapes: n a multiple of 512 (up to 16384), ff a multiple of 64 up to 4096 (moe_fast.cu:557).
  * x [T][n] fp32, any T >= 1: one launch takes up to 8 tokens (the reference's kMaxWindow,
  * moe_fast.cu:38) and 128 (token, slot) items, and reads each distinct blob once per four of its
  * tokens (moe_fast.cu:195-355); a longer window runs in such launches, one after the other.

@@ -96,7 +96,8 @@ def test_router_logits_bit_exact(F, T, n, with_bias):
     assert np.array_equal(gt.cpu().numpy(), gref)
 
 
-@pytest.mark.parametrize("T,n,with_bias", [(300, 2048, True), (2048, 2048, False), (70, 2560, True), (64, 1024, False)])
+@pytest.mark.parametrize("T,n,with_bias", [(300, 2048, True), (2048, 2048, False), (70, 2560, True), (64, 1024, False),
+                                            (100, 512, True), (65, 1536, False), (40, 3584, True)])
 def test_router_logits_gemm_bit_exact(F, T, n, with_bias):
     """The prefill router GEMM (K split along the canonical tree; the chains on the matrix cores,
     whose f32 MFMA accumulates its four products as a chain of fmas in K order) equals the oracle's
@@ -372,6 +373,51 @@ def test_layer_envelope_decode(F, n, ff):
         assert H.out_rel(out, ref) <= H.OUT_REL, (n, ff, T)
 
 
+@pytest.mark.parametrize("n,ff", ENVELOPE)
+def test_moe_q2_run_envelope(F, n, ff):
+    """moe_q2::run at those shapes, T = 200 (ff above 1024: the down GEMM in chunks of 1024 added up in
+    fp32 yd): sampled slots within 2e-3 of the oracle's expert_ffn; bf16 yd with ff above 1024 and ff
+    above 4096 are refused (FRT_ERR_SHAPE)."""
+    T, K, E = 200, 4, 12
+    w = H.World(cfg=0, n=n, ff=ff, E=E, K=K)
+    rng = np.random.default_rng(7 * n + ff)
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    ids = np.stack([rng.choice(E, size=K, replace=False) for _ in range(T)]).astype(np.int32)
+    nb = F.moe_q2.workspace_bytes(T, K, n, ff, E)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    yd = torch.full((T * K, n), float("nan"), dtype=torch.float32, device="cuda")
+    F.moe_q2.run(w.arena.data_ptr(), w.stride, E, n, ff, dev(x), dev(ids), T, K, yd, ws, nb)
+    torch.cuda.synchronize()
+    y = yd.cpu().numpy().reshape(T, K, n)
+    assert np.isfinite(y).all()
+    for t in range(0, T, 23):
+        for k in range(K):
+            ref = O.expert_ffn(w.blob(int(ids[t, k])), n, ff, x[t])
+            assert H.out_rel(y[t, k][None], ref) <= H.OUT_REL, (n, ff, t, k)
+    if ff > 1024:
+        yb = torch.empty((T * K, n), dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(F.FrtError) as e:
+            F.moe_q2.run(w.arena.data_ptr(), w.stride, E, n, ff, dev(x), dev(ids), T, K, yb, ws, nb, None, False, True)
+        assert e.value.code == -1
+    with pytest.raises(F.FrtError) as e:
+        F.moe_q2.workspace_bytes(T, K, n, 4224, E)
+        F.moe_q2.run(w.arena.data_ptr(), w.stride, E, n, 4224, dev(x), dev(ids), T, K, yd, ws, nb)
+    assert e.value.code in (-1, -2)
+
+
+@pytest.mark.parametrize("n,ff", ENVELOPE)
+def test_layer_envelope_prefill(F, n, ff):
+    """Whole layers at those shapes for a 200-token chunk (router GEMM, routing, the grouped GEMMs
+    with the shared expert as group E, combine): ids bit-exact, weights 1e-6, outputs 2e-3."""
+    w = H.World(cfg=0, n=n, ff=ff, E=16, K=4)
+    x = np.random.default_rng(5 * n + ff).standard_normal((200, n)).astype(np.float32)
+    out, ids, wts = w.gpu_forward(x)
+    ref, rid, rw, _ = w.oracle_forward(x)
+    assert np.array_equal(ids, rid), (n, ff)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    assert H.out_rel(out, ref) <= H.OUT_REL, (n, ff)
+
+
 def test_moe_hits(F, w0):
     """tests/test_moe_hits.cpp:42-166: per-slot expert outputs; pad entries (k >= hit_n) untouched."""
     T, K = 3, 16
@@ -582,13 +628,13 @@ def test_moe_q2_run_shapes(F, n, ff, T, K, E):
 
 
 def test_moe_q2_run_shape_errors(F, w0):
-    """The grouped GEMMs' shape limits (n and ff multiples of 128, ff up to 1024) fail loudly."""
+    """The grouped GEMMs' shape limits (n and ff multiples of 128, ff up to 4096) fail loudly."""
     T, K = 4, 2
     x = torch.zeros((T, 2048), dtype=torch.float32, device="cuda")
     ids = torch.zeros((T, K), dtype=torch.int32, device="cuda")
     ids[:, 1] = 1
     yd = torch.empty((T * K, 2048), dtype=torch.float32, device="cuda")
-    for n, ff in ((2048, 704), (1000, 512), (2048, 1152), (64, 512)):
+    for n, ff in ((2048, 704), (1000, 512), (2048, 4224), (64, 512)):
         nb = F.moe_q2.workspace_bytes(T, K, n, ff, 8)
         ws = torch.empty(max(nb, 1 << 20), dtype=torch.uint8, device="cuda")
         with pytest.raises(F.FrtError) as e:
