@@ -37,7 +37,7 @@ SIGNATURES = {
     "frt_moe_dispatch": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _sz]),
     "frt_moe_q2_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "frt_moe_q2_run": (_i, [_vp, _sz, _i, _i, _i, _vp, _vp, _i, _i, _vp, _vp, _sz, _vp, _i, _i]),
-    "frt_moe_hits_scratch_bytes": (_sz, [_i, _i, _i, _i]),
+    "frt_moe_hits_scratch_bytes": (_sz, [_i, _i, _i]),
     "frt_moe_hits": (_i, [_vp, _vp, _i, _vp, _i, _i, _vp, _vp, _vp, _i]),
     "frt_moe_layer_workspace_bytes": (_sz, [_vp, _i]),
     "frt_moe_layer_forward": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),

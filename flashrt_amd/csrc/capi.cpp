@@ -166,7 +166,9 @@ static int hits_chunk(int T, int K, int ff) {
     while (c > 1 && c * k > 128) --c;
     return T < c ? T : c;
 }
-// decode-side scratch for moe_hits: x quantized (T rows) ahead of the dec scratch of one chunk
+// decode-side scratch for moe_hits: x quantized (T rows of up to kHitsMaxN values) ahead of the dec
+// scratch of one chunk; the size does not depend on the call's n (as the reference's, moe_fast.hpp:134)
+constexpr int kHitsMaxN = 16384;
 static size_t hits_bytes(int K, int ff, int T, int n) {
     return up256(size_t(T) * n) + up256(size_t(T) * (n / kQ8) * 4) + dec_scratch_bytes(hits_chunk(T, K, ff), K, ff);
 }
@@ -528,13 +530,13 @@ int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, 
                   yd_bf16);
 }
 
-size_t frt_moe_hits_scratch_bytes(int K, int ff, int T, int n) { return hits_bytes(K, ff, T, n); }
+size_t frt_moe_hits_scratch_bytes(int K, int ff, int T) { return hits_bytes(K, ff, T, kHitsMaxN); }
 int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const float* x, int n, int ff,
                  void* scratch, float* yh, void* stream, int T) {
     if (!hit_ptr || !hit_n || !x || !scratch || !yh) return set_error(kErrNull, "moe_hits: null pointer");
     if (T < 1 || K < 1 || K > 32) return set_error(kErrShape, "moe_hits: T=%d K=%d", T, K);
     const int tc = hits_chunk(T, K, ff);
-    if (!dec_shape_templated(n, ff) && !dec_shape_generic(n, ff))   // (moe_fast.cu:557)
+    if (n > kHitsMaxN || (!dec_shape_templated(n, ff) && !dec_shape_generic(n, ff)))   // (moe_fast.cu:557)
         return set_error(kErrShape, "moe_hits: n=%d ff=%d (n %% 512 == 0, ff %% 64 == 0, ff <= 4096)", n, ff);
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint8_t* p = static_cast<uint8_t*>(scratch);

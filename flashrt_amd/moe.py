@@ -158,10 +158,10 @@ moe_q2 = SimpleNamespace(workspace_bytes=_q2_workspace_bytes, run=_q2_run)
 
 # ---------------------------------------------------------------- decode hits
 
-def moe_hits_scratch_bytes(K: int, ff: int, T: int = 1, n: int = 4096) -> int:
-    """Scratch for moe_hits; n defaults to the largest d_model decode supports (4096), so that a
-    reference-style call without n is never undersized."""
-    return int(lib().frt_moe_hits_scratch_bytes(K, ff, T, n))
+def moe_hits_scratch_bytes(K: int, ff: int, T: int = 1) -> int:
+    """moe_hits_scratch_bytes (arch/qwen4exp/moe_fast.hpp:134): the scratch of a moe_hits call of T
+    tokens with K slots each, for any n the call takes."""
+    return int(lib().frt_moe_hits_scratch_bytes(K, ff, T))
 
 
 def moe_hits(hit_ptr, hit_n, K: int, x, n: int, ff: int, scratch, yh, stream=None, T: int = 1) -> None:

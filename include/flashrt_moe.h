@@ -151,8 +151,9 @@ int frt_moe_q2_run(const uint8_t* experts, size_t stride, int E, int n, int ff, 
  * x [T][n] fp32, any T >= 1: one launch takes up to 8 tokens (the reference's kMaxWindow,
  * moe_fast.cu:38) and 128 (token, slot) items, and reads each distinct blob once per four of its
  * tokens (moe_fast.cu:195-355); a longer window runs in such launches, one after the other.
- * Activations are quantized to Q8_0 per 32 (the reference quantizes per 64 here). */
-size_t frt_moe_hits_scratch_bytes(int K, int ff, int T, int n);
+ * Activations are quantized to Q8_0 per 32 (the reference quantizes per 64 here); the scratch holds
+ * them for any n the call takes (so its size needs no n, as the reference's). */
+size_t frt_moe_hits_scratch_bytes(int K, int ff, int T);
 int frt_moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const float* x, int n, int ff,
                  void* scratch, float* yh, void* stream, int T);
 

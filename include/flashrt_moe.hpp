@@ -184,8 +184,8 @@ inline void moe_route_topk(hipStream_t stream, const float* logits, int T, int E
 
 // The reference sizes the scratch without d_model; this library also keeps the window's Q8
 // activations there, so the size takes d_model (default: the largest supported, 16384).
-inline size_t moe_hits_scratch_bytes(int K, int ff, int T = 1, int d_model = 16384) {
-    return frt_moe_hits_scratch_bytes(K, ff, T, d_model);
+inline size_t moe_hits_scratch_bytes(int K, int ff, int T = 1) {
+    return frt_moe_hits_scratch_bytes(K, ff, T);
 }
 
 inline void moe_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const float* x, int n, int ff,

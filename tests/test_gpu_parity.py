@@ -335,7 +335,7 @@ def test_moe_hits_envelope(F, n, ff):
             experts[1, 0] = experts[0, 0]
         ptr = torch.tensor((w.arena.data_ptr() + experts * w.stride).reshape(-1), dtype=torch.int64, device="cuda")
         yh = torch.full((T, K, n), float("nan"), dtype=torch.float32, device="cuda")
-        scratch = torch.empty(F.moe_hits_scratch_bytes(K, ff, T, n), dtype=torch.uint8, device="cuda")
+        scratch = torch.empty(F.moe_hits_scratch_bytes(K, ff, T), dtype=torch.uint8, device="cuda")
         F.moe_hits(ptr, dev(hit_n), K, dev(x), n, ff, scratch, yh, T=T)
         torch.cuda.synchronize()
         y = yh.cpu().numpy()
@@ -429,7 +429,7 @@ def test_moe_hits(F, w0):
     base = w0.arena.data_ptr()
     ptr = torch.tensor((base + experts * w0.stride).reshape(-1), dtype=torch.int64, device="cuda")
     yh = torch.full((T, K, H.N), float("nan"), dtype=torch.float32, device="cuda")
-    scratch = torch.empty(F.moe_hits_scratch_bytes(K, H.FF, T, H.N), dtype=torch.uint8, device="cuda")
+    scratch = torch.empty(F.moe_hits_scratch_bytes(K, H.FF, T), dtype=torch.uint8, device="cuda")
     F.moe_hits(ptr, dev(hit_n), K, dev(x), H.N, H.FF, scratch, yh, T=T)
     torch.cuda.synchronize()
     y = yh.cpu().numpy()
@@ -464,7 +464,7 @@ def test_moe_hits_repeated_blob(F, w0):
     base = w0.arena.data_ptr()
     ptr = torch.tensor((base + experts * w0.stride).reshape(-1), dtype=torch.int64, device="cuda")
     yh = torch.full((T, K, H.N), float("nan"), dtype=torch.float32, device="cuda")
-    scratch = torch.empty(F.moe_hits_scratch_bytes(K, H.FF, T, H.N), dtype=torch.uint8, device="cuda")
+    scratch = torch.empty(F.moe_hits_scratch_bytes(K, H.FF, T), dtype=torch.uint8, device="cuda")
     F.moe_hits(ptr, dev(hit_n), K, dev(x), H.N, H.FF, scratch, yh, T=T)
     torch.cuda.synchronize()
     y = yh.cpu().numpy()
@@ -491,7 +491,7 @@ def test_moe_hits_long_windows(F, w0, T, K):
     base = w0.arena.data_ptr()
     ptr = torch.tensor((base + experts * w0.stride).reshape(-1), dtype=torch.int64, device="cuda")
     yh = torch.full((T, K, H.N), float("nan"), dtype=torch.float32, device="cuda")
-    scratch = torch.empty(F.moe_hits_scratch_bytes(K, H.FF, T, H.N), dtype=torch.uint8, device="cuda")
+    scratch = torch.empty(F.moe_hits_scratch_bytes(K, H.FF, T), dtype=torch.uint8, device="cuda")
     F.moe_hits(ptr, dev(hit_n), K, dev(x), H.N, H.FF, scratch, yh, T=T)
     torch.cuda.synchronize()
     y = yh.cpu().numpy()

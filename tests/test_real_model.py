@@ -145,7 +145,7 @@ def _check_model(F, path, t_sizes=(96, 1200), sample=4):
         x = rng.standard_normal((T, n)).astype(np.float32)
         hp = torch.tensor([arena.blob(0, int(e)) for e in ids.reshape(-1)], dtype=torch.int64, device="cuda")
         hn = torch.full((T,), K, dtype=torch.int32, device="cuda")
-        scratch = torch.empty(F.moe_hits_scratch_bytes(K, ff, T, n), dtype=torch.uint8, device="cuda")
+        scratch = torch.empty(F.moe_hits_scratch_bytes(K, ff, T), dtype=torch.uint8, device="cuda")
         yh = torch.full((T, K, n), float("nan"), dtype=torch.float32, device="cuda")
         F.moe_hits(hp, hn, K, torch.from_numpy(x).cuda(), n, ff, scratch, yh, T=T)
         torch.cuda.synchronize()
