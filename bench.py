@@ -484,6 +484,8 @@ def main():
     ap.add_argument("--window-min-t", type=int, default=2,
                     help="windows of at least this many tokens (2..8) take the window path (router, top-k and "
                          "grouping in one workgroup, one moe_hits launch, combine); 9: none")
+    ap.add_argument("--route-waves", type=int, default=1, choices=[1, 8],
+                    help="waves of a persistent decode workgroup that route the token (8: all, 1: one)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -507,6 +509,7 @@ def main():
     F.set_option("window_min_t", args.window_min_t)
     F.set_option("decode_grid", args.decode_grid)
     F.set_option("decode_xcd", args.decode_xcd)
+    F.set_option("route_waves", args.route_waves)
     st = run_stack(args, F, torch)
     if st["sync_error"]:
         sys.exit("bench.py: a persistent decode call ran out of time waiting for another workgroup")

@@ -116,6 +116,7 @@ int dec2_stack(const frt_moe_layer* L, int n_layer, const float* x, float* out, 
                void* sync_ws, hipStream_t stream);
 extern int g_dec2_on;
 extern uint64_t* g_dec2_stamps;
+extern int g_route8;
 extern thread_local bool g_dec1_no_alloc;
 extern int g_dec1_on;
 extern uint64_t g_dec1_ticks;
@@ -726,6 +727,11 @@ int frt_set_option(const char* name, int64_t value) {
     }
     if (!std::strcmp(name, "decode_stamps")) {   // (a device buffer of 64 x 12 x 1024 words, or 0)
         g_dec2_stamps = reinterpret_cast<uint64_t*>(uintptr_t(value));
+        return kOk;
+    }
+    if (!std::strcmp(name, "route_waves")) {   // (8: all waves of the persistent kernels route; 1: one)
+        if (value != 1 && value != 8) return set_error(kErrShape, "set_option: route_waves %lld (1 or 8)", (long long)value);
+        g_route8 = value == 8 ? 1 : 0;
         return kOk;
     }
     if (!std::strcmp(name, "decode_xcd")) {

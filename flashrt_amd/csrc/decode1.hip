@@ -82,6 +82,7 @@ struct Dec1Args {
     const float* next_w;   // the next layer's router [E][n] (cache warming) or null
     uint64_t ticks;        // bound of the call's waits, in ticks of the 100 MHz constant clock
     uint32_t* host_err;    // host-visible flag set with the error word (pinned host memory), or null
+    int route8;            // the single-token routing by all 8 waves (route_8waves) rather than one
     int E, K, ff, norm;
 };
 
@@ -91,6 +92,7 @@ typedef const __attribute__((address_space(4))) Dec1Layer KLayer;
 struct Dec1Lds {
     WinLds R;
     float s_h[32];
+    Route8Lds q8;
 };
 
 template <int NB, int V, int NBF, bool STACK>
@@ -243,6 +245,9 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
     // ---- 2. all logits, the routing, gate/up
     wait_words<(1024 + 1 + kNT1 - 1) / kNT1, kLgStride>(a.lg, E + 1, tag, deadline, &a.sync->err, err_val, a.host_err,
                                             [&](int i, uint32_t p) { s_lg[i] = __uint_as_float(p); });
+    if (E <= 512 && a.route8) {   // the 8 waves route together (each may start on its own logits)
+        route_8waves(s_lg, E, K, LY.arena, a.stride, LY.shared, R, S.q8);
+    } else {
     __syncthreads();
     if (wave == 0) {
         float v[V];
@@ -260,6 +265,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
             for (int i = 0; i < V; ++i) v[i] = s_lg[min(V * lane + i, E - 1)];   // past E: masked by the keys
         }
         route1_wave<V, true>(v, E, K, s_lg[E], LY.arena, a.stride, LY.shared, R);
+    }
     }
     __syncthreads();
     if (R.many) {   // more than 64 candidates (heavily tied logits): four waves select, as window_entries
@@ -591,6 +597,7 @@ thread_local bool g_dec1_no_alloc = false;
 int g_dec1_on = 1;
 uint64_t g_dec1_ticks = 20000000ull;
 int g_dec1_grid_cap = 0;   // workgroups per call (0: one per CU)
+int g_route8 = 0;          // single-token routing by the workgroup's 8 waves (1) or by one wave (0, measured faster)
 
 // Launches the persistent kernel for a filled-in argument block (layers, input and outputs).
 // Returns kErrUnfit (no error message) when the kernel for this shape cannot have every workgroup
@@ -607,6 +614,7 @@ static int dec1_launch(Dec1Args& a, int E, int K, int n, int ff, int norm, void*
     a.xb = reinterpret_cast<uint64_t*>(base + kDec1Head + kDec1Lg + kDec1Hb);
     a.next_w = next_w;
     a.ticks = g_dec1_ticks;
+    a.route8 = g_route8;
     if (!probe_only)
         if (int rc = host_err_flag(dev, !g_dec1_no_alloc, &a.host_err)) return rc;
     a.E = E;

@@ -95,6 +95,7 @@ struct Dec2Args {
     uint64_t ticks;        // bound of the call's waits, in ticks of the 100 MHz constant clock
     uint32_t* host_err;
     uint64_t* stamps;      // measurement only (null: none): [layer][phase][workgroup] constant-clock ticks
+    int route8;            // the single-token routing by all 8 waves (route_8waves) rather than one
     int E, K, ff, nbf, norm;
 };
 
@@ -147,6 +148,7 @@ __global__ void __launch_bounds__(kNT2) k_dec2(Dec2Args a_byval) {
     __shared__ float xd[n / kQ8];
     __shared__ __align__(16) float s_lg[64 * V + 4];
     __shared__ WinLds R;
+    __shared__ Route8Lds s_q8;
     __shared__ float s_part[8][kMaxRW];
     __shared__ uint64_t s_stamp[kMaxStack][kD2Phases];
 
@@ -347,8 +349,11 @@ __global__ void __launch_bounds__(kNT2) k_dec2(Dec2Args a_byval) {
         wait_words_at<(1024 + 1 + kNT2 - kPollT0 - 1) / (kNT2 - kPollT0), kNT2 - kPollT0>(
             [&](int i) { return LGL + i; }, E + 1, tag, deadline, errw, err_val, a.host_err,
             [&](int i, uint32_t p) { s_lg[i] = __uint_as_float(p); }, kPollT0);
-    __syncthreads();
     FRT_D2_STAMP(3);
+    if (E <= 512 && kPollT0 == 0 && a.route8) {   // the 8 waves route together (each may start on its own logits)
+        route_8waves(s_lg, E, K, LY.arena, a.stride, LY.shared, R, s_q8);
+    } else {
+    __syncthreads();
     if (wave == 0) {
         float v[V];
         if (E == 64 * V) {
@@ -365,8 +370,9 @@ __global__ void __launch_bounds__(kNT2) k_dec2(Dec2Args a_byval) {
             for (int i = 0; i < V; ++i) v[i] = s_lg[min(V * lane + i, E - 1)];   // past E: masked by the keys
         }
         route1_wave<V, true>(v, E, K, s_lg[E], LY.arena, a.stride, LY.shared, R);
-        FRT_D2_STAMP(11);
     }
+    }
+    FRT_D2_STAMP(11);
     __syncthreads();
     if (R.many) {   // more than 64 candidates (heavily tied logits): four waves select, as window_entries
         float mx;
@@ -734,6 +740,7 @@ __global__ void k_dec2_zero(uint64_t* p, size_t words) {
 }  // namespace
 
 extern int g_dec1_grid_cap;
+extern int g_route8;
 extern uint64_t g_dec1_ticks;
 int g_dec2_on = 0;   // 1: single-token calls take this kernel where it fits (else decode1.hip's)
 uint64_t* g_dec2_stamps = nullptr;   // measurement only: phase stamps of the next calls (device buffer)
@@ -753,6 +760,7 @@ static int dec2_launch(Dec2Args& a, int E, int K, int n, int ff, int norm, void*
     a.next_w = next_w;
     a.ticks = g_dec1_ticks;
     a.stamps = g_dec2_stamps;
+    a.route8 = g_route8;
     a.E = E;
     a.K = K;
     a.ff = ff;

@@ -143,6 +143,98 @@ __device__ __forceinline__ void route1_wave(const float (&v)[V], int E, int K, f
     }
 }
 
+// ---- The same routing of a single token (selection, tie rule, entries and records as
+// route1_wave<V, true>) by the 8 waves of a workgroup, for latency: wave w holds experts 64 w + lane
+// (E <= 512), one per lane, so each wave's steps are on one value per lane.
+//   1. each wave: a lower bound on its own K-th largest key (wave_kth_key_hi); their maximum T is a
+//      lower bound on the K-th largest key of all E (a wave with K keys >= t puts K keys >= t in all);
+//   2. each wave compacts its keys >= T (every member of the top K) into LDS in ascending id;
+//   3. wave 0 takes the candidates, in ascending id, one per lane, and ranks them by logit (ties: the
+//      lower id, the lower position) as route1_wave does; more than 64 candidates (heavily tied
+//      logits) sets L.many.
+// Every wave of the workgroup calls it (it holds barriers). A wave may start as soon as its own
+// lanes' logits are in s_lg (each lane reads only the word at its expert); s_lg[E] (the shared gate
+// logit) is read by wave 0 after the first barrier.
+struct Route8Lds {
+    uint32_t t[8];
+    int32_t cnt[8];
+    float v[8][64];
+    int32_t id[8][64];
+};
+__device__ __forceinline__ void route_8waves(const float* s_lg, int E, int K, const uint8_t* __restrict__ arena,
+                                             size_t stride, const uint8_t* __restrict__ shared_blob, WinLds& L,
+                                             Route8Lds& Q) {
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6), lane = threadIdx.x & 63;
+    const int e = 64 * wave + lane;
+    const float v = s_lg[min(e, E - 1)];
+    const uint32_t key = e < E ? logit_key(v) : 0u;
+    const uint32_t tw = wave_kth_key_hi(key, K) << 20;
+    if (lane == 0) Q.t[wave] = tw;
+    __syncthreads();
+    uint32_t T = Q.t[0];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) T = max(T, Q.t[w]);
+    const bool c = key != 0u && key >= T;
+    const uint64_t m = __ballot(c);
+    if (c) {
+        const int pos = lanes_below(m);
+        Q.v[wave][pos] = v;
+        Q.id[wave][pos] = e;
+    }
+    if (lane == 0) Q.cnt[wave] = int(__popcll(m));
+    __syncthreads();
+    if (wave != 0) return;
+    int C = 0, sw = 0, si = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        const int cw = Q.cnt[w];
+        if (lane >= C && lane < C + cw) {
+            sw = w;
+            si = lane - C;
+        }
+        C += cw;
+    }
+    if (C > 64) {
+        if (lane == 0) L.many = 1;
+        return;
+    }
+    const bool cl = lane < C;
+    const float cv = cl ? Q.v[sw][si] : 0.0f;
+    const int ci = cl ? Q.id[sw][si] : 0x7fffffff;
+    int rank = 0;   // candidates ahead: higher logit, or equal and lower id (= lower position)
+    for (int j = 0; j < C; ++j) {
+        const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), j));
+        rank += int(o > cv || (o == cv && j < lane));
+    }
+    const bool sel = cl && rank < K;
+    const int u = lanes_below(__ballot(sel));   // entry index: ascending expert id
+    if (sel) {
+        L.ids[0][rank] = ci;
+        L.w[0][rank] = cv;
+        DecEntry& d = L.ent[u];
+        d.blob = arena + size_t(ci) * stride;
+        d.ntok = 1;
+        d.base = u;
+        d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
+        d.slot[0] = rank;
+        d.slot[1] = d.slot[2] = d.slot[3] = -1;
+        d.w[0] = cv;
+        d.w[1] = d.w[2] = d.w[3] = 0.0f;
+    }
+    if (lane == 63) {
+        DecEntry& d = L.ent[K];
+        d.blob = shared_blob;
+        d.ntok = 1;
+        d.base = K;
+        d.tok[0] = d.tok[1] = d.tok[2] = d.tok[3] = 0;
+        d.slot[0] = d.slot[1] = d.slot[2] = d.slot[3] = -1;
+        d.w[0] = s_lg[E];
+        d.w[1] = d.w[2] = d.w[3] = 0.0f;
+        L.n_ent = K + 1;
+        L.many = 0;
+    }
+}
+
 // after_issue() runs once the routing's own loads are issued (a single token: the logits in wave 0),
 // for loads the caller wants in flight during the routing but not waited for before it.
 struct NoLoads {

@@ -1249,6 +1249,31 @@ def test_decode_xcd_layer_matches_oracle(F, case):
     assert err <= H.OUT_REL
 
 
+@pytest.mark.parametrize("xcd", [0, 1])
+@pytest.mark.parametrize("E", [512, 128, 300])
+def test_decode_route_waves_equal(F, xcd, E):
+    """The persistent kernels' single-token routing by all 8 waves (option route_waves = 8) gives the
+    one-wave routing's ids, weights and outputs bit for bit, also with coarse (tied) logits."""
+    w = H.World(cfg=0, E=E)
+    rng = np.random.default_rng(E + xcd)
+    xs = [(rng.standard_normal((1, H.N))).astype(np.float32), np.round(rng.standard_normal((1, H.N)) * 2) / 2]
+    try:
+        F.set_option("decode_xcd", xcd)
+        for x in xs:
+            x = x.astype(np.float32)
+            F.set_option("route_waves", 1)
+            a = w.gpu_forward(x)
+            F.set_option("route_waves", 8)
+            b = w.gpu_forward(x)
+            for p, q in zip(a, b):
+                assert np.array_equal(p, q)
+            ref, rid, rw, _ = w.oracle_forward(x)
+            assert np.array_equal(b[1], rid)
+    finally:
+        F.set_option("route_waves", 1)
+        F.set_option("decode_xcd", 0)
+
+
 def _stack_worlds(nl, x_seed=21):
     layers = []
     for layer in range(nl):
