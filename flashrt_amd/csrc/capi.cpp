@@ -366,7 +366,7 @@ static LayerWs layer_carve(void* base, const frt_moe_layer& L, int T, size_t tot
 // ---- the allocation-free decode entry point's workspace: a file-scope device array, one copy per
 // GPU, held until the process ends. Host code never passes the array's name to a kernel or a copy:
 // it uses the device address hipGetSymbolAddress returns, looked up once per device.
-constexpr size_t kNoAllocScratchBytes = size_t(2) << 20;
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 namespace {
 constexpr int kMaxDevices = 64;

@@ -238,7 +238,7 @@ int frt_set_option(const char* name, int64_t value);
 int frt_moe_layer_sync_error(void* ws, void* stream);
 
 /* ---- allocation-free decode: frt_moe_layer_forward for decode windows (1 <= T <= 4, T * K <= 63)
- * with the workspace taken from a static device array of frt_noalloc_scratch_bytes() (2 MiB) per
+ * with the workspace taken from a static device array of frt_noalloc_scratch_bytes() (4 MiB) per
  * GPU, held until the process ends. No reference counterpart: for callers that cannot allocate
  * device memory or pass a workspace (code under graph capture, tight serving loops, harnesses that
  * forbid allocation). The call itself allocates nothing. All calls on one GPU share that GPU's

@@ -49,6 +49,25 @@ def test_noalloc_matches_workspace_entry(cfg):
         assert not F.noalloc_sync_error()   # no allocation-free call ran out of time
 
 
+def test_noalloc_largest_decode_workspace_fits():
+    """Every decode window the entry point takes (E <= 1024, n <= 4096, ff <= 1024, T <= 4,
+    T * K <= 63) has a layer workspace within the static array."""
+    import ctypes as C
+    import flashrt_amd as F
+    from flashrt_amd._lib import FrtMoeLayer
+    worst = 0
+    for E in (512, 1024):
+        for n in (1024, 2048, 4096):
+            for ff in (512, 1024):
+                for T in (1, 3, 4):
+                    for K in (10, 21, 32):
+                        if T * K > 63:
+                            continue
+                        d = FrtMoeLayer(1, 4096, E, 1, 1, 0, 1, n, ff, K, 0)
+                        worst = max(worst, F.lib().frt_moe_layer_workspace_bytes(C.byref(d), T))
+    assert 0 < worst <= F.noalloc_scratch_bytes(), worst
+
+
 def test_noalloc_refuses_prefill_sizes():
     import flashrt_amd as F
     w = H.World(cfg=0)
@@ -58,4 +77,4 @@ def test_noalloc_refuses_prefill_sizes():
         w.layer_obj.forward_noalloc(x, out, T=8)
     assert e.value.code == -1
     assert "decode windows only" in str(e.value)
-    assert F.noalloc_scratch_bytes() == 2 << 20
+    assert F.noalloc_scratch_bytes() == 4 << 20
