@@ -213,7 +213,7 @@ def time_prefill_layer(F, torch, ml, x, reps):
     dn_flops = 2.0 * S * N * FF
     util = {}
     # gate/up runs as two kernels per layer (tiles of 2-4 token columns, then those of one)
-    for name, parts, fl in (("pf_gateup", ("pf_gateup", "pf_gateup1"), gu_flops), ("pf_down", ("pf_down",), dn_flops)):
+    for name, parts, fl in (("pf_gateup", ("pf_gateup", "pf_gateup1"), gu_flops), ("pf_down", ("pf_down", "pf_down1"), dn_flops)):
         if all(p in kt for p in parts):
             avg_ms = sum(kt[p][0] / kt[p][1] for p in parts)
             util[name] = dict(avg_us=avg_ms * 1e3, tflops=fl / (avg_ms * 1e-3) / 1e12,
@@ -592,7 +592,7 @@ def main():
         pf = run_prefill(args, F, torch)
         line["prefill_2k"] = pf_entry(pf)
         # the prefill roofline: expert flops over the grouped GEMM kernels' summed average durations
-        parts = [p for p in ("pf_gateup", "pf_gateup1", "pf_down") if p in pf.kernels]
+        parts = [p for p in ("pf_gateup", "pf_gateup1", "pf_down", "pf_down1") if p in pf.kernels]
         if parts:
             gemm_ms = sum(pf.kernels[p][0] / pf.kernels[p][1] for p in parts)
             tf = pf.flops / (gemm_ms * 1e-3) / 1e12

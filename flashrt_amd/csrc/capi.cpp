@@ -73,6 +73,9 @@ int router_gemm(const float* x, int T, const float* W, const float* bias, const 
 size_t router_gemm_ws_bytes(int T, int E, bool gate);
 int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xhi, _Float16* xlo,
                 hipStream_t stream);
+int router_gemm_topk(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
+                     float* logits, float* gate, float* part, int K, int32_t* ids, float* wts, uint32_t* counts,
+                     hipStream_t stream);
 int route_topk(hipStream_t stream, const float* logits, int T, int E, int K, int32_t* ids, float* wts, uint32_t* counts,
                uint32_t* tail_counts, int tail_from);
 bool router_fused_fits(int T, int n);
@@ -286,14 +289,16 @@ static int dense_layer(const frt_moe_layer& L, const LayerWs& lw, const DenseWs&
             if (int rc = router_logits(u, T, L.router_w, L.router_bias, L.gate_w, E, n, lw.logits, lw.gate, s, 0, nullptr,
                                        nullptr))
                 return rc;
-        } else if (int rc = router_gemm(u, T, L.router_w, L.router_bias, L.gate_w, E, n, lw.logits, lw.gate, w.part, s)) {
+        } else if (int rc = router_gemm_topk(u, T, L.router_w, L.router_bias, L.gate_w, E, n, lw.logits, lw.gate,
+                                             w.part, K, ids, wts, counts, s)) {
             return rc;
         }
         if (small || (dense && L.shared_type == FRT_GGML_Q8_0))
             if (int rc = quantize_q8(u, T, n, w.xq, w.xd, nullptr, nullptr, s)) return rc;
     }
     timing_mark(s, "router");
-    if (int rc = route_topk(s, lw.logits, T, E, K, ids, wts, counts, nullptr, 1 << 30)) return rc;
+    if (small)   // (the GEMM path selected already)
+        if (int rc = route_topk(s, lw.logits, T, E, K, ids, wts, counts, nullptr, 1 << 30)) return rc;
     timing_mark(s, "route_topk");
     if (small) {
         if (int rc = hits_from_ids(ids, T, K, L.experts, L.stride, dense ? nullptr : L.shared, w.hit_ptr, w.hit_n, s))
@@ -614,11 +619,11 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
         xin = w.u;
         timing_mark(s, "rmsnorm");
     }
-    // router logits and the shared expert's gate logit (row E) as one K-split register-tiled GEMM
-    if (int rc = router_gemm(xin, T, L->router_w, L->router_bias, L->gate_w, E, n, w.logits, w.gate, w.part, s))
+    // router logits and the shared expert's gate logit (row E) as one K-split GEMM, then the top-k
+    // (with the split's combine where E <= 512)
+    if (int rc = router_gemm_topk(xin, T, L->router_w, L->router_bias, L->gate_w, E, n, w.logits, w.gate, w.part, K,
+                                  ids_o, wts_o, counts, s))
         return rc;
-    timing_mark(s, "router_gemm");
-    if (int rc = route_topk(s, w.logits, T, E, K, ids_o, wts_o, counts, nullptr, 1 << 30)) return rc;
     timing_mark(s, "route_topk");
     return pf_moe(L->experts, L->stride, E, L->shared, n, ff, xin, ids_o, wts_o, w.gate, T, K, resid, out, w.rest,
                   w.rest_bytes, s);

@@ -118,11 +118,12 @@ __device__ __forceinline__ void block_excl_scan_v(const int (&v)[N], int (&r)[N]
 // so that the grouped GEMMs start the long tiles first and finish on short ones.
 __device__ __forceinline__ int tile_class(int rows) { return (rows + 15) / 16; }   // 1..4
 
-__global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int nchunk, int E, int T, int K, int shared,
-                                                  int32_t* __restrict__ bounds, int2* __restrict__ tiles,
-                                                  int32_t* __restrict__ n_tiles) {
+// The body of k_pf_scan for a 1024-thread workgroup: s_rows[e] (LDS) holds group e's rows on entry
+// and its first row on exit; bounds[e] gets the same first rows (bounds[E] = T K, bounds[E + 1] =
+// T K + T with the shared group), tiles and n_tiles the tile list.
+__device__ void pf_scan_body(int* s_rows, int E, int T, int shared, int32_t* __restrict__ bounds,
+                             int2* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
     __shared__ int ws[17 * 5];
-    __shared__ int s_rows[4096];   // each group's rows from pass 1 (E <= 4096)
     static_assert(1024 / 64 <= 16, "the wave-total scan covers 16 waves");
     // tiles of each class of group e (rows c): c / 64 full tiles (class 4) and one of class (c % 64)
     auto count = [&](int c, int (&n)[5]) {
@@ -130,15 +131,12 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
         n[4] = c / kTN;
         if (c % kTN) ++n[tile_class(c % kTN)];
     };
-    auto group_rows = [&](int e) { return bounds[e]; };   // (k_pf_colscan's group sizes)
     // pass 1: tiles per class over all groups (the shared group E included)
     int total[5] = {0, 0, 0, 0, 0};
     for (int e0 = 0; e0 < E; e0 += blockDim.x) {
         const int e = e0 + threadIdx.x;
         int n[5];
-        const int c = e < E ? group_rows(e) : 0;
-        if (e < E) s_rows[e] = c;
-        count(c, n);
+        count(e < E ? s_rows[e] : 0, n);
         const int v[4] = {n[1], n[2], n[3], n[4]};
         int r[4], tot[4];
         block_excl_scan_v<4>(v, r, tot, ws);
@@ -156,7 +154,7 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
     int run_rows = 0;
     for (int e0 = 0; e0 < E; e0 += blockDim.x) {
         const int e = e0 + threadIdx.x;
-        const int c = e < E ? s_rows[e] : 0;   // (written by this thread in pass 1)
+        const int c = e < E ? s_rows[e] : 0;   // (each thread reads and then writes only its own groups')
         int n[5], at[5];
         count(c, n);
         const int v[5] = {c, n[1], n[2], n[3], n[4]};
@@ -168,7 +166,8 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
             base[k] += tot[k];
         }
         if (e < E) {
-            bounds[e] = off;   // (each thread reads and then writes only its own groups' entries)
+            bounds[e] = off;
+            s_rows[e] = off;
             for (int i = 0; i < c / kTN; ++i) tiles[at[4] + i] = make_int2(e, i * kTN);
             if (c % kTN) {
                 const int k = tile_class(c % kTN);
@@ -190,6 +189,15 @@ __global__ void __launch_bounds__(1024) k_pf_scan(int32_t* __restrict__ cnt, int
         n_tiles[0] = total[1] + total[2] + total[3] + total[4];
         n_tiles[1] = total[2] + total[3] + total[4];   // the one-column tiles come last
     }
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(1024) k_pf_scan(int E, int T, int shared, int32_t* __restrict__ bounds,
+                                                  int2* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
+    __shared__ int s_rows[4096];   // (E <= 4096)
+    for (int e = threadIdx.x; e < E; e += blockDim.x) s_rows[e] = bounds[e];   // (k_pf_colscan's group sizes)
+    __syncthreads();
+    pf_scan_body(s_rows, E, T, shared, bounds, tiles, n_tiles);
 }
 
 // one wave per chunk; stable ranks from a ballot match-any over the expert id bits
@@ -665,8 +673,11 @@ __device__ __forceinline__ void store4(__hip_bfloat16* p, floatx4 v) {
 // ff above 1024 runs in chunks of K = 1024 (the tile's activations of one chunk in LDS): chunk k0 .. k0
 // + 256 NQ - 1 of h (rows hstride long) against weight blocks k0 / 64 .. of each row, the chunk's
 // products added to yd (fp32) after the first chunk (accumulate).
-template <int NQ, bool TAIL, typename OutT>
-__global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ arena, size_t stride, int E,
+// SMALL: the one-column tiles (16 tokens; the list's n_tiles[1] .. n_tiles[0] - 1) with a quarter of
+// the LDS and at most 168 registers, so 3 workgroups share a CU; otherwise the tiles before them
+// (2-4 columns). Measured on configs[3]: the layer 542 -> 522 us against one kernel for all tiles.
+template <int NQ, bool TAIL, typename OutT, bool SMALL>
+__global__ void __launch_bounds__(256, SMALL ? 3 : 2) k_pf_down(const uint8_t* __restrict__ arena, size_t stride, int E,
                                                  const uint8_t* __restrict__ shared_blob, int n, int ff,
                                                  const _Float16* __restrict__ h, const int32_t* __restrict__ bounds,
                                                  const int2* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
@@ -677,20 +688,24 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
     const int b0 = k0 / kBlock;        // the chunk's first weight block
     const int nbc = min(nbk - b0, ffp / kBlock);   // weight blocks of the chunk
     constexpr int cpt = ffp / 8;       // 16-byte activation chunks per token
-    constexpr int kDB = kTN * cpt / 256;   // activation loads per lane
-    if (int(blockIdx.y) >= *n_tiles) return;
+    constexpr int TN = SMALL ? 16 : kTN;   // tokens per tile
+    constexpr int MC = TN / 16;              // token columns at most
+    constexpr int kDB = TN * cpt / 256;      // activation loads per lane
+    static_assert(TN * cpt % 256 == 0, "whole activation loads per lane");
+    const int ti = SMALL ? n_tiles[1] + int(blockIdx.y) : int(blockIdx.y);
+    if (ti >= n_tiles[SMALL ? 0 : 1]) return;
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int sRow[kTN];
-    const int2 tile = tiles[blockIdx.y];
+    __shared__ int sRow[TN];
+    const int2 tile = tiles[ti];
     const int grp = tile.x;
     const int row0 = bounds[grp] + tile.y;
-    const int cnt = min(kTN, bounds[grp + 1] - row0);
+    const int cnt = min(TN, bounds[grp + 1] - row0);
     const uint8_t* blob = grp < E ? arena + size_t(grp) * stride : shared_blob;
     const uint8_t* const md = blob + 2 * mat_bytes(ff, n);   // down [n][ff]
     const size_t scale_off = size_t(n) * nbk * 16;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lg = lane >> 4;
-    if (tid < kTN) sRow[tid] = row0 + min(tid, cnt - 1);   // past the group's end: repeat a row
+    if (tid < TN) sRow[tid] = row0 + min(tid, cnt - 1);   // past the group's end: repeat a row
     __syncthreads();
 #pragma unroll
     for (int p = 0; p < kDB; ++p) {
@@ -720,9 +735,9 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
     };
     const DqMagic mg = dq_magic();
 
-    size_t yslot[4];   // yd row of this lane's token column c (loaded before the weight stream)
+    size_t yslot[MC];   // yd row of this lane's token column c (loaded before the weight stream)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) yslot[c] = size_t(slot_of[row0 + min(c * 16 + li, cnt - 1)]) * n;
+    for (int c = 0; c < MC; ++c) yslot[c] = size_t(slot_of[row0 + min(c * 16 + li, cnt - 1)]) * n;
     auto run = [&](auto nc) {
         constexpr int NC = decltype(nc)::value;
         ARegs a0, a1, a2, a3;
@@ -760,7 +775,6 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
 #pragma unroll
                     for (int c = 0; c < NC; ++c) acc[i][c] = mfma_acc(av, bv[c], acc[i][c]);
                 }
-                __builtin_amdgcn_sched_barrier(0);   // one K-step of operands live at a time
             }
             if (q == NQ - 1) {   // row block s / NQ done: yd[slot][row], then a fresh block
                 const int rb = s / NQ;
@@ -790,11 +804,14 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(const uint8_t* __restrict__ 
             step(s + 3, qof(s + 3, 3), a3, a2);
         }
     };
-    switch ((cnt + 15) / 16) {   // token columns with at least one real token
-        case 1: run(std::integral_constant<int, 1>{}); break;
-        case 2: run(std::integral_constant<int, 2>{}); break;
-        case 3: run(std::integral_constant<int, 3>{}); break;
-        default: run(std::integral_constant<int, 4>{}); break;
+    if constexpr (SMALL) {
+        run(std::integral_constant<int, 1>{});
+    } else {
+        switch ((cnt + 15) / 16) {   // token columns with at least one real token (2..4 here)
+            case 2: run(std::integral_constant<int, 2>{}); break;
+            case 3: run(std::integral_constant<int, 3>{}); break;
+            default: run(std::integral_constant<int, 4>{}); break;
+        }
     }
 }
 
@@ -914,11 +931,11 @@ static int pf_gemm_attr() {
     return kOk;
 }
 
-template <int NQ, bool TAIL, typename OutT>
+template <int NQ, bool TAIL, typename OutT, bool SMALL>
 static int pf_down_attr(size_t lds) {
     static bool done = false;
     if (!done) {
-        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_down<NQ, TAIL, OutT>),
+        FRT_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_down<NQ, TAIL, OutT, SMALL>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
         done = true;
     }
@@ -949,15 +966,19 @@ static int pf_expert_gemms(const uint8_t* arena, size_t stride, int E, const uin
         return set_error(kErrShape, "prefill: ff=%d above 1024 needs fp32 per-slot outputs", ff);
     for (int k0 = 0; k0 < ffp; k0 += 1024) {
         const int nq = (ffp - k0 < 1024 ? ffp - k0 : 1024) / 256;   // stretches of this chunk
-        const size_t down_lds = size_t(kTN) * nq * 256 * 2;         // the tile's activations
+        const size_t down_lds = size_t(kTN) * nq * 256 * 2;         // the tile's activations (SMALL: a quarter)
         const bool tail = ((n + 255) / 256) * nq % 4 != 0;
         const int acc = k0 > 0 ? 1 : 0;
 #define FRT_PF_DOWN(NQV, TL)                                                                                 \
     if (nq == NQV && tail == TL) {                                                                           \
-        if (int rc = pf_down_attr<NQV, TL, OutT>(down_lds)) return rc;                                       \
-        launch_timed("pf_down", k_pf_down<NQV, TL, OutT>, dim3(1, mt), dim3(256), down_lds, stream, arena, stride, E, \
-                     shared_blob, n, ff, (const _Float16*)w.h16, (const int32_t*)w.bounds, (const int2*)w.tiles, \
-                     (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of, k0, ffp, acc);               \
+        if (int rc = pf_down_attr<NQV, TL, OutT, false>(down_lds)) return rc;                                \
+        if (int rc = pf_down_attr<NQV, TL, OutT, true>(down_lds / 4)) return rc;                             \
+        launch_timed("pf_down", k_pf_down<NQV, TL, OutT, false>, dim3(1, mt), dim3(256), down_lds, stream, arena, \
+                     stride, E, shared_blob, n, ff, (const _Float16*)w.h16, (const int32_t*)w.bounds,            \
+                     (const int2*)w.tiles, (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of, k0, ffp, acc); \
+        launch_timed("pf_down1", k_pf_down<NQV, TL, OutT, true>, dim3(1, mt), dim3(256), down_lds / 4, stream, arena, \
+                     stride, E, shared_blob, n, ff, (const _Float16*)w.h16, (const int32_t*)w.bounds,            \
+                     (const int2*)w.tiles, (const int32_t*)w.n_tiles, ydf, (const int32_t*)w.slot_of, k0, ffp, acc); \
     }
         FRT_PF_DOWN(1, false) FRT_PF_DOWN(1, true) FRT_PF_DOWN(2, false) FRT_PF_DOWN(2, true)
         FRT_PF_DOWN(3, false) FRT_PF_DOWN(3, true) FRT_PF_DOWN(4, false) FRT_PF_DOWN(4, true)
@@ -981,8 +1002,8 @@ static int pf_experts(const uint8_t* arena, size_t stride, int E, const uint8_t*
     timing_mark(stream, "pf_quant_x");
     launch_timed("pf_hist", k_pf_hist, dim3(nchunk), dim3(256), size_t(E) * 4, stream, ids, T * K, E, w.cnt);
     launch_timed("pf_colscan", k_pf_colscan, dim3((E + 3) / 4), dim3(256), 0, stream, w.cnt, nchunk, E, w.bounds);
-    launch_timed("pf_scan", k_pf_scan, dim3(1), dim3(1024), 0, stream, w.cnt, nchunk, E, T, K, shared ? 1 : 0, w.bounds,
-                 w.tiles, w.n_tiles);
+    launch_timed("pf_scan", k_pf_scan, dim3(1), dim3(1024), 0, stream, E, T, shared ? 1 : 0, w.bounds, w.tiles,
+                 w.n_tiles);
     launch_timed("pf_place", k_pf_place, dim3(nchunk + (shared ? (T + 63) / 64 : 0)), dim3(64), size_t(E) * 4, stream,
                  ids, T * K, K, E, id_bits, (const int32_t*)w.cnt, (const int32_t*)w.bounds, w.tok_of, w.slot_of,
                  shared ? T : 0);
@@ -1049,7 +1070,7 @@ int pf_dispatch(const int32_t* ids, int T, int K, int E, int32_t* bounds, int32_
     while ((1 << id_bits) < E) ++id_bits;
     k_pf_hist<<<nchunk, 256, size_t(E) * 4, stream>>>(ids, T * K, E, cnt);
     k_pf_colscan<<<(E + 3) / 4, 256, 0, stream>>>(cnt, nchunk, E, bounds);
-    k_pf_scan<<<1, 1024, 0, stream>>>(cnt, nchunk, E, T, K, 0, bounds, tiles, n_tiles);
+    k_pf_scan<<<1, 1024, 0, stream>>>(E, T, 0, bounds, tiles, n_tiles);
     k_pf_place<<<nchunk, 64, size_t(E) * 4, stream>>>(ids, T * K, K, E, id_bits, cnt, bounds, tok_of, slot_of, 0);
     FRT_LAUNCHED("dispatch");
     return kOk;

@@ -601,47 +601,105 @@ __global__ void __launch_bounds__(256) k_router_combine(const float* __restrict_
     else gate[t] = v;
 }
 
+// k_router_combine and k_route_topk in one pass (E <= 512): wave w of a workgroup takes token
+// 4 blockIdx.x + w, sums its logits from the split's partials in k_router_combine's tree (writing the
+// logits and the gate as it does) into LDS, and selects from there with the same topk_wave.
+__global__ void __launch_bounds__(256) k_route_topk_part(const float* __restrict__ part, int T, int E, int E1,
+                                                         const float* __restrict__ bias, float* __restrict__ logits,
+                                                         float* __restrict__ gate, int K, int32_t* __restrict__ ids,
+                                                         float* __restrict__ wts, uint32_t* counts) {
+    __shared__ __align__(16) float row[4][512];
+    __shared__ float cand_v[4][64];
+    __shared__ int cand_id[4][64];
+    const int wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wave, lane = threadIdx.x & 63;
+    if (t >= T) return;   // (whole waves; no workgroup barrier below)
+    const size_t N = size_t(T) * E1;
+    for (int e = lane; e < E1; e += 64) {
+        const size_t i = size_t(t) * E1 + e;
+        const float v = ((part[i] + part[N + i]) + (part[2 * N + i] + part[3 * N + i])) +
+                        ((part[4 * N + i] + part[5 * N + i]) + (part[6 * N + i] + part[7 * N + i]));
+        if (e < E) {
+            const float l = bias ? v + bias[e] : v;
+            logits[size_t(t) * E + e] = l;
+            row[wave][e] = l;
+        } else {
+            gate[t] = v;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int id = topk_wave<8>(row[wave], E, K, ids + size_t(t) * K, wts + size_t(t) * K, cand_v[wave], cand_id[wave]);
+    if (lane < K && counts) atomicAdd(counts + id, 1u);
+}
+
 }  // namespace
 
 int g_router_mfma = 1;   // the prefill router GEMM on the matrix cores (0: the VALU kernel)
 
 size_t router_gemm_ws_bytes(int T, int E, bool gate) { return size_t(kRgSplit) * T * (E + (gate ? 1 : 0)) * 4; }
 
-int router_gemm(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
-                float* logits, float* gate, float* part, hipStream_t stream) {
+// the K-split partial sums of the router GEMM (logits and gate before the combine)
+static int router_gemm_part(const float* x, int T, const float* W, const float* gate_w, int E, int n, float* gate,
+                            float* part, hipStream_t stream) {
     if (n % 512 || n < 512 || n > 4096) return set_error(kErrShape, "router_gemm: n=%d (a multiple of 512 up to 4096)", n);
     if (T < 1 || E < 1 || !part || (gate_w && !gate)) return set_error(kErrShape, "router_gemm: T=%d E=%d", T, E);
     const int E1 = E + (gate_w ? 1 : 0);
     dim3 grid((E1 + 63) / 64, (T + 63) / 64, kRgSplit);
     if (g_router_mfma) {
         switch (n / 64) {
-            case 8: k_router_mfma<8><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 16: k_router_mfma<16><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 24: k_router_mfma<24><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 56: k_router_mfma<56><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 32: k_router_mfma<32><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 40: k_router_mfma<40><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 48: k_router_mfma<48><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 64: k_router_mfma<64><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 8: launch_timed("router_gemm", k_router_mfma<8>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 16: launch_timed("router_gemm", k_router_mfma<16>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 24: launch_timed("router_gemm", k_router_mfma<24>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 56: launch_timed("router_gemm", k_router_mfma<56>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 32: launch_timed("router_gemm", k_router_mfma<32>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 40: launch_timed("router_gemm", k_router_mfma<40>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 48: launch_timed("router_gemm", k_router_mfma<48>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 64: launch_timed("router_gemm", k_router_mfma<64>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
             default: return set_error(kErrShape, "router_gemm: n=%d", n);
         }
     } else {
         switch (n / 64) {
-            case 8: k_router_gemm<8><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 16: k_router_gemm<16><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 24: k_router_gemm<24><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 56: k_router_gemm<56><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 32: k_router_gemm<32><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 40: k_router_gemm<40><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 48: k_router_gemm<48><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
-            case 64: k_router_gemm<64><<<grid, 256, 0, stream>>>(x, T, W, gate_w, E, part); break;
+            case 8: launch_timed("router_gemm", k_router_gemm<8>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 16: launch_timed("router_gemm", k_router_gemm<16>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 24: launch_timed("router_gemm", k_router_gemm<24>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 56: launch_timed("router_gemm", k_router_gemm<56>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 32: launch_timed("router_gemm", k_router_gemm<32>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 40: launch_timed("router_gemm", k_router_gemm<40>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 48: launch_timed("router_gemm", k_router_gemm<48>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
+            case 64: launch_timed("router_gemm", k_router_gemm<64>, grid, dim3(256), 0, stream, x, T, W, gate_w, E, part); break;
             default: return set_error(kErrShape, "router_gemm: n=%d", n);
         }
     }
     FRT_LAUNCHED("router_gemm");
+    return kOk;
+}
+
+int router_gemm(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
+                float* logits, float* gate, float* part, hipStream_t stream) {
+    if (int rc = router_gemm_part(x, T, W, gate_w, E, n, gate, part, stream)) return rc;
+    const int E1 = E + (gate_w ? 1 : 0);
     const size_t N = size_t(T) * E1;
     k_router_combine<<<unsigned((N + 255) / 256), 256, 0, stream>>>(part, T, E, E1, bias, logits, gate);
     FRT_LAUNCHED("router_combine");
+    return kOk;
+}
+
+// router_gemm then route_topk, the partials' combine fused into the selection where E <= 512
+int router_gemm_topk(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
+                     float* logits, float* gate, float* part, int K, int32_t* ids, float* wts, uint32_t* counts,
+                     hipStream_t stream) {
+    if (E > 512 || K > 64 || K < 1 || K > E) {
+        if (int rc = router_gemm(x, T, W, bias, gate_w, E, n, logits, gate, part, stream)) return rc;
+        return route_topk(stream, logits, T, E, K, ids, wts, counts, nullptr, 1 << 30);
+    }
+    if (int rc = router_gemm_part(x, T, W, gate_w, E, n, gate, part, stream)) return rc;
+    if (!ids || !wts) return set_error(kErrNull, "moe_route_topk: null pointer");
+    const int E1 = E + (gate_w ? 1 : 0);
+    launch_timed("route_topk", k_route_topk_part, dim3((T + 3) / 4), dim3(256), 0, stream, (const float*)part, T, E, E1,
+                 bias, logits, gate, K, ids, wts, counts);
+    FRT_LAUNCHED("router combine + top-k");
     return kOk;
 }
 

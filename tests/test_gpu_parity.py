@@ -185,7 +185,7 @@ def test_route_topk_errors(F):
 
 # ---------------------------------------------------------------- dispatch
 
-@pytest.mark.parametrize("T,skew", [(1, 0.0), (3, 0.0), (2048, 1.2), (8208, 3.0)])
+@pytest.mark.parametrize("T,skew", [(1, 0.0), (3, 0.0), (2048, 1.2), (2457, 0.0), (8208, 3.0)])
 def test_dispatch_bit_exact(F, T, skew):
     E, K = 512, 10
     rng = np.random.default_rng(T)
