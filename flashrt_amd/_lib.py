@@ -30,6 +30,7 @@ SIGNATURES = {
     "frt_moe_route_topk": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i]),
     "frt_router_logits": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "frt_quantize_q8": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
+    "frt_quantize_pairs": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
     "frt_router_widen": (_i, [_vp, _vp, _i, _sz, _vp]),
     "frt_router_gemm_workspace_bytes": (_sz, [_i, _i, _i]),
     "frt_router_logits_gemm": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _sz]),

@@ -73,6 +73,7 @@ int router_gemm(const float* x, int T, const float* W, const float* bias, const 
 size_t router_gemm_ws_bytes(int T, int E, bool gate);
 int quantize_q8(const float* x, int rows, int n, int8_t* xq, float* xd, _Float16* xhi, _Float16* xlo,
                 hipStream_t stream);
+int quantize_pairs(const float* x, int rows, int n, int np, int blk, _Float16* xhi, _Float16* xlo, hipStream_t stream);
 int router_gemm_topk(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
                      float* logits, float* gate, float* part, int K, int32_t* ids, float* wts, uint32_t* counts,
                      hipStream_t stream);
@@ -518,6 +519,12 @@ int frt_router_widen(void* stream, const void* src, int type, size_t count, floa
 int frt_quantize_q8(void* stream, const float* x, int rows, int n, int8_t* xq, float* xd) {
     if (!x || !xq || !xd) return set_error(kErrNull, "quantize_q8: null pointer");
     return quantize_q8(x, rows, n, xq, xd, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int frt_quantize_pairs(void* stream, const float* x, int rows, int n, int block, uint16_t* xhi, uint16_t* xlo) {
+    if (!x || !xhi || !xlo) return set_error(kErrNull, "quantize_pairs: null pointer");
+    return quantize_pairs(x, rows, n, (n + 511) & ~511, block, reinterpret_cast<_Float16*>(xhi),
+                          reinterpret_cast<_Float16*>(xlo), static_cast<hipStream_t>(stream));
 }
 
 size_t frt_moe_dispatch_workspace_bytes(int T, int K, int E) { return pf_dispatch_ws_bytes(T, K, E); }

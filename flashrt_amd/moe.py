@@ -134,6 +134,11 @@ def quantize_q8(x, rows: int, n: int, xq, xd, stream=None) -> None:
     check(lib().frt_quantize_q8(_s(stream), _p(x), rows, n, _p(xq), _p(xd)))
 
 
+def quantize_pairs(x, rows: int, n: int, block: int, xhi, xlo, stream=None) -> None:
+    """frt_quantize_pairs: xhi / xlo [rows][n rounded up to 512] fp16 (the prefill GEMM operand)."""
+    check(lib().frt_quantize_pairs(_s(stream), _p(x), rows, n, block, _p(xhi), _p(xlo)))
+
+
 def moe_dispatch(ids, T: int, K: int, E: int, bounds, tok_of, slot_of, stream=None):
     nbytes = int(lib().frt_moe_dispatch_workspace_bytes(T, K, E))
     ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")

@@ -128,6 +128,14 @@ int frt_router_widen(void* stream, const void* src, int type, size_t count, floa
  * d = fp16(amax/127), q = roundf(x * 127/amax). xq [rows][n] int8, xd [rows][n/32] float. */
 int frt_quantize_q8(void* stream, const float* x, int rows, int n, int8_t* xq, float* xd);
 
+/* ---- the prefill GEMMs' activation operand. No counterpart in the reference (its moe_q2 keeps int8
+ * codes, moe_q2.cu:58-81); exposed so that the format can be checked on its own. Per row: the Q8_0
+ * values a = q * d (blocks of `block` = 32 or 64 values, as frt_quantize_q8 / moe_q2's block64)
+ * as exact fp16 pairs hi = fp16(a), lo = fp16(a - hi), in rows of np = n rounded up to 512; value k
+ * of each 256-wide stretch sits at position perm256(k) of it (the order the GEMM's lanes load),
+ * the pad (k >= n) is zero. n a multiple of 128. xhi / xlo [rows][np] fp16. */
+int frt_quantize_pairs(void* stream, const float* x, int rows, int n, int block, uint16_t* xhi, uint16_t* xlo);
+
 /* ---- dispatch permutation (kernels/cuda/moe_q2.cu:83-168): a stable sort of slots s = t*K + k by
  * ids[s]: bounds [E+1], row r holds slot_of[r] and tok_of[r] = slot_of[r] / K. */
 size_t frt_moe_dispatch_workspace_bytes(int T, int K, int E);

@@ -78,6 +78,42 @@ def test_quantize_q8_bit_exact(F):
     assert np.array_equal(xd.cpu().numpy().reshape(-1), d)
 
 
+def _perm256(k):
+    """Position of value k of a 256-wide stretch in the prefill operand rows: lane group g = k / 64
+    holds its block's codes in the order the Q2_0 dwords unpack (code c of dword d at 2c bits)."""
+    g, j = k >> 6, k & 63
+    c = 4 * (j & 3) + (j >> 4)
+    d = (j & 15) >> 2
+    return 32 * (2 * d + ((c >> 2) & 1)) + 8 * g + 2 * (c & 3) + (c >> 3)
+
+
+@pytest.mark.parametrize("rows,n,blk", [(5, 2048, 32), (3, 640, 32), (4, 2560, 64), (2, 128, 64)])
+def test_quantize_pairs_exact(F, rows, n, blk):
+    """The prefill GEMM's activation operand on its own: hi + lo equals the Q8_0 value q * d of the
+    oracle exactly, hi is fp16(q * d) rounded to nearest even, value k of each stretch sits at
+    perm256(k) (a permutation of the 256 positions), and the pad past n (rows of n rounded up to 512)
+    is zero in both parts."""
+    perm = np.array([_perm256(k) for k in range(256)])
+    assert np.array_equal(np.sort(perm), np.arange(256))
+    rng = np.random.default_rng(rows * n + blk)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    x[0, :blk] = 0.0                      # a zero block
+    x[-1, blk:2 * blk] *= 3e3             # large values
+    np_ = (n + 511) // 512 * 512
+    hi = torch.full((rows, np_), 0x7E00, dtype=torch.int16, device="cuda")   # NaN fill: every position written
+    lo = torch.full((rows, np_), 0x7E00, dtype=torch.int16, device="cuda")
+    F.quantize_pairs(dev(x), rows, n, blk, hi, lo)
+    torch.cuda.synchronize()
+    h = hi.cpu().numpy().view(np.float16).reshape(rows, np_ // 256, 256)
+    l_ = lo.cpu().numpy().view(np.float16).reshape(rows, np_ // 256, 256)
+    h, l_ = h[:, :, perm].reshape(rows, np_), l_[:, :, perm].reshape(rows, np_)   # back to value order
+    qs, d = O.quantize_q8(x, blk)
+    a = (qs.astype(np.float64) * np.repeat(d, 32).astype(np.float64)).reshape(rows, n)
+    assert np.array_equal(h[:, :n].astype(np.float64) + l_[:, :n].astype(np.float64), a)
+    assert np.array_equal(h[:, :n], a.astype(np.float32).astype(np.float16))
+    assert not np.any(h[:, n:]) and not np.any(l_[:, n:])
+
+
 @pytest.mark.parametrize("T,n,with_bias", [(1, 2048, False), (3, 2048, True), (17, 2048, True), (5, 2560, False)])
 def test_router_logits_bit_exact(F, T, n, with_bias):
     E = 512
