@@ -494,7 +494,9 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 template <int L>
 __global__ void __launch_bounds__(256) k_router_mfma(const float* __restrict__ x, int T, const float* __restrict__ W,
                                                      const float* __restrict__ gate_w, int E, float* __restrict__ part) {
-    constexpr int LS = L + 4;                  // LDS row stride (floats)
+    // LDS row stride (floats): L + 2 = 2 mod 4 with (L + 2) / 2 odd, so the 16 rows x 2 K lanes of
+    // each half-wave's operand read hit 32 distinct banks (rows 8 apart no longer share one)
+    constexpr int LS = L + 2;
     constexpr int F4 = L / 4;                  // float4 per row and chain
     constexpr int NP = (64 * F4 + 255) / 256;  // staging passes
     __shared__ __align__(16) float sx[2][64 * LS];
@@ -523,8 +525,12 @@ __global__ void __launch_bounds__(256) k_router_mfma(const float* __restrict__ x
             const int idx = p * 256 + tid;
             if (idx >= 64 * F4) continue;
             const int row = idx / F4, q = idx % F4;
-            *reinterpret_cast<float4*>(&sx[buf][row * LS + q * 4]) = rx[p];
-            *reinterpret_cast<float4*>(&sw[buf][row * LS + q * 4]) = rw[p];
+            float2* dx = reinterpret_cast<float2*>(&sx[buf][row * LS + q * 4]);   // (8-byte aligned rows)
+            float2* dw = reinterpret_cast<float2*>(&sw[buf][row * LS + q * 4]);
+            dx[0] = make_float2(rx[p].x, rx[p].y);
+            dx[1] = make_float2(rx[p].z, rx[p].w);
+            dw[0] = make_float2(rw[p].x, rw[p].y);
+            dw[1] = make_float2(rw[p].z, rw[p].w);
         }
     };
     load(c0);
