@@ -490,18 +490,6 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
             ldsdma16(blo + boff[p] + size_t(st) * Sh::stage_k, b + Sh::slot_b + p * Sh::threads * 16 + wave * 1024);
         }
     };
-    auto read_b = [&](auto nc, int st, int t, half8(&bv)[4][NP]) {   // K-step t of stage st
-        constexpr int NC = decltype(nc)::value;
-        const half8* sb = reinterpret_cast<const half8*>(smem + (st % Sh::stages) * NP * Sh::slot_b);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int j = c * 16 + li, kc = t * 4 + lg;
-#pragma unroll
-            for (int part = 0; part < NP; ++part)
-                bv[c][part] = sb[part * (Sh::slot_b / 16) + j * Sh::cpt + (kc ^ (j & (Sh::cpt - 1)))];
-        }
-    };
-
     floatx4 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -509,20 +497,37 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
         for (int c = 0; c < 4; ++c) acc[i][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     const DqMagic mg = dq_magic();
 
-    // K-step tt (0..7) of a stretch: dequantize the 4 A fragments, NC columns x NP parts x 4 tiles
-    auto mul = [&](auto nc, const ARegs& a, int tt, const half8(&bv)[4][NP]) {
+    // K-step t of stage st (K-step tt of the stretch whose weights are in a), by token column: column
+    // 0's activations are read first, the 4 A fragments dequantized while they land, then each
+    // column's MFMAs run while the next column's activations are read (two column buffers).
+    auto kstep = [&](auto nc, int st, int t, const ARegs& a, int tt) {
         constexpr int NC = decltype(nc)::value;
+        const half8* sb = reinterpret_cast<const half8*>(smem + (st % Sh::stages) * NP * Sh::slot_b);
+        auto rd = [&](int c, half8(&b)[NP]) {
+            const int j = c * 16 + li, kc = t * 4 + lg;
+#pragma unroll
+            for (int part = 0; part < NP; ++part) b[part] = sb[part * (Sh::slot_b / 16) + j * Sh::cpt + (kc ^ (j & (Sh::cpt - 1)))];
+        };
+        half8 b0[NP], b1[NP];
+        rd(0, b0);
+        half8 av[4];
+        const int d = tt >> 1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint4 w = a.cw[i];
-            const int d = tt >> 1;
             const uint32_t cw = d == 0 ? w.x : d == 1 ? w.y : d == 2 ? w.z : w.w;
-            const _Float16 s = __builtin_bit_cast(_Float16, uint16_t(a.sc[i]));
-            const half8 av = dequant8((tt & 1) ? cw >> 8 : cw, half2v{s, s}, mg);
+            const _Float16 sc = __builtin_bit_cast(_Float16, uint16_t(a.sc[i]));
+            av[i] = dequant8((tt & 1) ? cw >> 8 : cw, half2v{sc, sc}, mg);
+        }
 #pragma unroll
-            for (int c = 0; c < NC; ++c)
+        for (int c = 0; c < NC; ++c) {
+            half8(&cur)[NP] = (c & 1) ? b1 : b0;
+            half8(&nxt)[NP] = (c & 1) ? b0 : b1;
+            if (c + 1 < NC) rd(c + 1, nxt);
 #pragma unroll
-                for (int part = 0; part < NP; ++part) acc[i][c] = mfma_acc(av, bv[c][part], acc[i][c]);
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int part = 0; part < NP; ++part) acc[i][c] = mfma_acc(av[i], cur[part], acc[i][c]);
         }
     };
 
@@ -560,11 +565,7 @@ k_pf_gemm(const uint8_t* __restrict__ arena, size_t stride, int E, const uint8_t
                 if (h == 0) load_a(min(q + 1, nq - 1), nxt);
                 issue_b(min(st + Sh::ahead, nst - 1), (st + Sh::ahead) % Sh::stages);   // into stage st - 1's slot
 #pragma unroll
-                for (int t = 0; t < Sh::ksps; ++t) {
-                    half8 bv[4][NP];
-                    read_b(nc, st, t, bv);   // the NC columns the tile uses
-                    mul(nc, cur, Sh::ksps * h + t, bv);
-                }
+                for (int t = 0; t < Sh::ksps; ++t) kstep(nc, st, t, cur, Sh::ksps * h + t);
             }
         };
         for (int q = 0; q < nq; q += 2) {   // nq is even
