@@ -140,8 +140,9 @@ def run_stack(args, F, torch):
     ms_per_step = gpu_ms / args.steps
     log(f"stack: {args.steps} steps x {layers} layers: {gpu_ms:.2f} ms on the stream ({wall * 1e3:.2f} ms wall), "
         f"{ms_per_step * 1e3:.1f} us/token")
-    # the graph-replayed launch alone (what rocprof's kernel average sees): events right around each
-    # replay in a pass of its own, after the input copy
+    # the launch as the timed loop runs it: events right around each graph replay, in a pass of its own
+    # after the input copy (the interval also holds the graph launch's start-up, which rocprof's
+    # kernel time leaves out)
     n_ev = min(64, args.steps)
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_ev)]
     with torch.cuda.stream(stream):

@@ -696,12 +696,11 @@ int router_gemm(const float* x, int T, const float* W, const float* bias, const 
 int router_gemm_topk(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int n,
                      float* logits, float* gate, float* part, int K, int32_t* ids, float* wts, uint32_t* counts,
                      hipStream_t stream) {
-    if (E > 512 || K > 64 || K < 1 || K > E) {
+    if (E > 512 || K > 32 || K < 1 || K > E || !ids || !wts) {   // (route_topk's own checks and errors)
         if (int rc = router_gemm(x, T, W, bias, gate_w, E, n, logits, gate, part, stream)) return rc;
         return route_topk(stream, logits, T, E, K, ids, wts, counts, nullptr, 1 << 30);
     }
     if (int rc = router_gemm_part(x, T, W, gate_w, E, n, gate, part, stream)) return rc;
-    if (!ids || !wts) return set_error(kErrNull, "moe_route_topk: null pointer");
     const int E1 = E + (gate_w ? 1 : 0);
     launch_timed("route_topk", k_route_topk_part, dim3((T + 3) / 4), dim3(256), 0, stream, (const float*)part, T, E, E1,
                  bias, logits, gate, K, ids, wts, counts);
