@@ -91,6 +91,12 @@ int dec_hits(const uint8_t* const* hit_ptr, const int32_t* hit_n, int K, const i
 int dec_check(int T, int K, int n, int ff);
 size_t dec_window_bytes(int T, int K, int n, int ff);
 int dec_window_fits(int T, int K, int ff);
+bool decw_support(int T, int E, int K, int n, int ff);
+int decw_layer(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int K,
+               const uint8_t* arena, size_t stride, const uint8_t* shared, int n, int ff, int norm, const float* resid,
+               float* out, float* logits, float* gate, int32_t* ids, float* wts, uint32_t* counts, void* sync_ws,
+               hipStream_t stream);
+extern int g_decw_on;
 int dec_window(const float* logits, int E, int32_t* ids, float* wts, uint32_t* counts, const float* gate, int T, int K,
                const uint8_t* arena, size_t stride, const uint8_t* shared_blob, const int8_t* xq, const float* xd, int n,
                int ff, const float* resid, float* out, void* scratch, hipStream_t stream);
@@ -601,6 +607,9 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
     if (T == 1 && g_dec1_on && dec1_support(E, K, n, ff) >= 1)   // the whole layer in one persistent launch
         return dec1_layer(x, L->router_w, L->router_bias, L->gate_w, E, K, L->experts, L->stride, L->shared, n, ff,
                           norm, resid, out, ids_o, wts_o, counts, w.sync, L->next_router_w, s);
+    if (T >= 2 && T >= g_window_min_t && decw_support(T, E, K, n, ff))   // a window of 2-4 tokens in one persistent launch
+        return decw_layer(x, T, L->router_w, L->router_bias, L->gate_w, E, K, L->experts, L->stride, L->shared, n, ff,
+                          norm, resid, out, w.logits, w.gate, ids_o, wts_o, counts, w.sync, s);
     if (!window_path(*L, T) && T <= kDecodeMaxT && T * K <= 63) {
         if (int rc = dec_check(T, K, n, ff)) return rc;
         // router logits, the shared gate, the RMS scale and Q8_0 of the input in one launch
@@ -762,6 +771,10 @@ int frt_set_option(const char* name, int64_t value) {
     }
     if (!std::strcmp(name, "router_mfma")) {
         g_router_mfma = value ? 1 : 0;
+        return kOk;
+    }
+    if (!std::strcmp(name, "decode_window_persistent")) {   // 0: windows of 2-4 tokens take the four-launch path
+        g_decw_on = value ? 1 : 0;
         return kOk;
     }
     if (!std::strcmp(name, "sync_ticks")) {

@@ -316,6 +316,45 @@ def test_layer_decode_config1_window(F, min_t):
         assert H.out_rel(o1, out[t:t + 1]) <= H.OUT_REL
 
 
+@pytest.mark.parametrize("T", [2, 3, 4])
+def test_layer_window_persistent(F, T):
+    """Windows of 2-4 tokens as one persistent launch (decodew.hip, the default where the shape fits)
+    against the oracle and against the four-launch window path (option decode_window_persistent = 0):
+    the same ids, outputs within the output bar of the oracle for both, the residual added exactly,
+    the same bits on a second call, and the routing records (counts) of the window."""
+    w1 = H.World(cfg=1)
+    xc = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    F.gen.correlated(xc, 1, 7, O.X_TENSOR, T, H.N, 0.8)
+    x = xc.cpu().numpy()
+    out, ids, wts = w1.gpu_forward(x)
+    ref, rid, rw, _ = w1.oracle_forward(x)
+    assert np.array_equal(ids, rid)
+    assert H.w_rel(wts, rw) <= H.W_REL
+    err = H.out_rel(out, ref)
+    print(f"persistent window T={T}: out rel err {err:.2e}, {len(set(ids.reshape(-1).tolist()))} distinct experts")
+    assert err <= H.OUT_REL
+    again = w1.gpu_forward(x)
+    for a_, b_ in zip(again, (out, ids, wts)):
+        assert np.array_equal(a_, b_)
+    F.set_option("decode_window_persistent", 0)
+    try:
+        o4, i4, w4 = w1.gpu_forward(x)
+    finally:
+        F.set_option("decode_window_persistent", 1)
+    assert np.array_equal(i4, ids)
+    assert H.out_rel(o4, ref) <= H.OUT_REL
+    assert H.out_rel(out, o4) <= H.OUT_REL
+    r = O.gen_normal(1, 0, O.X_TENSOR + 9, T * H.N).reshape(T, H.N)
+    out_r, _, _ = w1.gpu_forward(x, resid=r)
+    assert np.array_equal(out_r, (r + out).astype(np.float32))
+    counts = torch.zeros(H.E, dtype=torch.int32, device="cuda")
+    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    o = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    w1.layer_obj.forward(xd, o, T=T, counts=counts)
+    torch.cuda.synchronize()
+    assert np.array_equal(counts.cpu().numpy(), np.bincount(ids.reshape(-1), minlength=H.E))
+
+
 @pytest.mark.parametrize("T", [5, 8])
 def test_layer_verify_window(F, T):
     """Verify windows of 5 and 8 tokens (the reference's kMaxWindow = 8, moe_fast.cu:38; correlated
@@ -1111,22 +1150,22 @@ def test_decode_fused_router_logits_bit_exact(F, xcd):
     assert got[H.E] == gate
 
 
-@pytest.mark.parametrize("xcd", [0, 1])
-def test_decode_fused_timeout_path(F, w0, xcd):
+@pytest.mark.parametrize("xcd,T", [(0, 1), (1, 1), (0, 3)])
+def test_decode_fused_timeout_path(F, w0, xcd, T):
     """With a zero wait bound the persistent layer cannot wait for the other workgroups: every call
     still completes (no hang), the next call reports it (FRT_ERR_SYNC, without a synchronisation),
     the error word reports it, and the next call with the normal bound returns the right answer
-    again (both persistent kernels)."""
+    again (both single-token persistent kernels, and the persistent window kernel at T = 3)."""
     F.set_option("decode_xcd", xcd)
     try:
-        _timeout_path(F, w0)
+        _timeout_path(F, w0, T)
     finally:
         F.set_option("decode_xcd", 0)
 
 
-def _timeout_path(F, w0):
-    x = O.gen_normal(0, 0, O.X_TENSOR, H.N).reshape(1, H.N)
-    ws = w0.layer_obj.workspace(1)
+def _timeout_path(F, w0, T=1):
+    x = O.gen_normal(0, 0, O.X_TENSOR, T * H.N).reshape(T, H.N)
+    ws = w0.layer_obj.workspace(T)
     good = w0.gpu_forward(x)
     assert not F.layer_sync_error(ws)
     try:
