@@ -10,8 +10,9 @@
 //      publishes the T logits of each row; then the workgroup quantizes the T inputs (Q8_0 per 32)
 //      into its LDS.
 //   2. routing + gate/up: every workgroup waits for the T (E + 1) logits, routes token t with wave t
-//      (topk_wave_fast, k_win_route's selection), groups the (token, slot) items into one entry per
-//      distinct expert (the shared one included) in order of first appearance, as k_win_route does,
+//      (topk_wave_fast, k_win_route's selection), groups the (token, slot) items into entries of at
+//      most 4 tokens per distinct expert (the shared one included) in order of first appearance, as
+//      k_win_route does,
 //      and forms each token's combine list (its routed slots in ascending expert id, then the shared
 //      one). Unit q = b + i G: entry q / RB, ff rows 32 (q % RB) .. + 31, for every token of the
 //      entry; SwiGLU and Q8_0 of each token's 32-row h block, published as 9 words.
@@ -36,10 +37,20 @@ namespace {
 
 constexpr int kNTW = kNTP;          // threads per workgroup
 constexpr int kNWW = kNTW / 64;     // waves per workgroup
-constexpr int kWMaxT = 4;           // tokens per window
+// The kernel is written for windows of up to 8 tokens (the reference's kMaxWindow; entries of at most
+// 4 tokens, k_win_route's split) and takes those of 2-4 tokens. Measured on configs[1]-like windows (same box, the four-launch path
+// beside it): T = 2 26.2 -> 23.5 us, T = 3 29.1 -> 25.8; but T = 5 35.9 -> 37.0 and T = 8 46.4 -> 47.7
+// (at T = 8 each workgroup runs about 5 gate/up units one after another, where the four-launch
+// path spreads them over 3 workgroups of 4 waves per CU), so larger windows keep the four launches.
+constexpr int kWUseT = 4;
 constexpr int kWLgStride = 4;       // words between two published logits (as k_dec1)
-constexpr int kWLgWait = (kWMaxT * 1025 + kNTW - 1) / kNTW;   // logit words per thread to wait for
-constexpr int kWHWait = 16;         // h words per thread to wait for: T (K + 1) ff/32 9 <= 16 * 512
+// logit and h words per thread to wait for, for windows of at most MT tokens: T (E + 1) logits,
+// T (K + 1) ff / 32 9 h words
+template <int MT>
+struct DecwWait {
+    static constexpr int lg = (MT * 1025 + kNTW - 1) / kNTW;
+    static constexpr int h = MT <= 4 ? 16 : 25;
+};
 
 struct DecwArgs {
     const float* W;          // [E][n] router
@@ -58,7 +69,7 @@ struct DecwArgs {
     uint32_t* counts;        // [E] or null
     Dec1Sync* sync;
     uint64_t* lg;            // [T][E + 1] tagged logits, kWLgStride words apart
-    uint64_t* hb;            // [T (K + 1)][ff / 32][9] tagged h blocks of each compact slot
+    uint64_t* hb;            // [T (K + 1)][ff / 32][9] tagged h blocks of each compact slot (after the logits)
     uint64_t ticks;
     uint32_t* host_err;
     uint64_t* stamps;        // measurement only (null: none): [phase][workgroup] constant-clock ticks
@@ -68,35 +79,39 @@ constexpr int kWPhases = 10;
 
 typedef const __attribute__((address_space(4))) DecwArgs KWArgs;
 
+template <int MT>
 struct DecwLds {
-    float cand_v[kWMaxT][128];
-    int cand_id[kWMaxT][128];
-    int32_t ids[kWMaxT][32];
-    float w[kWMaxT][32];
-    uint32_t mask[1025];   // per expert (and E: the shared one), the tokens that chose it
-    int ent_of[1025];      // per expert, its entry
+    float cand_v[MT][128];
+    int cand_id[MT][128];
+    int32_t ids[MT][32];
+    float w[MT][32];
+    uint32_t mask[1025];      // per expert (and E: the shared one), the tokens that chose it
+    int ent_of[1025][2];      // per expert, its entries (tokens 0-3 and 4-7 of its list)
     int wtot[2][2];
-    int item_c[kWMaxT][33];   // compact slot of item (t, k)
-    int comb_c[kWMaxT][33];   // token t's slots: routed in ascending expert id, then the shared one
-    float comb_w[kWMaxT][33];
-    float s_h[kWMaxT][32];
-    DecEntry ent[kWMaxT * 33];
+    int comb_c[MT][33];       // token t's slots: routed in ascending expert id, then the shared one
+    float comb_w[MT][33];
+    float s_h[kDecMaxT][32];
+    DecEntry ent[128];        // at most T (K + 1) <= 128 items
     int n_ent;
 };
 
-template <int NB, int V, int NBF>
+// MT: the largest window of the instance (4, or 8 where the LDS allows)
+template <int NB, int V, int NBF, int MT>
 __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
     (void)a_byval;   // read where it lies (the kernel argument segment), as k_dec1 does
     const KWArgs& a = *(const KWArgs*)__builtin_amdgcn_kernarg_segment_ptr();
     constexpr int n = 64 * NB, L = NB;
-    extern __shared__ __align__(16) uint8_t smem[];   // sh_q [NS][ff] | sh_d [NS][ff/32] | sh_y [NS][8]
-    __shared__ float xs[kWMaxT][64 * (L + 1)];        // each token's x by chain, chains padded by one float
-    __shared__ __align__(16) int8_t xq[kWMaxT][n];
-    __shared__ float xd[kWMaxT][n / kQ8];
-    __shared__ __align__(16) float s_lg[kWMaxT][64 * V + 4];
-    __shared__ DecwLds S;
+    // dynamic: the inputs xs [T][64 (L + 1)] (each token's x by chain, chains padded by one float)
+    // until they are quantized, then sh_q [NS][ff] | sh_d [NS][ff/32] | sh_y [NS][8]
+    extern __shared__ __align__(16) uint8_t smem[];
+    float* const xs0 = reinterpret_cast<float*>(smem);
+    constexpr int XS = 64 * (L + 1);   // floats per token in xs
+    __shared__ __align__(16) int8_t xq[MT][n];
+    __shared__ float xd[MT][n / kQ8];
+    __shared__ __align__(16) float s_lg[MT][64 * V + 4];
+    __shared__ DecwLds<MT> S;
     __shared__ uint32_t s_ep[kNWW];
-    __shared__ float s_r[kWMaxT];
+    __shared__ float s_r[MT];
     __shared__ uint64_t s_stamp[kWPhases];   // (kept in LDS, written out at the end)
 #define FRT_DW_STAMP(ph)                                              \
     do {                                                              \
@@ -139,7 +154,7 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
         for (int i = tid; i < T * (n / 4); i += kNTW) {
             const int t = i / (n / 4), e = 4 * (i % (n / 4));   // L % 4 == 0: a float4 stays within one chain
             const float4 v = x4[i];
-            float* d = &xs[t][(e / L) * (L + 1) + e % L];
+            float* d = xs0 + t * XS + (e / L) * (L + 1) + e % L;
             d[0] = v.x;
             d[1] = v.y;
             d[2] = v.z;
@@ -155,13 +170,13 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
     const uint32_t tag = sync_tag(ep * uint32_t(kMaxStack));
     FRT_DW_STAMP(1);
     if (wave < T) {   // token `wave`'s RMS scale (LDS: the token index below is a runtime value)
-        const float rt = a.norm ? rms_scale_wave<L>(&xs[wave][lane * (L + 1)], n) : 1.0f;
+        const float rt = a.norm ? rms_scale_wave<L>(xs0 + wave * XS + lane * (L + 1), n) : 1.0f;
         if (lane == 0) s_r[wave] = rt;
     }
     __syncthreads();
     auto router_dot = [&](int s, const float (&w)[L], float bv) {
         for (int t = 0; t < T; ++t) {
-            const float* xc = &xs[t][lane * (L + 1)];
+            const float* xc = xs0 + t * XS + lane * (L + 1);
             float acc = 0.0f;
             if (a.norm) {
 #pragma unroll
@@ -204,7 +219,7 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const int k = blk * kQ8 + 16 * h + j;
-                v[j] = xs[t][(k / L) * (L + 1) + k % L];
+                v[j] = xs0[t * XS + (k / L) * (L + 1) + k % L];
                 if (a.norm) v[j] = v[j] * s_r[t];
                 am = fmaxf(am, fabsf(v[j]));
             }
@@ -225,7 +240,7 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
 
     FRT_DW_STAMP(3);
     // ---- 2. all logits, the routing of each token, the entries, gate/up
-    wait_words_at<kWLgWait, kNTW>([&](int i) { return a.lg + size_t(i) * kWLgStride; }, T * (E + 1), tag, deadline,
+    wait_words_at<DecwWait<MT>::lg, kNTW>([&](int i) { return a.lg + size_t(i) * kWLgStride; }, T * (E + 1), tag, deadline,
                                   &a.sync->err, err_val, a.host_err, [&](int i, uint32_t p) {
                                       const int t = i / (E + 1), e = i % (E + 1);
                                       s_lg[t][e] = __uint_as_float(p);
@@ -253,9 +268,10 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
     const int key = live ? (ik < K ? S.ids[it][ik] : E) : 0;
     const uint32_t m = live ? S.mask[key] : 0u;
     const int j = __popc(m & ((1u << it) - 1u)), tot = __popc(m);
-    const bool opens = live && j == 0;
+    const bool opens = live && j % kDecMaxT == 0;   // an entry holds at most 4 tokens (k_win_route's split)
+    const int nt = opens ? min(kDecMaxT, tot - j) : 0;
     int tu = 0, tb = 0;
-    const int su = wave_excl_scan(int(opens), &tu), sb = wave_excl_scan(opens ? tot : 0, &tb);
+    const int su = wave_excl_scan(int(opens), &tu), sb = wave_excl_scan(nt, &tb);
     if (lane == 0 && wave < 2) {
         S.wtot[0][wave] = tu;
         S.wtot[1][wave] = tb;
@@ -265,24 +281,24 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
         const int u = (wave == 1 ? S.wtot[0][0] : 0) + su;
         DecEntry& d = S.ent[u];
         d.blob = key < E ? a.arena + size_t(key) * a.stride : a.shared;
-        d.ntok = tot;
+        d.ntok = nt;
         d.base = (wave == 1 ? S.wtot[1][0] : 0) + sb;
         for (int q = 0; q < kDecMaxT; ++q) {
             d.tok[q] = 0;
             d.slot[q] = -1;
             d.w[q] = 0.0f;
         }
-        S.ent_of[key] = u;
+        S.ent_of[key][j / kDecMaxT] = u;
     }
     if (tid == 0) S.n_ent = S.wtot[0][0] + (N > 64 ? S.wtot[0][1] : 0);
     __syncthreads();
     if (live) {
-        DecEntry& d = S.ent[S.ent_of[key]];
-        d.tok[j] = it;
-        d.slot[j] = ik;
-        d.w[j] = 1.0f;
-        const int c = d.base + j;
-        S.item_c[it][ik] = c;
+        DecEntry& d = S.ent[S.ent_of[key][j / kDecMaxT]];
+        const int sl = j % kDecMaxT;
+        d.tok[sl] = it;
+        d.slot[sl] = ik;
+        d.w[sl] = 1.0f;
+        const int c = d.base + sl;
         if (ik < K) {   // rank of the item among the token's routed experts by id (the ids are distinct)
             int rk = 0;
             for (int k2 = 0; k2 < K; ++k2) rk += int(S.ids[it][k2] < key);
@@ -400,18 +416,17 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
         }
         __syncthreads();   // s_h is free for the next unit
     };
-    // a window has more units than workgroups (about 21 entries x ff / 32 at configs[1]): the second
-    // unit's rows load with the first's, so that the two units cost one weight round trip
+    // a window has more units than workgroups (about 21 entries x ff / 32 at configs[1], 5 units per
+    // workgroup at T = 8): two register sets in turn, unit i + 1's rows in flight while unit i computes
     {
         GuRegs g0, g1;
-        const int q1 = b + G;
         if (b < NU) gu_load(b, g0);
-        if (q1 < NU) gu_load(q1, g1);
-        if (b < NU) gu_compute(b, g0);
-        if (q1 < NU) gu_compute(q1, g1);
-        for (int q = b + 2 * G; q < NU; q += G) {   // (more than two units per workgroup)
-            gu_load(q, g0);
+        for (int q = b; q < NU; q += 2 * G) {
+            if (q + G < NU) gu_load(q + G, g1);
             gu_compute(q, g0);
+            if (q + G >= NU) break;
+            if (q + 2 * G < NU) gu_load(q + 2 * G, g0);
+            gu_compute(q + G, g1);
         }
     }
 
@@ -426,7 +441,7 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
     const bool has_down = r0 < n;
     DownRegs<NBF, BATCH> D;
     if (has_down) down_load<NBF, BATCH, kNWW, true>(S.ent, n_ent, wave, r0, n, ff, D);   // land during the wait
-    wait_words_at<kWHWait, kNTW>([&](int i) { return a.hb + i; }, NS * RB * 9, tag, deadline, &a.sync->err, err_val,
+    wait_words_at<DecwWait<MT>::h, kNTW>([&](int i) { return a.hb + i; }, NS * RB * 9, tag, deadline, &a.sync->err, err_val,
                                  a.host_err, [&](int i, uint32_t p) {
                                      const int c = i / (RB * 9), rem = i % (RB * 9), rb = rem / 9, part = rem % 9;
                                      if (part < 8) *reinterpret_cast<uint32_t*>(sh_q + size_t(c) * ff + rb * 32 + 4 * part) = p;
@@ -492,9 +507,17 @@ size_t dec1_sync_bytes();
 int dec1_eligible(int E, int K, int n, int ff);
 int g_decw_on = 1;   // 1: windows of 2-4 tokens take this kernel where it fits (else the window path)
 
-static size_t decw_smem(int T, int K, int ff) {
+// the sync region's words of a call: T (E + 1) logits kWLgStride words apart, then the h blocks
+static size_t decw_lg_bytes(int T, int E) { return up256(size_t(T) * (E + 1) * kWLgStride * 8); }
+static size_t decw_sync_need(int T, int E, int K, int ff) {
+    return kSyncHead + decw_lg_bytes(T, E) + size_t(T) * (K + 1) * (ff / 32) * 9 * 8;
+}
+
+// the dynamic LDS: the inputs by chain, later the h codes, scales and down rows of the NS slots
+static size_t decw_smem(int T, int K, int n, int ff) {
     const size_t NS = size_t(T) * (K + 1);
-    return NS * ff + NS * (ff / kQ8) * 4 + NS * 8 * 4;
+    const size_t xs = size_t(T) * 64 * (n / 64 + 1) * 4, sh = NS * ff + NS * (ff / kQ8) * 4 + NS * 8 * 4;
+    return xs > sh ? xs : sh;
 }
 
 template <typename Kern>
@@ -534,7 +557,7 @@ static int decw_go(Kern kern, DecwArgs& a, size_t smem, hipStream_t stream, bool
 static int decw_run(DecwArgs& a, int n, size_t smem, hipStream_t stream, bool probe_only) {
     const int nb = n / 64, nbf = a.ff / 64;
     const bool v8 = a.E <= 512;
-#define FRT_DWS(NBV, VV, NBFV) return decw_go(k_decw<NBV, VV, NBFV>, a, smem, stream, probe_only);
+#define FRT_DWS(NBV, VV, NBFV) return decw_go(k_decw<NBV, VV, NBFV, kWUseT>, a, smem, stream, probe_only);
 #define FRT_DWF(NBV, VV)              \
     switch (nbf) {                    \
         case 4: FRT_DWS(NBV, VV, 4)   \
@@ -563,14 +586,16 @@ static int decw_run(DecwArgs& a, int n, size_t smem, hipStream_t stream, bool pr
 // Whether a window of T tokens can take this kernel (shape, the h words one wait covers, every
 // workgroup resident with its LDS).
 bool decw_support(int T, int E, int K, int n, int ff) {
-    if (!g_decw_on || T < 2 || T > kWMaxT || K + 1 > 32 || !dec1_eligible(E, K, n, ff)) return false;
-    if (size_t(T) * (K + 1) * (ff / 32) * 9 > size_t(kWHWait) * kNTW) return false;
+    if (!g_decw_on || T < 2 || T > kWUseT || T * (K + 1) > 128 || !dec1_eligible(E, K, n, ff)) return false;
+    const int hw = DecwWait<kWUseT>::h;
+    if (size_t(T) * (K + 1) * (ff / 32) * 9 > size_t(hw) * kNTW) return false;
+    if (decw_sync_need(T, E, K, ff) > dec1_sync_bytes()) return false;   // (the layer workspace's sync region)
     DecwArgs a{};
     a.T = T;
     a.E = E;
     a.K = K;
     a.ff = ff;
-    return decw_run(a, n, decw_smem(T, K, ff), nullptr, true) == kOk;
+    return decw_run(a, n, decw_smem(T, K, n, ff), nullptr, true) == kOk;
 }
 
 int decw_layer(const float* x, int T, const float* W, const float* bias, const float* gate_w, int E, int K,
@@ -602,7 +627,7 @@ int decw_layer(const float* x, int T, const float* W, const float* bias, const f
     uint8_t* base = static_cast<uint8_t*>(sync_ws);
     a.sync = reinterpret_cast<Dec1Sync*>(base);
     a.lg = reinterpret_cast<uint64_t*>(base + kSyncHead);
-    a.hb = reinterpret_cast<uint64_t*>(base + kSyncHead + kSyncLg);
+    a.hb = reinterpret_cast<uint64_t*>(base + kSyncHead + decw_lg_bytes(T, E));   // (after this call's logits)
     a.ticks = g_dec1_ticks;
     a.stamps = g_dec2_stamps;
     if (int rc = host_err_flag(dev, !g_dec1_no_alloc, &a.host_err)) return rc;
@@ -613,7 +638,7 @@ int decw_layer(const float* x, int T, const float* W, const float* bias, const f
             FRT_LAUNCHED("decode window zero");
         }
     }
-    const int rc = decw_run(a, n, decw_smem(T, K, ff), stream, false);
+    const int rc = decw_run(a, n, decw_smem(T, K, n, ff), stream, false);
     return rc == 1 ? set_error(kErrShape, "decode window: the persistent grid does not fit (T=%d K=%d ff=%d)", T, K, ff)
                    : rc;
 }
