@@ -229,8 +229,12 @@ int frt_moe_layer_forward(const frt_moe_layer* L, const float* x, int T, const f
  *       by XCD (router logits relayed into each XCD's L2, each XCD a share of the experts' ff rows,
  *       XCD partials summed last) where the shape fits; outputs within the layer bar of the default
  *       kernel's, not bit-equal to them.
+ *   "decode_window_persistent" (default 1): decode windows of 2-4 tokens run as one persistent launch
+ *       (routing, gate/up and down joined inside the kernel) where the shape fits; 0 selects the
+ *       four-launch window path. Both give identical results.
  *   "decode_stamps" (default 0): a device buffer of 64 x 12 x 1024 uint64 that the XCD-split kernel
- *       fills with per-layer phase times (100 MHz ticks; measurement only), or 0 for none.
+ *       fills with per-layer phase times, and the persistent window kernel with its 10 phase times
+ *       per workgroup (100 MHz ticks; measurement only), or 0 for none.
  *   "decode_grid" (default 0): workgroups of a persistent single-token call, at most one per CU (0:
  *       one per CU).
  *   "sync_ticks" (default 20000000): bound of a persistent call's waits for other workgroups, in
