@@ -85,6 +85,7 @@ struct DecwLds {
     int cand_id[MT][128];
     int32_t ids[MT][32];
     float w[MT][32];
+    int rk[MT][32];           // rank of selection k by expert id
     uint32_t mask[1025];      // per expert (and E: the shared one), the tokens that chose it
     int ent_of[1025][2];      // per expert, its entries (tokens 0-3 and 4-7 of its list)
     int wtot[2][2];
@@ -209,10 +210,12 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
         router_dot(s, w2, a.bias && s < E ? a.bias[s] : 0.0f);
     }
     FRT_DW_STAMP(2);
-    {   // Q8_0 of the T inputs (u = x r with the norm): a lane pair per 32-block, 16 values a lane;
-        // T n / 32 is a multiple of 32, so every lane of a wave runs the same number of rounds
+    if (wave >= kNWW / 2) {   // Q8_0 of the T inputs (u = x r with the norm) by the last 4 waves (with one
+        // workgroup per CU they hold no router row below E = 4 G), while the first 4 compute theirs: a
+        // lane pair per 32-block, 16 values a lane; T n / 32 is a multiple of 32, so every lane of a
+        // wave runs the same number of rounds
         const int h = lane & 1, nblk = T * (n / kQ8);
-        for (int p0 = tid >> 1; p0 < nblk; p0 += kNTW / 2) {
+        for (int p0 = (tid - kNTW / 2) >> 1; p0 < nblk; p0 += kNTW / 4) {
             const int t = p0 / (n / kQ8), blk = p0 % (n / kQ8);
             float v[16];
             float am = 0.0f;
@@ -250,7 +253,10 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
     __syncthreads();
     if (wave < T) {   // token `wave`: ids and weights in rank order
         const int id = topk_wave_fast<V>(s_lg[wave], E, K, S.ids[wave], S.w[wave], S.cand_v[wave], S.cand_id[wave]);
+        int rk = 0;   // the selection's rank by expert id among the token's (the ids are distinct)
+        for (int k2 = 0; k2 < K; ++k2) rk += int(__builtin_amdgcn_readlane(id, k2) < id);
         if (lane < K) {
+            S.rk[wave][lane] = rk;
             atomicOr(&S.mask[id], 1u << wave);
             if (b == 0) {   // the routing records, once
                 if (a.ids) a.ids[wave * K + lane] = id;
@@ -299,9 +305,8 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
         d.slot[sl] = ik;
         d.w[sl] = 1.0f;
         const int c = d.base + sl;
-        if (ik < K) {   // rank of the item among the token's routed experts by id (the ids are distinct)
-            int rk = 0;
-            for (int k2 = 0; k2 < K; ++k2) rk += int(S.ids[it][k2] < key);
+        if (ik < K) {
+            const int rk = S.rk[it][ik];
             S.comb_c[it][rk] = c;
             S.comb_w[it][rk] = S.w[it][ik];
         } else {
