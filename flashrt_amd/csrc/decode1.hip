@@ -397,9 +397,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
         }
     };
 
-    constexpr int BATCH = 2;   // entries per wave in the first (prefetched) batch: 16 entries
     const bool has_down = r0 < n;
-    DownRegs<NBF, BATCH> D;
     if (b < NU) gu_load(b);
     // the routing weights while the rows load (rank order: w = e / sum e, e = exp(l - l_0), the
     // sum in rank order; the shared expert's: sigmoid(gate)), then each entry's
@@ -435,9 +433,13 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
     float* sh_y = sh_d + size_t(U) * (ff / kQ8);
     // warm this XCD's L2 with the next layer's router rows this workgroup will read (issued ahead of
     // the wait, which they would otherwise only delay at the kernel's end)
-    // the down rows of this workgroup's 8 output rows for every entry (the first 16 entries), issued
-    // once the gate/up rows no longer compete with them; they land during the wait below
-    if (has_down) down_load<NBF, BATCH, kNW1, true>(R.ent, U, wave, r0, n, ff, D);
+    // the down rows of this workgroup's 8 output rows for every entry (the first 12 entries), issued
+    // once the gate/up rows no longer compete with them; they land during the wait below. Loaded
+    // by waves 0-3 (entries wave + 4 i); waves 4-7 poll the h words meanwhile. A wave's waits count its
+    // loads in issue order, so a poller that had issued down rows would wait behind them (measured on
+    // the stack: all waves loading and polling 722-733 us per token, split 705-714)
+    DownRegs<NBF, 3> D3;
+    if (has_down && wave < 4) down_load<NBF, 3, 4, true>(R.ent, U, wave, r0, n, ff, D3);
     // warm this XCD's L2 with the router rows this workgroup reads next: the next layer's (a stack),
     // else the next call's
     const float* warm_w = l + 1 < n_layer ? a.lay[l + 1].W : a.next_w;
@@ -448,11 +450,22 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
 #pragma unroll
         for (int i = 0; i < L / 4; ++i) nv[i] = w4[i];
     }
-    wait_words<kMaxHWords / kNT1, kHbStride>(a.hb, NU * 9, tag, deadline, &a.sync->err, err_val, a.host_err, [&](int i, uint32_t p) {
-        const int q = i / 9, part = i % 9, u = q / RB, rb = q % RB;
-        if (part < 8) *reinterpret_cast<uint32_t*>(sh_q + size_t(u) * ff + rb * 32 + 4 * part) = p;
-        else sh_d[u * (ff / kQ8) + rb] = __uint_as_float(p);
-    });
+    {   // the first kHPoll words by waves 4-7, any beyond by waves 0-3 (shapes with many h blocks)
+        constexpr int kHPoll = 8 * (kNT1 / 2);
+        auto put_h = [&](int i, uint32_t p) {
+            const int q = i / 9, part = i % 9, u = q / RB, rb = q % RB;
+            if (part < 8) *reinterpret_cast<uint32_t*>(sh_q + size_t(u) * ff + rb * 32 + 4 * part) = p;
+            else sh_d[u * (ff / kQ8) + rb] = __uint_as_float(p);
+        };
+        const int nh = NU * 9;
+        if (wave >= kNW1 / 2)
+            wait_words_at<8, kNT1 / 2>([&](int i) { return a.hb + size_t(i) * kHbStride; }, min(nh, kHPoll), tag, deadline,
+                                       &a.sync->err, err_val, a.host_err, put_h, kNT1 / 2);
+        else if (nh > kHPoll)
+            wait_words_at<8, kNT1 / 2>([&](int i) { return a.hb + size_t(kHPoll + i) * kHbStride; }, nh - kHPoll, tag,
+                                       deadline, &a.sync->err, err_val, a.host_err,
+                                       [&](int i, uint32_t p) { put_h(kHPoll + i, p); }, 0);
+    }
     __syncthreads();
     // combine of rows g0 .. g0 + 7 (threads 0..7): the routed entries in ascending expert id from 0,
     // then the shared expert, then the residual (k_dec_down's single-token order)
@@ -474,11 +487,13 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
         }
     };
     if (has_down) {
-        down_compute<NBF, BATCH, kNW1>(R.ent, U, wave, D, sh_q, sh_d, sh_y, ff);
-        for (int u0 = wave + kNW1 * BATCH; u0 < U; u0 += kNW1 * BATCH) {
-            DownRegs<NBF, BATCH> D2;
-            down_load<NBF, BATCH, kNW1, true>(R.ent, U, u0, r0, n, ff, D2);
-            down_compute<NBF, BATCH, kNW1>(R.ent, U, u0, D2, sh_q, sh_d, sh_y, ff);
+        if (wave < 4) {
+            down_compute<NBF, 3, 4>(R.ent, U, wave, D3, sh_q, sh_d, sh_y, ff);
+            for (int u0 = wave + 12; u0 < U; u0 += 12) {
+                DownRegs<NBF, 3> D2;
+                down_load<NBF, 3, 4, true>(R.ent, U, u0, r0, n, ff, D2);
+                down_compute<NBF, 3, 4>(R.ent, U, u0, D2, sh_q, sh_d, sh_y, ff);
+            }
         }
         __syncthreads();
         combine(r0, res);
@@ -486,10 +501,11 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
     for (int g0 = r0 + 8 * G; g0 < n; g0 += 8 * G) {   // more 8-row groups than workgroups
         const float rv = (!stack && a.resid) ? a.resid[g0 + (tid & 7)] : 0.0f;
         __syncthreads();   // sh_y of the previous group is combined
-        for (int u0 = wave; u0 < U; u0 += kNW1 * BATCH) {
-            DownRegs<NBF, BATCH> D2;
-            down_load<NBF, BATCH, kNW1, true>(R.ent, U, u0, g0, n, ff, D2);
-            down_compute<NBF, BATCH, kNW1>(R.ent, U, u0, D2, sh_q, sh_d, sh_y, ff);
+        constexpr int MB = 2;   // entries per wave and batch (all waves: h is in LDS by now)
+        for (int u0 = wave; u0 < U; u0 += kNW1 * MB) {
+            DownRegs<NBF, MB> D2;
+            down_load<NBF, MB, kNW1, true>(R.ent, U, u0, g0, n, ff, D2);
+            down_compute<NBF, MB, kNW1>(R.ent, U, u0, D2, sh_q, sh_d, sh_y, ff);
         }
         __syncthreads();
         combine(g0, rv);

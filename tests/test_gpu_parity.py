@@ -6,6 +6,7 @@ Bars: ids and the dispatch permutation bit-exact; routing weights <= 1e-6 relati
 from __future__ import annotations
 
 import os
+import zlib
 
 import numpy as np
 import pytest
@@ -1069,7 +1070,7 @@ def test_decode_fused_matches_three_kernel(F, case):
     oracle, over shapes: config 0; a config 2 layer (RMS norm, Zipf bias, residual); E = 128 and 1000
     (one and two wave-halves of logits per lane); the reference tests' 2560 / 640; n = 1024 with
     ff = 1024 (more h blocks than workgroups); K = 32 (33 entries, a second down batch)."""
-    rng = np.random.default_rng(hash(case) % 1000)
+    rng = np.random.default_rng(zlib.crc32(case.encode()) % 1000)
     kw = {}
     resid = None
     if case == "stack":
@@ -1279,7 +1280,7 @@ def test_decode_xcd_layer_matches_oracle(F, case):
     split), K = 4 (no owned entry: every entry split over the XCDs), K = 7 (one owned entry per XCD, none
     split); n = 3072. Repeated calls
     on one workspace give the same bits, and no wait runs out of time."""
-    rng = np.random.default_rng(abs(hash(case)) % 1000 + 5)
+    rng = np.random.default_rng(zlib.crc32(case.encode()) % 1000 + 5)
     kw = dict(cfg=0)
     resid = None
     if case == "stack":
