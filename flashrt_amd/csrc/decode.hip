@@ -263,9 +263,10 @@ __device__ __forceinline__ void gateup_body(const DecEntry& e, int rb, const int
                             int n, int ff, int8_t* __restrict__ hq, float* __restrict__ hd, float (*hrow)[32],
                             const uint8_t* warm = nullptr, const DecAct<MT>* pre = nullptr,
                             AfterLoads after_loads = {}) {
-    constexpr int RPW = (64 % NB == 0) ? 64 / NB : 1;
+    constexpr int RPW = gu_rpw<NB>();
     constexpr int ROWS = 32 / NW;                       // rows per wave
-    constexpr int PASSES = (ROWS + RPW - 1) / RPW;
+    constexpr int PASSES = gu_passes<NB, NW>();
+    __shared__ __align__(16) float seqbuf[NW][MT * 128];   // per wave: the block terms of seq_row_sums
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rsub = lane / NB, b = lane % NB;
     const bool live = rsub < RPW;
@@ -365,23 +366,12 @@ __device__ __forceinline__ void gateup_body(const DecEntry& e, int rb, const int
             ag[j] = fg * dg;
             au[j] = fu * du;
         }
-        // sum over the row's NB lanes (DPP pairwise tree); the total lands in the group's last lane
-#pragma unroll
-        for (int j = 0; j < MT; ++j) {
-            if (j >= e.ntok) continue;
-            float a = ag[j], c = au[j];
-            bool writer;
-            if (RPW > 1) {
-                a = group_sum<NB>(a);
-                c = group_sum<NB>(c);
-                writer = live && b == NB - 1;
-            } else {
-                a = wave_sum_tree(a);
-                c = wave_sum_tree(c);
-                writer = lane == 0;
-            }
-            if (writer && p * RPW + rsub < ROWS) hrow[j][wave * ROWS + p * RPW + rsub] = a / (1.0f + expf(-a)) * c;
-        }
+        // the rows' sums over their NB lanes in the CPU path's order: lane 2 RPW j + r holds token j's
+        // row p RPW + r
+        const float2 gu = seq_row_sums<NB, RPW, MT>(ag, au, seqbuf[wave], lane);
+        const int j = lane / (2 * RPW), r = lane % (2 * RPW);
+        if (j < e.ntok && r < RPW && p * RPW + r < ROWS)
+            hrow[j][wave * ROWS + p * RPW + r] = gu.x / (1.0f + expf(-gu.x)) * gu.y;
     }
     __syncthreads();
     // Q8_0 of the 32-row block of h for each token: wave w < ntok, lanes 0..31
@@ -728,14 +718,15 @@ __global__ void __launch_bounds__(256) k_hits_down(const DecEntry* __restrict__ 
 // ---- moe_hits at any shape of the reference's envelope (n a multiple of 512, ff a multiple of 64 up
 // to 4096; arch/qwen4exp/moe_fast.cu:557): the same products with the row length a runtime value. Each
 // lane walks the 64-blocks lane, lane + 64, ... of a row; the activation blocks are read from the
-// global Q8_0 input (L1 / L2 hits after the first row). Float order: each lane's blocks in order, then
-// the wave's pairwise tree (the shapes of the templated kernels keep those kernels).
+// global Q8_0 input (L1 / L2 hits after the first row). Float order: the block terms are added one
+// after another, blocks ascending (the shapes of the templated kernels keep those kernels).
 // Gate / up: workgroup (rb, u) takes ff rows 32 rb .. 32 rb + 31 of entry u, 8 rows per wave; SwiGLU
 // and Q8_0 of the 32-row h block per token, as gateup_body.
 __global__ void __launch_bounds__(256) k_gen_gateup(const DecEntry* __restrict__ ent, const int32_t* __restrict__ n_ent,
                                                     const int8_t* __restrict__ xq, const float* __restrict__ xd, int n,
                                                     int ff, int8_t* __restrict__ hq, float* __restrict__ hd) {
     __shared__ float hrow[kDecMaxT][32];
+    __shared__ float terms[4][2 * kDecMaxT][kGenMaxN / kBlock];   // per wave: a row's block terms by token
     if (int(blockIdx.y) >= *n_ent) return;
     const DecEntry e = ent[blockIdx.y];
     const int rb = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -747,9 +738,6 @@ __global__ void __launch_bounds__(256) k_gen_gateup(const DecEntry* __restrict__
     const uint16_t* uscal = reinterpret_cast<const uint16_t*>(e.blob + mb + size_t(ff) * nb * 16);
     for (int i = 0; i < 8; ++i) {
         const int r = rb * 32 + wave * 8 + i;
-        float ag[kDecMaxT], au[kDecMaxT];
-#pragma unroll
-        for (int j = 0; j < kDecMaxT; ++j) ag[j] = au[j] = 0.0f;
         for (int b = lane; b < nb; b += 64) {
             const uint4 cg = gld_u4(gcodes + (size_t(r) * nb + b) * 16);
             const uint4 cu = gld_u4(ucodes + (size_t(r) * nb + b) * 16);
@@ -789,16 +777,19 @@ __global__ void __launch_bounds__(256) k_gen_gateup(const DecEntry* __restrict__
                 const float xd0 = xd[size_t(t) * (n / kQ8) + 2 * b], xd1 = xd[size_t(t) * (n / kQ8) + 2 * b + 1];
                 const float fg = float(g0 - s0) * xd0 + float(g1 - s1) * xd1;
                 const float fu = float(u0 - s0) * xd0 + float(u1 - s1) * xd1;
-                ag[j] = ag[j] + fg * dg;
-                au[j] = au[j] + fu * du;
+                terms[wave][2 * j][b] = fg * dg;
+                terms[wave][2 * j + 1][b] = fu * du;
             }
         }
-#pragma unroll
-        for (int j = 0; j < kDecMaxT; ++j) {
-            if (j >= e.ntok) break;
-            const float a = wave_sum_tree(ag[j]), c = wave_sum_tree(au[j]);
-            if (lane == 0) hrow[j][wave * 8 + i] = a / (1.0f + expf(-a)) * c;
-        }
+        // the row's sums in the CPU path's order (matvec_ref: blocks ascending from 0): lane 2 j adds
+        // token j's gate terms, lane 2 j + 1 its up terms
+        __builtin_amdgcn_wave_barrier();   // the wave's LDS operations complete in order
+        float sum = 0.0f;
+        if (lane < 2 * e.ntok)
+            for (int b = 0; b < nb; ++b) sum = sum + terms[wave][lane][b];
+        __builtin_amdgcn_wave_barrier();
+        const float up = __shfl(sum, min(lane + 1, 63));
+        if (lane < 2 * e.ntok && (lane & 1) == 0) hrow[lane >> 1][wave * 8 + i] = sum / (1.0f + expf(-sum)) * up;
     }
     __syncthreads();
     if (wave < e.ntok) {   // Q8_0 of the 32-row block of h for token slot `wave`

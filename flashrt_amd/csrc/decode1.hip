@@ -89,10 +89,12 @@ struct Dec1Args {
 typedef const __attribute__((address_space(4))) Dec1Args KArgs;
 typedef const __attribute__((address_space(4))) Dec1Layer KLayer;
 
+template <int PASSES>
 struct Dec1Lds {
     WinLds R;
     float s_h[32];
     Route8Lds q8;
+    __align__(16) float seq[kNW1][PASSES * 128];   // per wave: the gate/up block terms of seq_row_sums
 };
 
 template <int NB, int V, int NBF, bool STACK>
@@ -107,7 +109,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
     __shared__ __align__(16) int8_t xq[n];
     __shared__ float xd[n / kQ8];
     __shared__ __align__(16) float s_lg[64 * V + 4];
-    __shared__ Dec1Lds S;
+    __shared__ Dec1Lds<gu_passes<NB, kNW1>()> S;
     WinLds& R = S.R;
 
     const int b = blockIdx.x, G = gridDim.x;
@@ -303,9 +305,9 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
     }
 
     // gate/up unit q = b + i G: entry q / RB, ff rows 32 (q % RB) .. + 31; 32 / kNW1 rows per wave
-    constexpr int RPW = (64 % NB == 0) ? 64 / NB : 1;   // rows per wave pass
+    constexpr int RPW = gu_rpw<NB>();   // rows per wave pass
     constexpr int ROWS = 32 / kNW1;
-    constexpr int PASSES = (ROWS + RPW - 1) / RPW;
+    constexpr int PASSES = gu_passes<NB, kNW1>();
     const int rsub = lane / NB, bk = lane % NB;
     const bool live = rsub < RPW;
     const int bl = live ? bk : 0;
@@ -349,6 +351,7 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
         for (int i = 0; i < 8; ++i) xs0 = dot4(xa[i], 0x01010101, xs0);
 #pragma unroll
         for (int i = 8; i < 16; ++i) xs1 = dot4(xa[i], 0x01010101, xs1);
+        float tg[PASSES], tu[PASSES];
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const uint32_t wg[4] = {cg[p].x, cg[p].y, cg[p].z, cg[p].w};
@@ -369,18 +372,15 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
             }
             const float fg = float(g0 - xs0) * xd0 + float(g1 - xs1) * xd1;
             const float fu = float(u0 - xs0) * xd0 + float(u1 - xs1) * xd1;
-            float ag = fg * dg, au = fu * du;
-            bool writer;
-            if (RPW > 1) {
-                ag = group_sum<NB>(ag);
-                au = group_sum<NB>(au);
-                writer = live && bk == NB - 1;
-            } else {
-                ag = wave_sum_tree(ag);
-                au = wave_sum_tree(au);
-                writer = lane == 0;
-            }
-            if (writer && p * RPW + rsub < ROWS) S.s_h[wave * ROWS + p * RPW + rsub] = ag / (1.0f + expf(-ag)) * au;
+            tg[p] = fg * dg;
+            tu[p] = fu * du;
+        }
+        // the rows' sums over their NB lanes in the CPU path's order, all passes at once: lane
+        // 2 RPW p + r holds row p RPW + r
+        const float2 gu = seq_row_sums<NB, RPW, PASSES>(tg, tu, S.seq[wave], lane);
+        {
+            const int p = lane / (2 * RPW), r = lane % (2 * RPW), row = p * RPW + r;
+            if (r < RPW && p < PASSES && row < ROWS) S.s_h[wave * ROWS + row] = gu.x / (1.0f + expf(-gu.x)) * gu.y;
         }
         __syncthreads();
         if (wave == 0) {   // Q8_0 of the 32-row h block, published as 8 words of 4 codes and the scale

@@ -409,9 +409,10 @@ __global__ void __launch_bounds__(kNT2) k_dec2(Dec2Args a_byval) {
     }
 
     // ---- gate/up of this workgroup's pairs p0 .. p1 - 1, RPW rows per wave pass, 2 passes per batch
-    constexpr int RPW = (64 % NB == 0) ? 64 / NB : 1;
+    constexpr int RPW = gu_rpw<NB>();
     constexpr int SLOTS = kNW2 * RPW;
     constexpr int PB = 2;
+    __shared__ __align__(16) float seqbuf[kNW2][PB * 128];   // per wave: the block terms of seq_row_sums
     const int rsub = lane / NB, bk = lane % NB;
     const bool live = rsub < RPW;
     const int bl = live ? bk : 0;
@@ -457,6 +458,7 @@ __global__ void __launch_bounds__(kNT2) k_dec2(Dec2Args a_byval) {
         for (int i = 0; i < 8; ++i) xs0 = dot4(xa[i], 0x01010101, xs0);
 #pragma unroll
         for (int i = 8; i < 16; ++i) xs1 = dot4(xa[i], 0x01010101, xs1);
+        float tg[PB], tu[PB];
 #pragma unroll
         for (int k = 0; k < PB; ++k) {
             const uint32_t wg[4] = {cg[k].x, cg[k].y, cg[k].z, cg[k].w};
@@ -477,20 +479,14 @@ __global__ void __launch_bounds__(kNT2) k_dec2(Dec2Args a_byval) {
             }
             const float fg = float(g0 - xs0) * xd0 + float(g1 - xs1) * xd1;
             const float fu = float(u0 - xs0) * xd0 + float(u1 - xs1) * xd1;
-            float ag = fg * dg, au = fu * du;
-            bool writer;
-            if (RPW > 1) {
-                ag = group_sum<NB>(ag);
-                au = group_sum<NB>(au);
-                writer = live && bk == NB - 1;
-            } else {
-                ag = wave_sum_tree(ag);
-                au = wave_sum_tree(au);
-                writer = lane == 0;
-            }
-            const int p = pb + k * SLOTS + slot;
-            if (writer && p < p1) h_f[p] = ag / (1.0f + expf(-ag)) * au;   // published below by one wave
+            tg[k] = fg * dg;
+            tu[k] = fu * du;
         }
+        // the rows' sums in the CPU path's order: lane 2 RPW k + r holds pair pb + k SLOTS + wave RPW + r
+        const float2 gu = seq_row_sums<NB, RPW, PB>(tg, tu, seqbuf[wave], lane);
+        const int k = lane / (2 * RPW), r = lane % (2 * RPW);
+        const int p = pb + k * SLOTS + wave * RPW + r;
+        if (r < RPW && k < PB && p < p1) h_f[p] = gu.x / (1.0f + expf(-gu.x)) * gu.y;   // published below by one wave
     };
 
     // ---- down: this workgroup's rows r0 .. r0 + RW - 1 over the XCD's part of ff. Owned entries: one

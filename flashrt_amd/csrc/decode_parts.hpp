@@ -26,6 +26,47 @@ namespace {
 
 __device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + expf(-g)); }
 
+// ---- gate/up row sums in the CPU path's float order. matvec_ref (quant/q2_0/q2_0.cpp:119-140) adds a
+// row's per-block terms p_b = d_w * (d_a0 s0 + d_a1 s1) one after another from 0, blocks ascending;
+// h is then quantized, so a sum off by an ulp can move h across a Q8 code boundary (a pairwise tree
+// did on about 3-5% of tokens, up to 2.5e-3 relative in the layer output). Here lane r NB + b
+// (r < RPW) holds block b of row r, for M row sets (tokens, or passes over the rows): the gate term
+// g[m] and the up term u[m]. Every lane stores its terms in the wave's LDS area buf (M * 128 floats,
+// 16-byte aligned); lane c = 2 RPW m + r adds row r's gate terms of set m, lane c + RPW its up terms,
+// one after another. Returns (gate sum, up sum) in lane 2 RPW m + r, for m < M and r < RPW (other
+// lanes: unspecified). Call with the whole wave active; 2 RPW M <= 64.
+// gate/up rows of a 32-row unit over NW waves: 32 / NW rows per wave, RPW = 64 / NB rows per pass (one
+// when NB does not divide 64), gu_passes passes
+template <int NB> constexpr int gu_rpw() { return (64 % NB == 0) ? 64 / NB : 1; }
+template <int NB, int NW> constexpr int gu_passes() { return (32 / NW + gu_rpw<NB>() - 1) / gu_rpw<NB>(); }
+
+template <int NB, int RPW, int M>
+__device__ __forceinline__ float2 seq_row_sums(const float (&g)[M], const float (&u)[M], float* buf, int lane) {
+    static_assert(2 * RPW * M <= 64 && NB % 4 == 0 && RPW * NB <= 64, "seq_row_sums shape");
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        buf[(2 * m) * 64 + lane] = g[m];
+        buf[(2 * m + 1) * 64 + lane] = u[m];
+    }
+    __builtin_amdgcn_wave_barrier();   // the wave's LDS operations complete in order
+    const int m = lane / (2 * RPW), rem = lane % (2 * RPW), gu = rem / RPW, r = rem % RPW;
+    float s = 0.0f;
+    if (m < M) {
+        const float4* q = reinterpret_cast<const float4*>(buf + (2 * m + gu) * 64 + r * NB);
+#pragma unroll
+        for (int i = 0; i < NB / 4; ++i) {
+            const float4 v = q[i];
+            s = s + v.x;
+            s = s + v.y;
+            s = s + v.z;
+            s = s + v.w;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float su = __shfl(s, min(lane + RPW, 63));
+    return make_float2(s, su);
+}
+
 // ---- the window's routing and its entry list, built in LDS by one 1024-thread workgroup: the 4
 // waves of group g route token g together (topk_group4); then wave 0, one lane per selection,
 // orders the distinct experts ascending (first occurrences ranked by id), the shared expert last,

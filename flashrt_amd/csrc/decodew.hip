@@ -79,7 +79,7 @@ constexpr int kWPhases = 10;
 
 typedef const __attribute__((address_space(4))) DecwArgs KWArgs;
 
-template <int MT>
+template <int MT, int PASSES>
 struct DecwLds {
     float cand_v[MT][128];
     int cand_id[MT][128];
@@ -94,6 +94,7 @@ struct DecwLds {
     float s_h[kDecMaxT][32];
     DecEntry ent[128];        // at most T (K + 1) <= 128 items
     int n_ent;
+    __align__(16) float seq[kNWW][PASSES * 128];   // per wave: the gate/up block terms of seq_row_sums
 };
 
 // MT: the largest window of the instance (4, or 8 where the LDS allows)
@@ -110,7 +111,7 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
     __shared__ __align__(16) int8_t xq[MT][n];
     __shared__ float xd[MT][n / kQ8];
     __shared__ __align__(16) float s_lg[MT][64 * V + 4];
-    __shared__ DecwLds<MT> S;
+    __shared__ DecwLds<MT, gu_passes<NB, kNWW>()> S;
     __shared__ uint32_t s_ep[kNWW];
     __shared__ float s_r[MT];
     __shared__ uint64_t s_stamp[kWPhases];   // (kept in LDS, written out at the end)
@@ -319,9 +320,9 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
     FRT_DW_STAMP(5);
 
     // gate/up unit q: entry q / RB, ff rows 32 (q % RB) .. + 31, 32 / kNWW rows per wave
-    constexpr int RPW = (64 % NB == 0) ? 64 / NB : 1;   // rows per wave pass
+    constexpr int RPW = gu_rpw<NB>();   // rows per wave pass
     constexpr int ROWS = 32 / kNWW;
-    constexpr int PASSES = (ROWS + RPW - 1) / RPW;
+    constexpr int PASSES = gu_passes<NB, kNWW>();
     const int rsub = lane / NB, bk = lane % NB;
     const bool rlive = rsub < RPW;
     const int bl = rlive ? bk : 0;
@@ -372,6 +373,7 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
             for (int i = 0; i < 8; ++i) xs0 = dot4(xa[i], 0x01010101, xs0);
 #pragma unroll
             for (int i = 8; i < 16; ++i) xs1 = dot4(xa[i], 0x01010101, xs1);
+            float tg[PASSES], tu[PASSES];
 #pragma unroll
             for (int p = 0; p < PASSES; ++p) {
                 const uint32_t wg[4] = {g.cg[p].x, g.cg[p].y, g.cg[p].z, g.cg[p].w};
@@ -392,19 +394,13 @@ __global__ void __launch_bounds__(kNTW) k_decw(DecwArgs a_byval) {
                 }
                 const float fg = float(g0 - xs0) * xd0 + float(g1 - xs1) * xd1;
                 const float fu = float(u0 - xs0) * xd0 + float(u1 - xs1) * xd1;
-                float ag = fg * dg, au = fu * du;
-                bool writer;
-                if (RPW > 1) {
-                    ag = group_sum<NB>(ag);
-                    au = group_sum<NB>(au);
-                    writer = rlive && bk == NB - 1;
-                } else {
-                    ag = wave_sum_tree(ag);
-                    au = wave_sum_tree(au);
-                    writer = lane == 0;
-                }
-                if (writer && p * RPW + rsub < ROWS) S.s_h[jt][wave * ROWS + p * RPW + rsub] = ag / (1.0f + expf(-ag)) * au;
+                tg[p] = fg * dg;
+                tu[p] = fu * du;
             }
+            // the rows' sums in the CPU path's order (lane 2 RPW p + r: row p RPW + r)
+            const float2 gu = seq_row_sums<NB, RPW, PASSES>(tg, tu, S.seq[wave], lane);
+            const int p = lane / (2 * RPW), r = lane % (2 * RPW), row = p * RPW + r;
+            if (r < RPW && p < PASSES && row < ROWS) S.s_h[jt][wave * ROWS + row] = gu.x / (1.0f + expf(-gu.x)) * gu.y;
         }
         __syncthreads();
         if (wave < ntok) {   // Q8_0 of token `wave`'s 32-row h block, published as 8 words of 4 codes and the scale
