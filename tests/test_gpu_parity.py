@@ -358,6 +358,34 @@ def test_layer_window_persistent(F, T):
     assert np.array_equal(counts.cpu().numpy(), np.bincount(ids.reshape(-1), minlength=H.E))
 
 
+@pytest.mark.parametrize("path", ["T1", "T1_xcd", "T3", "T3_four_launch", "T6"])
+def test_decode_h_in_cpu_order(F, path):
+    """The decode paths sum each gate/up row's block terms in the CPU path's order (matvec_ref), so h
+    takes the CPU's Q8 codes and the layer output differs from the oracle only by the order of the down
+    and combine sums (~1e-7 relative). A pairwise tree moved h codes across Q8 boundaries on 2.6% of
+    1000 single tokens (K = 4; 5.3% at K = 10), up to 2.5e-3 relative; in order, 1000 seeds gave at most
+    1.9e-5. Here: 40 seeded windows per path, K = 4 (fewest experts, largest weight per flipped code),
+    every token within 1e-4 of the oracle, ids bit-exact."""
+    T = int(path.split("_")[0][1:])
+    opts = {"T1_xcd": {"decode_xcd": 1}, "T3_four_launch": {"decode_window_persistent": 0}}.get(path, {})
+    w = H.World(cfg=0, K=4)
+    worst = 0.0
+    try:
+        for k, v in opts.items():
+            F.set_option(k, v)
+        for seed in range(40):
+            x = np.random.default_rng(1000 + seed).standard_normal((T, w.n)).astype(np.float32)
+            out, ids, wts = w.gpu_forward(x)
+            ref, rid, rw, _ = w.oracle_forward(x)
+            assert np.array_equal(ids, rid), seed
+            worst = max(worst, H.out_rel(out, ref))
+    finally:
+        for k in opts:
+            F.set_option(k, 1 if k == "decode_window_persistent" else 0)
+    print(f"{path}: worst out rel err over 40 windows {worst:.2e}")
+    assert worst <= 1e-4
+
+
 @pytest.mark.parametrize("T", [5, 8])
 def test_layer_verify_window(F, T):
     """Verify windows of 5 and 8 tokens (the reference's kMaxWindow = 8, moe_fast.cu:38; correlated
