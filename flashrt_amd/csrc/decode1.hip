@@ -9,11 +9,12 @@
 //      quantizes the experts' input (Q8_0 per 32) into its own LDS.
 //   2. routing + gate/up: every workgroup waits for all E + 1 logits (the shared gate last), routes
 //      the token itself (route1_wave), issues the gate/up rows of its unit (entry x 32 ff rows) and,
-//      behind them, the down rows of its 8 output rows for every entry (those land while the gate/up
-//      work and the wait below run); SwiGLU and Q8_0 of the 32-row h block, published.
-//   3. down: every workgroup waits for all h blocks, finishes its down rows and the combine, the
-//      same float order as k_dec_down's single-token combine (outputs equal the three-kernel path's
-//      bit for bit).
+//      behind them (waves 0-3), the down rows of its 8 output rows for every entry (those land while
+//      the gate/up work and the wait below run); each row's block terms are added in the CPU path's
+//      order (seq_row_sums); SwiGLU and Q8_0 of the 32-row h block, published.
+//   3. down: every workgroup waits for all h blocks (polled by waves 4-7, whose waits do not queue
+//      behind down-row loads), finishes its down rows and the combine, the same float order as
+//      k_dec_down's single-token combine (outputs equal the three-kernel path's bit for bit).
 //
 // Joins: epoch-tagged 8-byte words, (tag << 32) | payload, stored and loaded at agent scope (sc1),
 // so that a reader on another XCD sees the writer's value and never a stale line of its own L2.
