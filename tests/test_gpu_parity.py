@@ -771,6 +771,28 @@ def test_layer_prefill_config3(F):
     assert np.isfinite(out).all()
 
 
+def test_layer_prefill_config3_all_rows(F):
+    """Config 3 (the bench's prefill layer and input), every one of the 2048 token rows against the
+    oracle: ids bit-exact and each row within the output bar. The prefill path sums gate/up on the
+    matrix cores and carries h and the per-slot outputs in fp16, so rows sit near 3e-4 (median) with a
+    tail from h codes that the sum order moves: measured median 3.0e-4, 99th percentile 5.8e-4,
+    worst 1.81e-3. Guards: median <= 5e-4, 99th percentile <= 1e-3, every row <= 2e-3."""
+    T = 2048
+    bias = O.gen_zipf_bias(3, 0, H.E, H.ZIPF_S_PREFILL, H.PREFILL_ALPHA)
+    w3 = H.World(cfg=3, bias=bias)
+    xt = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    F.gen.normal(xt, 3, 0, O.X_TENSOR, 1.0, round_bf16=True)
+    x = xt.cpu().numpy()
+    out, ids, wts = w3.gpu_forward(x)
+    ref, rid, rw, _ = w3.oracle_forward(x, threads=16)
+    assert np.array_equal(ids, rid)
+    g, r = out.astype(np.float64), ref.astype(np.float64)
+    e = np.abs(g - r).max(axis=1) / np.abs(r).max(axis=1)
+    print(f"configs[3] all rows: median {np.median(e):.2e}, p99 {np.quantile(e, 0.99):.2e}, max {e.max():.2e}")
+    assert np.median(e) <= 5e-4 and np.quantile(e, 0.99) <= 1e-3
+    assert e.max() <= H.OUT_REL
+
+
 def test_layer_prefill_repeatable(F):
     """The prefill kernels sum without atomics, so one input gives the same bits on every call: 8
     calls of the config 3 layer agree exactly on all 2048 tokens (a load that an LDS ring reads
