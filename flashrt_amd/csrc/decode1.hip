@@ -489,11 +489,11 @@ __global__ void __launch_bounds__(kNT1) k_dec1(Dec1Args a_byval) {
     };
     if (has_down) {
         if (wave < 4) {
-            down_compute<NBF, 3, 4>(R.ent, U, wave, D3, sh_q, sh_d, sh_y, ff);
+            down_compute1<NBF, 3, 4>(U, wave, D3, sh_q, sh_d, sh_y, ff);
             for (int u0 = wave + 12; u0 < U; u0 += 12) {
                 DownRegs<NBF, 3> D2;
                 down_load<NBF, 3, 4, true>(R.ent, U, u0, r0, n, ff, D2);
-                down_compute<NBF, 3, 4>(R.ent, U, u0, D2, sh_q, sh_d, sh_y, ff);
+                down_compute1<NBF, 3, 4>(U, u0, D2, sh_q, sh_d, sh_y, ff);
             }
         }
         __syncthreads();

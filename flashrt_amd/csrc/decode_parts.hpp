@@ -494,6 +494,72 @@ __device__ __forceinline__ void down_load(const DecEntry* ent, int U, int u0, in
     }
 }
 
+// down_compute for a single token (entry u's compact slot is u): the same products and sums, with the
+// BATCH entries computed side by side (no per-entry reads of the entry list, whose LDS round trips
+// would otherwise run one after another)
+template <int NBF, int BATCH, int US = 4>
+__device__ __forceinline__ void down_compute1(int U, int u0, const DownRegs<NBF, BATCH>& R, const int8_t* sh_q,
+                                              const float* sh_d, float* sh_y, int ff) {
+    using D = DownRegs<NBF, BATCH>;
+    const int lane = threadIdx.x & 63;
+    const int rsub = lane / NBF, b = lane % NBF;
+    const bool live = rsub < D::RPP;
+    float part[BATCH][D::PASSES];
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+        const int c = min(u0 + US * i, U - 1);
+        const int4* hp = reinterpret_cast<const int4*>(sh_q + size_t(c) * ff + (live ? b : 0) * kBlock);
+        int ha[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int4 v = hp[q];
+            ha[4 * q] = v.x;
+            ha[4 * q + 1] = v.y;
+            ha[4 * q + 2] = v.z;
+            ha[4 * q + 3] = v.w;
+        }
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i2 = 0; i2 < 8; ++i2) s0 = dot4(ha[i2], 0x01010101, s0);
+#pragma unroll
+        for (int i2 = 8; i2 < 16; ++i2) s1 = dot4(ha[i2], 0x01010101, s1);
+        const float d0 = sh_d[size_t(c) * (ff / kQ8) + 2 * (live ? b : 0)];
+        const float d1 = sh_d[size_t(c) * (ff / kQ8) + 2 * (live ? b : 0) + 1];
+#pragma unroll
+        for (int p = 0; p < D::PASSES; ++p) {
+            const bool ok = (R.ok >> (i * D::PASSES + p)) & 1u;
+            const uint32_t wd[4] = {ok ? R.cd[i][p].x : 0u, ok ? R.cd[i][p].y : 0u, ok ? R.cd[i][p].z : 0u,
+                                    ok ? R.cd[i][p].w : 0u};
+            const float dw = ok ? h2f(uint16_t(R.sd[i][p])) : 0.0f;
+            int q0 = 0, q1 = 0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                q0 = dot4(int(wd[w] & 0x03030303u), ha[w], q0);
+                q0 = dot4(int((wd[w] >> 2) & 0x03030303u), ha[4 + w], q0);
+                q1 = dot4(int((wd[w] >> 4) & 0x03030303u), ha[8 + w], q1);
+                q1 = dot4(int((wd[w] >> 6) & 0x03030303u), ha[12 + w], q1);
+            }
+            const float f = float(q0 - s0) * d0 + float(q1 - s1) * d1;
+            part[i][p] = (live && p * D::RPP + rsub < D::RD) ? f * dw : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i)
+#pragma unroll
+        for (int p = 0; p < D::PASSES; ++p) {
+            float v = part[i][p];
+            if ((NBF & (NBF - 1)) == 0 && NBF <= 16) {
+                v = group_sum<(NBF <= 16 ? NBF : 16)>(v);
+            } else {
+                float acc = 0.0f;
+                for (int q = 0; q < NBF; ++q) acc += __shfl(v, rsub * NBF + q, 64);
+                v = acc;
+            }
+            const int rl = p * D::RPP + rsub;
+            if (u0 + US * i < U && live && b == 0 && rl < D::RD) sh_y[(u0 + US * i) * D::RD + rl] = v;
+        }
+}
+
 // sh_q [S][ff] int8 and sh_d [S][ff/32] are the Q8_0 hidden vectors by compact slot; writes
 // sh_y[c * 8 + rl], the down row r0 + rl of slot c (pairwise tree over the row's NBF blocks)
 template <int NBF, int BATCH, int US = 4>
