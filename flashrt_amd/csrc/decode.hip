@@ -783,10 +783,14 @@ __global__ void __launch_bounds__(256) k_gen_gateup(const DecEntry* __restrict__
         }
         // the row's sums in the CPU path's order (matvec_ref: blocks ascending from 0): lane 2 j adds
         // token j's gate terms, lane 2 j + 1 its up terms
-        __builtin_amdgcn_wave_barrier();   // the wave's LDS operations complete in order
+        // the wave's LDS operations complete in order; the empty asm keeps the compiler from moving the
+    // reads of other lanes' terms above the stores
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
         float sum = 0.0f;
         if (lane < 2 * e.ntok)
             for (int b = 0; b < nb; ++b) sum = sum + terms[wave][lane][b];
+        asm volatile("" ::: "memory");   // the next row's stores stay after these reads
         __builtin_amdgcn_wave_barrier();
         const float up = __shfl(sum, min(lane + 1, 63));
         if (lane < 2 * e.ntok && (lane & 1) == 0) hrow[lane >> 1][wave * 8 + i] = sum / (1.0f + expf(-sum)) * up;

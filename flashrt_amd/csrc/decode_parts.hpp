@@ -48,7 +48,10 @@ __device__ __forceinline__ float2 seq_row_sums(const float (&g)[M], const float 
         buf[(2 * m) * 64 + lane] = g[m];
         buf[(2 * m + 1) * 64 + lane] = u[m];
     }
-    __builtin_amdgcn_wave_barrier();   // the wave's LDS operations complete in order
+    // the wave's LDS operations complete in order; the empty asm keeps the compiler from moving the
+    // reads of other lanes' terms above the stores
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
     const int m = lane / (2 * RPW), rem = lane % (2 * RPW), gu = rem / RPW, r = rem % RPW;
     float s = 0.0f;
     if (m < M) {
@@ -62,6 +65,7 @@ __device__ __forceinline__ float2 seq_row_sums(const float (&g)[M], const float 
             s = s + v.w;
         }
     }
+    asm volatile("" ::: "memory");   // the next call's stores stay after these reads
     __builtin_amdgcn_wave_barrier();
     const float su = __shfl(s, min(lane + RPW, 63));
     return make_float2(s, su);
