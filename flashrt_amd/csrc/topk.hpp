@@ -516,14 +516,19 @@ __device__ __forceinline__ void topk_group4(const float* __restrict__ l, int E, 
 }
 
 // Canonical RMS scale of one token by one wave: chains j = 64 lanes over contiguous L = n / 64
-// values (fmaf(x, x, acc) ascending from 0), the adjacent pairwise tree over the chains, then
-// r = 1 / sqrt(sum / n + 1e-6) with correctly rounded division and square root.
+// values, each chain as four contiguous quarters (fmaf(x, x, acc) ascending from 0 in each, so the
+// four run side by side) added as (q0 + q1) + (q2 + q3), the adjacent pairwise tree over the chains,
+// then r = 1 / sqrt(sum / n + 1e-6) with correctly rounded division and square root.
 // xc points at this lane's chain (stride between chain elements: 1).
 template <int L>
 __device__ __forceinline__ float rms_scale_wave(const float* xc, int n) {
-    float acc = 0.0f;
+    static_assert(L % 4 == 0, "chains of whole quarters");
+    float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int i = 0; i < L; ++i) acc = fmaf(xc[i], xc[i], acc);
+    for (int i = 0; i < L / 4; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = fmaf(xc[k * (L / 4) + i], xc[k * (L / 4) + i], q[k]);
+    float acc = (q[0] + q[1]) + (q[2] + q[3]);
     acc = wave_sum_tree(acc);
     const float ms = acc / float(n);
     return 1.0f / sqrtf(ms + 1e-6f);

@@ -284,15 +284,21 @@ float orc_dot_canon(const float* w, const float* x, int n) {
     return tree64(s);
 }
 
+// The RMS norm of the stack's input in this build's canonical order (no reference test pins one; the
+// GPU kernels share it, topk.hpp rms_scale_wave): per chain of n / 64 contiguous values, four
+// contiguous quarters each summed by fmaf from 0, (q0 + q1) + (q2 + q3), then the pairwise tree.
 void orc_rmsnorm(const float* x, int T, int n, float* u) {
     const int L = n / 64;
     for (int t = 0; t < T; ++t) {
         const float* xt = x + size_t(t) * n;
         float s[64];
-        for (int j = 0; j < 64; ++j) {
-            float acc = 0.0f;
-            for (int k = j * L; k < (j + 1) * L; ++k) acc = std::fmaf(xt[k], xt[k], acc);
-            s[j] = acc;
+        for (int j = 0; j < 64; ++j) {   // chain j in four quarters, each an fmaf chain from 0
+            float q[4];
+            for (int c = 0; c < 4; ++c) {
+                q[c] = 0.0f;
+                for (int k = j * L + c * (L / 4); k < j * L + (c + 1) * (L / 4); ++k) q[c] = std::fmaf(xt[k], xt[k], q[c]);
+            }
+            s[j] = (q[0] + q[1]) + (q[2] + q[3]);
         }
         const float ms = tree64(s) / float(n);
         const float r = 1.0f / std::sqrt(ms + 1e-6f);
