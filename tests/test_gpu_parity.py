@@ -1050,17 +1050,17 @@ def test_stack_layers_teacher_forced(F, T):
         x = out
 
 
-@pytest.mark.parametrize("T", [3, 300])
-def test_norm_input_routing(F, T):
-    """The layer with the stack's RMS norm on its input (FRT_LAYER_NORM_INPUT) off the single-token
-    path: a decode window (T = 3) and the prefill router GEMM (T = 300) route rmsnorm(x) as the
-    oracle does: ids bit-exact, each selection's probability within 1e-6 relative of the oracle's
-    softmax over its logits on rmsnorm(x), outputs within the layer bar. (The single-token path's
-    logits are compared bit for bit in test_decode_fused_router_logits_bit_exact.)"""
+@pytest.mark.parametrize("T,n", [(3, 2048), (300, 2048), (1, 2560), (3, 1024), (300, 2560)])
+def test_norm_input_routing(F, T, n):
+    """The layer with the stack's RMS norm on its input (FRT_LAYER_NORM_INPUT): the single-token
+    kernel (T = 1), a decode window (T = 3) and the prefill router GEMM (T = 300) route rmsnorm(x) as
+    the oracle does, at chains of 32, 40 and 16 values (the canonical RMS sums each chain in four
+    quarters): ids bit-exact, each selection's probability within 1e-6 relative of the oracle's
+    softmax over its logits on rmsnorm(x), outputs within the layer bar."""
     bias = O.gen_zipf_bias(2, 5, H.E, H.ZIPF_S_STACK)
-    w = H.World(cfg=2, layer=5, bias=bias, norm_input=True)
-    x = (np.random.default_rng(T).standard_normal((T, H.N)) * 3).astype(np.float32)
-    out = torch.empty((T, H.N), dtype=torch.float32, device="cuda")
+    w = H.World(cfg=2, layer=5, n=n, bias=bias, norm_input=True)
+    x = (np.random.default_rng(T + n).standard_normal((T, n)) * 3).astype(np.float32)
+    out = torch.empty((T, n), dtype=torch.float32, device="cuda")
     ids = torch.empty((T, H.K), dtype=torch.int32, device="cuda")
     wts = torch.empty((T, H.K), dtype=torch.float32, device="cuda")
     probs = torch.empty((T, H.K), dtype=torch.float32, device="cuda")
@@ -1075,6 +1075,10 @@ def test_norm_input_routing(F, T):
     want = np.take_along_axis(p, rid, axis=1)
     assert float((np.abs(probs.cpu().numpy() - want) / want).max()) <= 1e-6
     assert H.out_rel(out.cpu().numpy(), ref) <= H.OUT_REL
+    # the default call (no probabilities asked for): the persistent kernels at T = 1 and 3
+    o2, i2, _ = w.gpu_forward(x)
+    assert np.array_equal(i2, rid)
+    assert H.out_rel(o2, ref) <= H.OUT_REL
 
 
 def test_cpp_mirror_gpu():
