@@ -1110,7 +1110,7 @@ def _fused_vs_three(F, w, x, resid=None, reps=3):
             outs.append(w.gpu_forward(x, resid=resid))
     finally:
         F.set_option("decode_fused", 1)
-        F.set_option("decode_xcd", 1)
+        F.set_option("decode_xcd", 0)   # (the default)
     assert not F.layer_sync_error(ws)
     for o in outs:
         for a, b in zip(o, ref):
@@ -1118,12 +1118,13 @@ def _fused_vs_three(F, w, x, resid=None, reps=3):
     return outs[0]
 
 
-@pytest.mark.parametrize("case", ["cfg0", "stack", "E128", "E1000", "n2560", "n1024_ff1024", "K32"])
+@pytest.mark.parametrize("case", ["cfg0", "stack", "E128", "E1000", "n2560", "n1024_ff1024", "K32", "n4096"])
 def test_decode_fused_matches_three_kernel(F, case):
     """Persistent single-token layer == three-kernel path bit for bit, and within the bars of the
     oracle, over shapes: config 0; a config 2 layer (RMS norm, Zipf bias, residual); E = 128 and 1000
     (one and two wave-halves of logits per lane); the reference tests' 2560 / 640; n = 1024 with
-    ff = 1024 (more h blocks than workgroups); K = 32 (33 entries, a second down batch)."""
+    ff = 1024 (more h blocks than workgroups); K = 32 (33 entries, a second down batch); n = 4096
+    (two 8-row output groups per workgroup)."""
     rng = np.random.default_rng(zlib.crc32(case.encode()) % 1000)
     kw = {}
     resid = None
@@ -1139,6 +1140,8 @@ def test_decode_fused_matches_three_kernel(F, case):
         kw = dict(cfg=0, n=1024, ff=1024)
     elif case == "K32":
         kw = dict(cfg=0, K=32)
+    elif case == "n4096":
+        kw = dict(cfg=0, n=4096)
     else:
         kw = dict(cfg=0)
     w = H.World(**kw)
